@@ -1,0 +1,176 @@
+"""Decode benchmark: Qwen2.5-7B INT4 (W4A16, group 128, int8 lm_head),
+batch-1 greedy decode at 32K context on one MI355X.
+
+A step is one decode token: the whole recorded step graph (28 layers of
+RMSNorm+QKV+RoPE+KV-store, split-K attention over the full context, O-proj,
+RMSNorm+gate/up+SwiGLU, down-proj, then RMSNorm+lm_head+penalty and argmax),
+chained on the device.  Weights are seeded synthetic N(0, 0.02) quantized
+with the exporter's formulas; the KV cache is prefilled with seeded N(0, 1)
+values so the timed steps run at positions just below 32768.
+
+Prints one JSON line (rank 0).  Extra keys: `roofline` for the dominant
+kernel, `cpu_baseline` (host oracle, bounded sample, rank 0), `kernels`
+(per-kernel time and HBM GB/s at the same context) and `gemv_config1`.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_GBPS = 8000.0   # MI355X HBM3E
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--model", default="7B")
+    ap.add_argument("--quant", default="int4")
+    ap.add_argument("--ctx", type=int, default=32768, help="context length at the end of the timed steps")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-profile", action="store_true")
+    ap.add_argument("--cpu-threads", type=int, default=0)
+    return ap.parse_args()
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def gemv_config1(cq, np):
+    """W8A16 GEMV K=4864 N=896 (group 128), rotated over
+    128 distinct weight copies (568 MB > the 256 MB last-level cache)."""
+    rows, cols, nbuf = 896, 4864, 128
+    wbytes = rows * cols
+    sbytes = rows * (cols // 128) * 2
+    rng = np.random.default_rng(1)
+    w = rng.integers(-127, 128, (rows, cols), dtype=np.int8).view(np.uint8)
+    s = (np.abs(rng.standard_normal((rows, cols // 128))) * 1e-3).astype(np.float16)
+    bufs = []
+    for _ in range(nbuf):
+        bw = cq.DeviceBuffer.from_array(w)
+        bs = cq.DeviceBuffer.from_array(s)
+        bufs.append((bw, bs))
+    import ctypes
+    Wl = (ctypes.c_void_p * nbuf)(*[b[0].value for b in bufs])
+    Sl = (ctypes.c_void_p * nbuf)(*[b[1].value for b in bufs])
+    x = cq.DeviceBuffer.from_array(rng.standard_normal(cols).astype(np.float16))
+    y = cq.DeviceBuffer(rows * 2)
+    us = ctypes.c_double()
+    cq.check(cq.lib.cq_time_gemv(1, 128, nbuf, Wl, Sl, x.ptr, y.ptr, rows, cols, 4 * nbuf, ctypes.byref(us)))
+    alg = wbytes + sbytes + 2 * cols + 2 * rows
+    for b in bufs:
+        b[0].free()
+        b[1].free()
+    return {"shape": "M=1 K=4864 N=896 W8A16 g128", "us": round(us.value, 3), "bytes": alg,
+            "GBps": round(alg / us.value / 1e3, 1), "frac": round(alg / us.value / 1e3 / PEAK_GBPS, 4)}
+
+
+def cpu_baseline(cfg, ctx, threads):
+    """Host oracle (scalar C++ restatement) on this box's cores: a 1-layer and
+    a 2-layer model of the same shapes at `ctx`, one decode step each;
+    t_token = t1 + (L - 1) * (t2 - t1)."""
+    from oracle import oracle as orc
+    import numpy as np  # noqa: F401
+    if threads > 0:
+        orc.set_threads(threads)
+    cores = orc.lib.or_max_threads()
+    times = []
+    for nl in (1, 2):
+        c = cfg.replace(n_layers=nl)
+        m = orc.Model.synth(c, 0x5157454E, ctx)
+        m.fill_kv(ctx - 1, 77)
+        t0 = time.perf_counter()
+        m.forward(1, ctx - 1, [], mode=0)
+        times.append(time.perf_counter() - t0)
+        del m
+    t_layer = max(times[1] - times[0], 1e-9)
+    t_tok = times[0] + (cfg.n_layers - 1) * t_layer
+    return {"value": round(1.0 / t_tok, 4), "unit": "tok/s", "cores": cores, "kind": "port",
+            "sample": f"host oracle, one decode step of a 1-layer and a 2-layer Qwen2.5-{cfg.n_layers}L-shaped "
+                      f"model at ctx {ctx} (t1={times[0]:.3f}s, t2={times[1]:.3f}s), extrapolated to "
+                      f"{cfg.n_layers} layers"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
+              "the multi-GPU path is a design note, not built", file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import cuqwen_amd as cq
+
+    cfg = cq.preset(args.model, args.quant)
+    total = args.warmup + args.steps
+    pos0 = args.ctx - total
+    if pos0 < 1:
+        raise SystemExit("ctx too small for warmup + steps")
+    t0 = time.perf_counter()
+    w = cq.synth_weights(cfg, 0x5157454E)
+    st = cq.State(cfg, w)
+    st.fill_kv(pos0, 77)
+    log(f"[bench] {args.model} {args.quant}: weights + KV({pos0}) ready in {time.perf_counter() - t0:.1f}s")
+    tok = int(cq.lib.cq_synth_uniform(42, 0, 0, cfg.vocab_size))
+    # warmup (records the step graph), chained on the device
+    warm = st.decode(tok, pos0, args.warmup)
+    cq.synchronize()
+    t1 = time.perf_counter()
+    out = st.decode(int(warm[-1]), pos0 + args.warmup, args.steps)
+    cq.synchronize()
+    wall = time.perf_counter() - t1
+    dev_us = st.last_decode_us()
+    ms_per_step = wall * 1e3 / args.steps
+    value = args.steps / wall
+    log(f"[bench] {args.steps} steps at pos {pos0 + args.warmup}..{args.ctx - 1}: {ms_per_step:.4f} ms/step wall, "
+        f"{dev_us / 1e3:.4f} ms/step device, {value:.1f} tok/s; last tokens {list(out[-4:])}")
+
+    kernels, roof = None, None
+    if not args.no_profile:
+        prof = st.profile(args.ctx - 1, iters=5)
+        kernels = [{"kernel": k["kernel"], "us": round(k["us"], 3), "bytes": int(k["bytes"]),
+                    "GBps": round(k["GBps"], 1), "frac": round(k["GBps"] / PEAK_GBPS, 4)} for k in prof]
+        for k in kernels:
+            log(f"[bench]   {k['kernel']:18s} {k['us']:9.2f} us  {k['GBps']:8.1f} GB/s  {100 * k['frac']:5.1f}%")
+        # dominant kernel: the most algorithmic bytes per token
+        per_tok = {k["kernel"]: k["bytes"] * (cfg.n_layers if k["kernel"] not in ("lm_head", "argmax") else 1)
+                   for k in kernels}
+        dom = max(kernels, key=lambda k: per_tok[k["kernel"]])
+        roof = {"bound": "hbm", "kernel": dom["kernel"], "achieved": dom["GBps"], "peak": PEAK_GBPS,
+                "unit": "GB/s", "frac": dom["frac"], "traffic": None,
+                "bytes_per_launch": dom["bytes"], "us_per_launch": dom["us"]}
+    g1 = None
+    if not args.no_profile:
+        g1 = gemv_config1(cq, np)
+        log(f"[bench] config-1 GEMV: {g1}")
+    st.free()
+    w.free()
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        t2 = time.perf_counter()
+        cpu = cpu_baseline(cfg, args.ctx, args.cpu_threads)
+        log(f"[bench] cpu baseline {cpu} ({time.perf_counter() - t2:.1f}s)")
+
+    res = {
+        "metric": "batch-1 decode tok/s (Qwen2.5-7B INT4, 32K ctx) + GEMV HBM GB/s % of peak",
+        "value": round(value, 3), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "w4a16-f16acc32" if args.quant == "int4" else args.quant, "data": "synthetic",
+        "config": {"workload": f"Qwen2.5-{args.model} {args.quant.upper()} random-init batch-1 greedy decode, "
+                               f"KV prefilled, timed positions {pos0 + args.warmup}..{args.ctx - 1}",
+                   "model": f"Qwen2.5-{args.model}", "global_batch": 1, "seq_len": args.ctx,
+                   "parallelism": "single-gpu"},
+        "device_ms_per_step": round(dev_us / 1e3, 5),
+        "roofline": roof, "cpu_baseline": cpu, "kernels": kernels, "gemv_config1": g1,
+    }
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

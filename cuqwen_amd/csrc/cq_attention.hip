@@ -1,0 +1,240 @@
+// FlashDecoding GQA attention over the fp16 KV cache for gfx950.
+//
+// Reference: gqa_attention_wmma_ksplit_stage1_kernel + stage2
+// (src/kernels.cu:105-324).  Design here:
+//   * grid = (partitions, kv heads); a partition is a run of 32-key tiles,
+//     sized at run time from *d_pos so one recorded graph serves every
+//     position; blocks past the last partition exit at once;
+//   * 8 waves per block, each wave takes every 8th tile of the partition and
+//     keeps an online softmax (running max / sum) and its O accumulator in
+//     matrix-core registers;
+//   * S^T = K Q^T with v_mfma_f32_16x16x32_f16 (keys as rows, the group's
+//     query heads as columns, padded to 16), then O^T += V^T P^T with the
+//     same instruction.  The K and V tiles are stored in the cache in exactly
+//     the operand order the instruction consumes (cq_common.h), so every
+//     tile is streamed with contiguous 16-byte-per-lane loads and the score
+//     tile feeds the P^T operand without any cross-lane movement;
+//   * the 8 waves merge in LDS, write one (m, l, O) partial per partition,
+//     and the last block of each kv head (atomic ticket) performs the
+//     log-sum-exp merge (kernels.cu:222-288) and resets its ticket.
+// Rounding follows the reference: scores are rounded to fp16 after the
+// 1/sqrt(hd) scale (kernels.cu:171), probabilities are rounded to fp16 for
+// the PV product while the row sum uses the unrounded values (:185-186).
+#include "cq_device.h"
+#include "cq_internal.h"
+
+#include <cmath>
+
+namespace cq {
+
+constexpr int kAttnWaves = 8;
+constexpr int kAttnThreads = kAttnWaves * kWave;
+constexpr int kAttnBlocksTarget = 256;   // one block per CU of MI355X
+constexpr int kMinTilesPerPart = 8;      // 256 keys: one tile per wave at least
+constexpr int kTileKeys = 32;
+
+int attention_max_parts(int n_kv) { return (kAttnBlocksTarget + n_kv - 1) / n_kv; }
+
+// Workspace: [64 counters (256 B)] [m: n_kv*P*16] [l: n_kv*P*16] [o: n_kv*P*16*hd] floats.
+size_t attention_workspace_bytes(int n_heads, int n_kv, int head_dim) {
+  (void)n_heads;
+  const size_t P = (size_t)attention_max_parts(n_kv);
+  return 256 + (size_t)n_kv * P * 16 * (2 + (size_t)head_dim) * sizeof(float);
+}
+
+template <int HD>
+__global__ __launch_bounds__(kAttnThreads) void attention_kernel(const AttnArgs a, unsigned* counters) {
+  constexpr int KK = HD / 32;   // mfma k-steps over head_dim for S^T
+  constexpr int DT = HD / 16;   // 16-row d tiles of O^T
+  const int kvh = blockIdx.y;
+  const int part = blockIdx.x;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int g = a.n_heads / a.n_kv;
+  const int T = *a.d_pos + 1;
+  const int n_tiles = (T + kTileKeys - 1) / kTileKeys;
+  const int P = gridDim.x;
+  int tpp = (n_tiles + P - 1) / P;
+  if (tpp < kMinTilesPerPart) tpp = kMinTilesPerPart;
+  const int nparts = (n_tiles + tpp - 1) / tpp;
+  if (part >= nparts) return;
+  const int tile0 = part * tpp;
+  const int tile1 = min(tile0 + tpp, n_tiles);
+
+  const int h = lane & 15;        // query head column of this lane
+  const int j = lane >> 4;        // k-slot group of this lane
+  const float scale = 1.0f / sqrtf((float)HD);
+
+  // Q^T as the B operand: lane holds q[h][kk*32 + j*8 .. +8]
+  h8_t qb[KK];
+  {
+    const _Float16* q = reinterpret_cast<const _Float16*>(a.q) + (int64_t)(kvh * g + h) * HD;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      if (h < g) qb[kk] = __builtin_bit_cast(h8_t, load_u4(q + kk * 32 + j * 8));
+      else qb[kk] = h8_t{0, 0, 0, 0, 0, 0, 0, 0};
+    }
+  }
+
+  const _Float16* kbase = reinterpret_cast<const _Float16*>(a.kcache) + (int64_t)kvh * a.max_seq * HD;
+  const _Float16* vbase = reinterpret_cast<const _Float16*>(a.vcache) + (int64_t)kvh * a.max_seq * HD;
+
+  float m = -INFINITY, l = 0.f;
+  f4_t o[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) o[dt] = f4_t{0.f, 0.f, 0.f, 0.f};
+
+  for (int ti = tile0 + wave; ti < tile1; ti += kAttnWaves) {
+    const _Float16* kt = kbase + (int64_t)ti * kTileKeys * HD;
+    const _Float16* vt = vbase + (int64_t)ti * kTileKeys * HD;
+    h8_t ka[2][KK];
+    h8_t va[DT];
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk)
+        ka[st][kk] = __builtin_bit_cast(h8_t, load_u4(kt + st * 16 * HD + (kk * 64 + lane) * 8));
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) va[dt] = __builtin_bit_cast(h8_t, load_u4(vt + (dt * 64 + lane) * 8));
+
+    f4_t s[2];
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      s[st] = f4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk)
+        s[st] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[st][kk], qb[kk], s[st], 0, 0, 0);
+    }
+    // lane holds S^T[key = ti*32 + st*16 + 4j + i][head h]
+    const int key0 = ti * kTileKeys + 4 * j;
+    const bool tail = (ti + 1) * kTileKeys > T;
+    float sv[8];
+    float mt = -INFINITY;
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float v = (float)(_Float16)(s[st][i] * scale);
+        if (tail && key0 + st * 16 + i >= T) v = -INFINITY;
+        sv[st * 4 + i] = v;
+        mt = fmaxf(mt, v);
+      }
+    mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
+    mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
+    const float mn = fmaxf(m, mt);
+    const float alpha = __expf(m - mn);
+    m = mn;
+    l *= alpha;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
+    h8_t pb;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float p = __expf(sv[e] - mn);
+      l += p;
+      pb[e] = (_Float16)p;
+    }
+    if (tail) {
+      // keys past the end may hold anything; keep them out of P*V
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int key = ti * kTileKeys + (e < 4 ? 4 * j + e : 16 + 4 * j + e - 4);
+          if (key >= T) va[dt][e] = (_Float16)0.f;
+        }
+    }
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[dt], pb, o[dt], 0, 0, 0);
+  }
+  l += __shfl_xor(l, 16, kWave);
+  l += __shfl_xor(l, 32, kWave);
+
+  // ---- merge the 8 waves in LDS: per wave m[16], l[16], O[16][HD]
+  __shared__ float wm[kAttnWaves][16], wl[kAttnWaves][16];
+  __shared__ float wo[kAttnWaves][16][HD + 1];
+  if (j == 0) { wm[wave][h] = m; wl[wave][h] = l; }
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) wo[wave][h][dt * 16 + 4 * j + i] = o[dt][i];
+  __syncthreads();
+
+  float* ws_m = reinterpret_cast<float*>(reinterpret_cast<char*>(a.workspace) + 256);
+  const int Pmax = gridDim.x;
+  float* ws_l = ws_m + (size_t)a.n_kv * Pmax * 16;
+  float* ws_o = ws_l + (size_t)a.n_kv * Pmax * 16;
+  const size_t pslot = (size_t)kvh * Pmax + part;
+  _Float16* out = reinterpret_cast<_Float16*>(a.out);
+
+  // block-level (m, l) per head, then O
+  for (int idx = threadIdx.x; idx < g * HD; idx += kAttnThreads) {
+    const int hh = idx / HD, d = idx % HD;
+    float M = -INFINITY;
+    for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, wm[w][hh]);
+    float L = 0.f, O = 0.f;
+    for (int w = 0; w < kAttnWaves; ++w) {
+      const float f = wm[w][hh] == -INFINITY ? 0.f : __expf(wm[w][hh] - M);
+      L += wl[w][hh] * f;
+      O += wo[w][hh][d] * f;
+    }
+    if (nparts == 1) {
+      out[(int64_t)(kvh * g + hh) * HD + d] = (_Float16)(O * (1.0f / (L + 1e-9f)));
+    } else {
+      ws_o[(pslot * 16 + hh) * HD + d] = O;
+      if (d == 0) { ws_m[pslot * 16 + hh] = M; ws_l[pslot * 16 + hh] = L; }
+    }
+  }
+  if (nparts == 1) return;
+
+  // ---- last block of this kv head merges all partitions
+  __shared__ unsigned ticket;
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) ticket = atomicAdd(&counters[kvh], 1u);
+  __syncthreads();
+  if (ticket != (unsigned)(nparts - 1)) return;
+  __threadfence();
+
+  __shared__ float pw[16][kAttnBlocksTarget];   // per-head partition weights
+  __shared__ float pinv[16];
+  for (int idx = threadIdx.x; idx < g; idx += kAttnThreads) {
+    float M = -INFINITY;
+    for (int p = 0; p < nparts; ++p) M = fmaxf(M, ws_m[((size_t)kvh * Pmax + p) * 16 + idx]);
+    float L = 0.f;
+    for (int p = 0; p < nparts; ++p) {
+      const size_t sl = ((size_t)kvh * Pmax + p) * 16 + idx;
+      const float f = __expf(ws_m[sl] - M);
+      pw[idx][p] = f;
+      L += ws_l[sl] * f;
+    }
+    pinv[idx] = 1.0f / (L + 1e-9f);
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < g * HD; idx += kAttnThreads) {
+    const int hh = idx / HD, d = idx % HD;
+    float O = 0.f;
+    for (int p = 0; p < nparts; ++p) O += ws_o[(((size_t)kvh * Pmax + p) * 16 + hh) * HD + d] * pw[hh][p];
+    out[(int64_t)(kvh * g + hh) * HD + d] = (_Float16)(O * pinv[hh]);
+  }
+  if (threadIdx.x == 0) counters[kvh] = 0u;
+}
+
+int launch_attention(const AttnArgs& a, hipStream_t stream) {
+  if (a.head_dim != 64 && a.head_dim != 128) return fail(CQ_EINVAL, "attention: head_dim must be 64 or 128");
+  if (a.n_kv <= 0 || a.n_heads % a.n_kv || a.n_heads / a.n_kv > 16 || a.n_kv > 64)
+    return fail(CQ_EINVAL, "attention: need n_heads/n_kv_heads <= 16 and n_kv_heads <= 64");
+  if (a.max_seq <= 0 || a.max_seq % kTileKeys) return fail(CQ_EINVAL, "attention: max_seq_len must be a multiple of 32");
+  if (!a.q || !a.kcache || !a.vcache || !a.out || !a.d_pos || !a.workspace)
+    return fail(CQ_EINVAL, "attention: null pointer");
+  const dim3 grid(attention_max_parts(a.n_kv), a.n_kv);
+  unsigned* counters = reinterpret_cast<unsigned*>(a.workspace);
+  if (a.head_dim == 128)
+    hipLaunchKernelGGL(attention_kernel<128>, grid, dim3(kAttnThreads), 0, stream, a, counters);
+  else
+    hipLaunchKernelGGL(attention_kernel<64>, grid, dim3(kAttnThreads), 0, stream, a, counters);
+  CQ_HIP(hipGetLastError());
+  return CQ_OK;
+}
+
+}  // namespace cq

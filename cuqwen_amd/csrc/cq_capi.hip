@@ -1,0 +1,213 @@
+// Op-level C ABI (the reference's launch_* family, include/kernels.cuh) and
+// device-memory helpers.
+#include "cq_internal.h"
+
+#include <vector>
+
+using namespace cq;
+
+static hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+extern "C" int cq_device_count(int32_t* n) {
+  if (!n) return fail(CQ_EINVAL, "null argument");
+  int c = 0;
+  CQ_HIP(hipGetDeviceCount(&c));
+  *n = c;
+  return CQ_OK;
+}
+extern "C" int cq_malloc(void** p, size_t bytes) {
+  if (!p) return fail(CQ_EINVAL, "null argument");
+  if (hipMalloc(p, bytes ? bytes : 1) != hipSuccess) return fail(CQ_ENOMEM, "hipMalloc failed");
+  return CQ_OK;
+}
+extern "C" int cq_free(void* p) {
+  if (p) CQ_HIP(hipFree(p));
+  return CQ_OK;
+}
+extern "C" int cq_memcpy_h2d(void* dst, const void* src, size_t bytes) {
+  CQ_HIP(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+  return CQ_OK;
+}
+extern "C" int cq_memcpy_d2h(void* dst, const void* src, size_t bytes) {
+  CQ_HIP(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+  return CQ_OK;
+}
+extern "C" int cq_memset(void* p, int value, size_t bytes) {
+  CQ_HIP(hipMemset(p, value, bytes));
+  return CQ_OK;
+}
+extern "C" int cq_synchronize(void) {
+  CQ_HIP(hipDeviceSynchronize());
+  return CQ_OK;
+}
+
+extern "C" int cq_embedding_lookup(const void* embed, const int32_t* d_token, void* out, int32_t dim, void* stream) {
+  return launch_embedding((const __half*)embed, d_token, (__half*)out, dim, as_stream(stream));
+}
+
+extern "C" int cq_rmsnorm(const void* x, const void* w, void* out, int32_t dim, float eps, void* stream) {
+  return launch_rmsnorm((const __half*)x, (const __half*)w, (__half*)out, dim, eps, as_stream(stream));
+}
+
+extern "C" int cq_gemv(int32_t quant_type, int32_t group_size, const void* W, const void* scale, const void* x, void* y,
+                       int32_t rows, int32_t cols, void* stream) {
+  GemvArgs a;
+  a.mode = GM_STORE; a.quant = quant_type; a.group = group_size; a.x = (const __half*)x;
+  a.K = cols; a.N = rows; a.W[0] = W; a.S[0] = (const __half*)scale; a.out[0] = (__half*)y;
+  return launch_gemv(a, as_stream(stream));
+}
+
+extern "C" int cq_gemv_add(int32_t quant_type, const void* W, const void* scale, const void* input, void* x_inout,
+                           int32_t rows, int32_t cols, void* stream) {
+  GemvArgs a;
+  a.mode = GM_RESID; a.quant = quant_type; a.x = (const __half*)input;
+  a.K = cols; a.N = rows; a.W[0] = W; a.S[0] = (const __half*)scale; a.out[0] = (__half*)x_inout;
+  return launch_gemv(a, as_stream(stream));
+}
+
+extern "C" int cq_fused_attn_block(int32_t quant_type, const void* x, const void* norm_weight, const void* Wq,
+                                   const void* Wk, const void* Wv, const void* Sq, const void* Sk, const void* Sv,
+                                   const void* bq, const void* bk, const void* bv, void* q_out, void* k_out,
+                                   void* v_out, int32_t dim, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
+                                   const int32_t* d_pos, float rope_theta, float eps, void* stream) {
+  if (!q_out || !k_out || !v_out) return fail(CQ_EINVAL, "fused_attn_block: null output");
+  GemvArgs a;
+  a.mode = GM_QKV; a.quant = quant_type; a.x = (const __half*)x; a.norm_w = (const __half*)norm_weight; a.eps = eps;
+  a.K = dim; a.N = (n_heads + 2 * n_kv_heads) * head_dim;
+  a.W[0] = Wq; a.W[1] = Wk; a.W[2] = Wv;
+  a.S[0] = (const __half*)Sq; a.S[1] = (const __half*)Sk; a.S[2] = (const __half*)Sv;
+  a.bias[0] = (const __half*)bq; a.bias[1] = (const __half*)bk; a.bias[2] = (const __half*)bv;
+  a.out[0] = (__half*)q_out; a.out[1] = (__half*)k_out; a.out[2] = (__half*)v_out;
+  a.n_heads = n_heads; a.n_kv = n_kv_heads; a.head_dim = head_dim; a.d_pos = d_pos; a.rope_theta = rope_theta;
+  return launch_gemv(a, as_stream(stream));
+}
+
+extern "C" int cq_fused_mlp_stage1(int32_t quant_type, const void* x, const void* norm_weight, const void* Wg,
+                                   const void* Wu, const void* Sg, const void* Su, void* out, int32_t dim,
+                                   int32_t inter_dim, float eps, void* stream) {
+  GemvArgs a;
+  a.mode = GM_SWIGLU; a.quant = quant_type; a.x = (const __half*)x; a.norm_w = (const __half*)norm_weight; a.eps = eps;
+  a.K = dim; a.N = inter_dim; a.W[0] = Wg; a.W[1] = Wu; a.S[0] = (const __half*)Sg; a.S[1] = (const __half*)Su;
+  a.out[0] = (__half*)out;
+  return launch_gemv(a, as_stream(stream));
+}
+
+extern "C" int cq_fused_mlp_stage2(int32_t quant_type, void* x, const void* Wd, const void* Sd, const void* inter,
+                                   int32_t dim, int32_t inter_dim, void* stream) {
+  return cq_gemv_add(quant_type, Wd, Sd, inter, x, dim, inter_dim, stream);
+}
+
+extern "C" int cq_compute_logits(int32_t lm_quant, const void* x, const void* W, const void* scale, void* logits,
+                                 int32_t vocab, int32_t dim, void* stream) {
+  if (lm_quant != CQ_LMHEAD_FP16 && lm_quant != CQ_LMHEAD_INT8) return fail(CQ_EINVAL, "compute_logits: bad format");
+  GemvArgs a;
+  a.mode = GM_STORE; a.quant = lm_quant == CQ_LMHEAD_INT8 ? CQ_QUANT_INT8 : CQ_QUANT_FP16; a.x = (const __half*)x;
+  a.K = dim; a.N = vocab; a.W[0] = W; a.S[0] = (const __half*)scale; a.out[0] = (__half*)logits;
+  return launch_gemv(a, as_stream(stream));
+}
+
+namespace cq {
+int launch_epoch_bump(uint32_t* d_epoch, hipStream_t stream);
+}
+
+// Workspace: [epoch uint32, padded to 256 B][stamp uint32 x vocab]; zero it
+// once before the first call.
+extern "C" size_t cq_penalty_workspace_bytes(int32_t vocab) { return 256 + (size_t)(vocab > 0 ? vocab : 0) * 4; }
+
+extern "C" int cq_apply_repetition_penalty(void* logits, const int32_t* d_history, const int32_t* d_history_len,
+                                           int32_t vocab, float penalty, void* workspace, void* stream) {
+  if (!logits || !d_history || !d_history_len || !workspace || vocab <= 0)
+    return fail(CQ_EINVAL, "repetition_penalty: bad arguments");
+  uint32_t* epoch = (uint32_t*)workspace;
+  uint32_t* stamp = (uint32_t*)((char*)workspace + 256);
+  const hipStream_t st = as_stream(stream);
+  CQ_TRY(launch_epoch_bump(epoch, st));
+  CQ_TRY(launch_stamp_history(stamp, d_history, d_history_len, vocab, epoch, st));
+  return launch_penalty_apply((__half*)logits, stamp, epoch, vocab, penalty, st);
+}
+
+extern "C" size_t cq_argmax_workspace_bytes(int32_t vocab) {
+  (void)vocab;
+  return kArgmaxBlocks * 8 + 64;
+}
+
+extern "C" int cq_argmax(const void* logits, int32_t* d_token_out, int32_t vocab, void* workspace, void* stream) {
+  if (!d_token_out) return fail(CQ_EINVAL, "argmax: null output");
+  return launch_argmax((const __half*)logits, vocab, (unsigned long long*)workspace, nullptr, d_token_out, nullptr,
+                       nullptr, as_stream(stream));
+}
+
+extern "C" int cq_kv_cache_store(const void* k, const void* v, void* kc, void* vc, const int32_t* d_pos,
+                                 int32_t n_kv_heads, int32_t max_seq_len, int32_t head_dim, void* stream) {
+  return launch_kv_store((const __half*)k, (const __half*)v, (__half*)kc, (__half*)vc, d_pos, n_kv_heads, max_seq_len,
+                         head_dim, as_stream(stream));
+}
+
+extern "C" size_t cq_attention_workspace_bytes(int32_t n_heads, int32_t n_kv_heads, int32_t head_dim) {
+  if (n_kv_heads <= 0 || head_dim <= 0) return 0;
+  return attention_workspace_bytes(n_heads, n_kv_heads, head_dim);
+}
+
+extern "C" int cq_gqa_attention_decode(const void* q, const void* kc, const void* vc, void* out, const int32_t* d_pos,
+                                       int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, int32_t max_seq_len,
+                                       void* workspace, void* stream) {
+  AttnArgs a;
+  a.q = (const __half*)q; a.kcache = (const __half*)kc; a.vcache = (const __half*)vc; a.out = (__half*)out;
+  a.d_pos = d_pos; a.n_heads = n_heads; a.n_kv = n_kv_heads; a.head_dim = head_dim; a.max_seq = max_seq_len;
+  a.workspace = workspace;
+  return launch_attention(a, as_stream(stream));
+}
+
+extern "C" int cq_dequantize(int32_t quant_type, int32_t group_size, const void* W, const void* scale, float* out,
+                             int32_t rows, int32_t cols, void* stream) {
+  return launch_dequant(quant_type, group_size, W, (const __half*)scale, out, rows, cols, as_stream(stream));
+}
+
+extern "C" int cq_time_gemv(int32_t quant_type, int32_t group_size, int32_t n_bufs, void* const* W_list,
+                            void* const* S_list, const void* x, void* y, int32_t rows, int32_t cols, int32_t iters,
+                            double* us_per_launch) {
+  if (n_bufs <= 0 || !W_list || iters <= 0 || !us_per_launch) return fail(CQ_EINVAL, "time_gemv: bad arguments");
+  hipStream_t st;
+  CQ_HIP(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
+  GemvArgs a;
+  a.mode = GM_STORE; a.quant = quant_type; a.group = group_size; a.x = (const __half*)x; a.K = cols; a.N = rows;
+  a.out[0] = (__half*)y;
+  int rc = CQ_OK;
+  hipGraph_t g = nullptr;
+  hipGraphExec_t ge = nullptr;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  float ms = 0.f;
+  auto body = [&]() -> int {
+    CQ_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+    for (int i = 0; i < iters; ++i) {
+      a.W[0] = W_list[i % n_bufs];
+      a.S[0] = S_list ? (const __half*)S_list[i % n_bufs] : nullptr;
+      int r = launch_gemv(a, st);
+      if (r != CQ_OK) {
+        hipGraph_t dummy;
+        hipStreamEndCapture(st, &dummy);
+        if (dummy) hipGraphDestroy(dummy);
+        return r;
+      }
+    }
+    CQ_HIP(hipStreamEndCapture(st, &g));
+    CQ_HIP(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
+    CQ_HIP(hipGraphLaunch(ge, st));   // warm-up
+    CQ_HIP(hipEventCreate(&e0));
+    CQ_HIP(hipEventCreate(&e1));
+    CQ_HIP(hipEventRecord(e0, st));
+    CQ_HIP(hipGraphLaunch(ge, st));
+    CQ_HIP(hipEventRecord(e1, st));
+    CQ_HIP(hipEventSynchronize(e1));
+    CQ_HIP(hipEventElapsedTime(&ms, e0, e1));
+    return CQ_OK;
+  };
+  rc = body();
+  if (ge) hipGraphExecDestroy(ge);
+  if (g) hipGraphDestroy(g);
+  if (e0) hipEventDestroy(e0);
+  if (e1) hipEventDestroy(e1);
+  hipStreamDestroy(st);
+  if (rc == CQ_OK) *us_per_launch = (double)ms * 1000.0 / iters;
+  return rc;
+}

@@ -1,0 +1,79 @@
+// Device-side building blocks for gfx950 (wave64): vector types, the
+// in-register int8/int4 -> fp16 unpack, packed fp16 dot products and wave
+// reductions.
+#pragma once
+
+#include "cq_common.h"
+
+namespace cq {
+
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ h2_t as_h2(uint32_t u) { return __builtin_bit_cast(h2_t, u); }
+__device__ __forceinline__ uint32_t as_u32(h2_t h) { return __builtin_bit_cast(uint32_t, h); }
+
+// v_dot2_f32_f16: a.x*b.x + a.y*b.y + c with fp32 accumulation.
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2(as_h2(a), as_h2(b), c, false);
+}
+
+// ---------------------------------------------------------------- unpack
+// Int4 (export_weights.py:197-199): byte k of a 32-bit word holds element 2k
+// in its low nibble and 2k+1 in its high nibble; the nibble is a 4-bit two's
+// complement value q in [-8, 7] (kernels.cu:35-37 sign-extends ((n^8)-8)).
+// After w ^= 0x88888888 each nibble is n' = q + 8 in [0, 15], and
+// (w' >> 4i) & 0x000F000F | 0x64006400 is the fp16 pair
+// (1024 + n'_{i}, 1024 + n'_{i+4}) -- exact, since fp16 spacing is 1 on
+// [1024, 2048).  So the word's 8 weights become 4 fp16 pairs holding
+// elements (0,4) (1,5) (2,6) (3,7), each equal to 1032 + q.
+constexpr uint32_t kInt4Flip = 0x88888888u;
+constexpr float kInt4Bias = 1032.0f;
+__device__ __forceinline__ uint32_t int4_pair(uint32_t flipped, int i) {
+  return ((flipped >> (4 * i)) & 0x000F000Fu) | 0x64006400u;
+}
+// Int8: byte b of a word is q in [-128, 127]; u = q ^ 0x80 = q + 128 and the
+// fp16 with bits 0x64uu is 1024 + u = 1152 + q.  v_perm_b32 builds the pair
+// (byte 2i, byte 2i+1) with 0x64 high bytes in one instruction.
+constexpr uint32_t kInt8Flip = 0x80808080u;
+constexpr float kInt8Bias = 1152.0f;
+__device__ __forceinline__ uint32_t int8_pair(uint32_t flipped, int i) {
+  // selector bytes 0-3 pick bytes of src1 (flipped), 4-7 bytes of src0.
+  return __builtin_amdgcn_perm(0x64646464u, flipped, i == 0 ? 0x04010400u : 0x04030402u);
+}
+
+// ------------------------------------------------------------- reductions
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+  return v;
+}
+
+// Block-wide sum for blockDim.x a multiple of 64 (<= 1024); `red` holds 16
+// floats of LDS.  All threads get the result.
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  const int w = threadIdx.x / kWave, nw = blockDim.x / kWave;
+  __syncthreads();
+  if ((threadIdx.x & (kWave - 1)) == 0) red[w] = v;
+  __syncthreads();
+  float t = 0.f;
+  for (int i = 0; i < nw; ++i) t += red[i];
+  return t;
+}
+
+__device__ __forceinline__ u4_t load_u4(const void* p) { return *reinterpret_cast<const u4_t*>(p); }
+__device__ __forceinline__ u4_t load_u4_stream(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(p));
+}
+
+}  // namespace cq

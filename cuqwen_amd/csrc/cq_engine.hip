@@ -1,0 +1,658 @@
+// Decode engine: device weights (file load or on-device synthesis), the
+// decode state and the HIP-graph-recorded decode step.
+//
+// Reference: src/load_weights.cpp:36-199 (loader), src/model.cu:5-223
+// (state, step body, graph capture and replay).
+#include "cq_device.h"
+#include "cq_format.h"
+#include "cq_internal.h"
+
+#include <cstdio>
+#include <cstring>
+#include <memory>
+#include <vector>
+
+using namespace cq;
+
+struct LayerW {
+  __half* in_norm = nullptr;
+  __half* post_norm = nullptr;
+  __half *bq = nullptr, *bk = nullptr, *bv = nullptr;
+  void *wq = nullptr, *wk = nullptr, *wv = nullptr, *wo = nullptr, *wg = nullptr, *wu = nullptr, *wd = nullptr;
+  __half *sq = nullptr, *sk = nullptr, *sv = nullptr, *so = nullptr, *sg = nullptr, *su = nullptr, *sd = nullptr;
+};
+
+struct cq_weights {
+  cq_config cfg{};
+  char* arena = nullptr;
+  size_t arena_bytes = 0;
+  __half* embed = nullptr;
+  __half* final_norm = nullptr;
+  void* lm_head = nullptr;        // fp16 [V][d] (possibly == embed) or int8 [V][d]
+  __half* lm_head_scale = nullptr;
+  std::vector<LayerW> layers;
+  // per tensor placement in the arena, in file order
+  struct Slot { TensorSpec spec; size_t w_off, s_off; };
+  std::vector<Slot> slots;
+};
+
+namespace {
+
+constexpr size_t kAlign = 256;
+size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+// Place every tensor in one device arena and wire the pointers.
+int weights_layout(cq_weights* w) {
+  size_t off = 0;
+  for (const auto& t : tensor_list(w->cfg)) {
+    cq_weights::Slot s{t, off, 0};
+    off = align_up(off + (size_t)t.weight_bytes);
+    if (t.scale_bytes) {
+      s.s_off = off;
+      off = align_up(off + (size_t)t.scale_bytes);
+    }
+    w->slots.push_back(s);
+  }
+  w->arena_bytes = off;
+  hipError_t e = hipMalloc(&w->arena, off);
+  if (e != hipSuccess) return fail(CQ_ENOMEM, std::string("weights: hipMalloc of ") + std::to_string(off) + " bytes failed");
+  w->layers.assign(w->cfg.n_layers, LayerW{});
+  for (const auto& s : w->slots) {
+    void* p = w->arena + s.w_off;
+    __half* sc = s.spec.scale_bytes ? reinterpret_cast<__half*>(w->arena + s.s_off) : nullptr;
+    __half* hp = reinterpret_cast<__half*>(p);
+    LayerW* L = s.spec.layer >= 0 ? &w->layers[s.spec.layer] : nullptr;
+    switch (s.spec.kind) {
+      case TK_EMBED: w->embed = hp; break;
+      case TK_FINAL_NORM: w->final_norm = hp; break;
+      case TK_LM_HEAD: w->lm_head = p; w->lm_head_scale = sc; break;
+      case TK_IN_NORM: L->in_norm = hp; break;
+      case TK_POST_NORM: L->post_norm = hp; break;
+      case TK_WQ: L->wq = p; L->sq = sc; break;
+      case TK_BQ: L->bq = hp; break;
+      case TK_WK: L->wk = p; L->sk = sc; break;
+      case TK_BK: L->bk = hp; break;
+      case TK_WV: L->wv = p; L->sv = sc; break;
+      case TK_BV: L->bv = hp; break;
+      case TK_WO: L->wo = p; L->so = sc; break;
+      case TK_WG: L->wg = p; L->sg = sc; break;
+      case TK_WU: L->wu = p; L->su = sc; break;
+      case TK_WD: L->wd = p; L->sd = sc; break;
+    }
+  }
+  if (!w->lm_head) w->lm_head = w->embed;   // tied (load_weights.cpp:159)
+  return CQ_OK;
+}
+
+// ------------------------------------------------------ on-device synthesis
+__global__ void synth_half_kernel(uint16_t* out, int64_t n, uint64_t seed, uint64_t stream, float mul, float mean) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    out[i] = synth_half(seed, stream, (uint64_t)i, mul, mean);
+}
+
+// One thread per (row, group of 128): generate, quantize as
+// export_weights.py:123-205 (fp32 scale for the division, fp16 stored scale).
+__global__ void synth_quant_kernel(uint8_t* q, uint16_t* s, int64_t rows, int64_t cols, int quant, uint64_t seed,
+                                   uint64_t stream, float mul) {
+  const int64_t ng = cols / kGroup;
+  const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= rows * ng) return;
+  const int64_t r = id / ng, gi = id % ng;
+  const uint64_t base = (uint64_t)(r * cols + gi * kGroup);
+  const float qmax = quant == CQ_QUANT_INT4 ? 7.0f : 127.0f;
+  float mx = 0.f;
+  for (int i = 0; i < kGroup; ++i) mx = fmaxf(mx, fabsf(h2f_bits(synth_half(seed, stream, base + i, mul, 0.f))));
+  const float sc = __fdiv_rn(mx, qmax);
+  const float safe = sc > 0.f ? sc : 1.0f;
+  s[id] = f2h_bits(sc);
+  if (quant == CQ_QUANT_INT8) {
+    int8_t* qr = reinterpret_cast<int8_t*>(q) + r * cols + gi * kGroup;
+    for (int i = 0; i < kGroup; ++i) {
+      float v = rintf(__fdiv_rn(h2f_bits(synth_half(seed, stream, base + i, mul, 0.f)), safe));
+      qr[i] = (int8_t)fminf(fmaxf(v, -qmax), qmax);
+    }
+  } else {
+    uint8_t* qr = q + r * (cols / 2) + gi * (kGroup / 2);
+    for (int i = 0; i < kGroup; i += 2) {
+      float v0 = rintf(__fdiv_rn(h2f_bits(synth_half(seed, stream, base + i, mul, 0.f)), safe));
+      float v1 = rintf(__fdiv_rn(h2f_bits(synth_half(seed, stream, base + i + 1, mul, 0.f)), safe));
+      const int q0 = (int)fminf(fmaxf(v0, -qmax), qmax), q1 = (int)fminf(fmaxf(v1, -qmax), qmax);
+      qr[i / 2] = (uint8_t)((q0 & 0xF) | ((q1 & 0xF) << 4));
+    }
+  }
+}
+
+int synth_device(cq_weights* w, uint64_t seed) {
+  const float mul = synth_mul(kWeightSigma);
+  for (const auto& s : w->slots) {
+    const TensorSpec& t = s.spec;
+    const uint64_t stream = tensor_stream(t.layer, t.kind);
+    if (t.quant == CQ_QUANT_FP16) {
+      const int64_t n = t.rows * t.cols;
+      const int blocks = (int)std::min<int64_t>((n + 255) / 256, 65536);
+      hipLaunchKernelGGL(synth_half_kernel, dim3(blocks), dim3(256), 0, 0, (uint16_t*)(w->arena + s.w_off), n, seed,
+                         stream, mul, kind_mean(t.kind));
+    } else {
+      const int64_t n = t.rows * (t.cols / kGroup);
+      hipLaunchKernelGGL(synth_quant_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, 0,
+                         (uint8_t*)(w->arena + s.w_off), (uint16_t*)(w->arena + s.s_off), t.rows, t.cols, t.quant,
+                         seed, stream, mul);
+    }
+    CQ_HIP(hipGetLastError());
+  }
+  CQ_HIP(hipDeviceSynchronize());
+  return CQ_OK;
+}
+
+}  // namespace
+
+// ====================================================================== state
+struct cq_state {
+  cq_config cfg{};
+  const cq_weights* w = nullptr;
+  hipStream_t stream = nullptr;
+  char* arena = nullptr;
+  __half *x = nullptr, *xb = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *inter = nullptr, *logits = nullptr;
+  __half *kcache = nullptr, *vcache = nullptr;
+  size_t layer_kv_halves = 0;
+  void* attn_ws = nullptr;
+  unsigned long long* argmax_ws = nullptr;
+  StepCtl* ctl = nullptr;
+  int* history = nullptr;
+  int* tokens_dev = nullptr;
+  uint32_t* stamp = nullptr;
+  int* host_pinned = nullptr;     // staging for the per-step control words
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  double last_us = 0.0;
+};
+
+namespace {
+
+int layer_gemvs(const cq_state* s, int l, GemvArgs* qkv, GemvArgs* o, GemvArgs* mlp1, GemvArgs* mlp2) {
+  const cq_config& c = s->cfg;
+  const LayerW& L = s->w->layers[l];
+  const int qd = c.n_heads * c.head_dim;
+  __half* kc = s->kcache + (size_t)l * s->layer_kv_halves;
+  __half* vc = s->vcache + (size_t)l * s->layer_kv_halves;
+  if (qkv) {
+    GemvArgs a;
+    a.mode = GM_QKV; a.quant = c.quant_type; a.x = s->x; a.norm_w = L.in_norm; a.eps = c.norm_eps;
+    a.K = c.dim; a.N = qd + 2 * c.n_kv_heads * c.head_dim;
+    a.W[0] = L.wq; a.W[1] = L.wk; a.W[2] = L.wv; a.S[0] = L.sq; a.S[1] = L.sk; a.S[2] = L.sv;
+    a.bias[0] = L.bq; a.bias[1] = L.bk; a.bias[2] = L.bv;
+    a.out[0] = s->q;
+    a.n_heads = c.n_heads; a.n_kv = c.n_kv_heads; a.head_dim = c.head_dim; a.d_pos = &s->ctl->pos;
+    a.rope_theta = c.rope_theta; a.kcache = kc; a.vcache = vc; a.max_seq = c.max_seq_len;
+    *qkv = a;
+  }
+  if (o) {
+    GemvArgs a;
+    a.mode = GM_RESID; a.quant = c.quant_type; a.x = s->xb; a.K = qd; a.N = c.dim;
+    a.W[0] = L.wo; a.S[0] = L.so; a.out[0] = s->x;
+    *o = a;
+  }
+  if (mlp1) {
+    GemvArgs a;
+    a.mode = GM_SWIGLU; a.quant = c.quant_type; a.x = s->x; a.norm_w = L.post_norm; a.eps = c.norm_eps;
+    a.K = c.dim; a.N = c.intermediate_size;
+    a.W[0] = L.wg; a.W[1] = L.wu; a.S[0] = L.sg; a.S[1] = L.su; a.out[0] = s->inter;
+    *mlp1 = a;
+  }
+  if (mlp2) {
+    GemvArgs a;
+    a.mode = GM_RESID; a.quant = c.quant_type; a.x = s->inter; a.K = c.intermediate_size; a.N = c.dim;
+    a.W[0] = L.wd; a.S[0] = L.sd; a.out[0] = s->x;
+    *mlp2 = a;
+  }
+  return CQ_OK;
+}
+
+AttnArgs layer_attn(const cq_state* s, int l) {
+  const cq_config& c = s->cfg;
+  AttnArgs a;
+  a.q = s->q;
+  a.kcache = s->kcache + (size_t)l * s->layer_kv_halves;
+  a.vcache = s->vcache + (size_t)l * s->layer_kv_halves;
+  a.out = s->xb;
+  a.d_pos = &s->ctl->pos;
+  a.n_heads = c.n_heads; a.n_kv = c.n_kv_heads; a.head_dim = c.head_dim; a.max_seq = c.max_seq_len;
+  a.workspace = s->attn_ws;
+  return a;
+}
+
+GemvArgs lm_head_gemv(const cq_state* s) {
+  const cq_config& c = s->cfg;
+  GemvArgs a;
+  a.mode = GM_STORE;
+  a.quant = c.lm_head_fmt == CQ_LMHEAD_INT8 ? CQ_QUANT_INT8 : CQ_QUANT_FP16;
+  a.x = s->x; a.norm_w = s->w->final_norm; a.eps = c.norm_eps;
+  a.K = c.dim; a.N = c.vocab_size;
+  a.W[0] = s->w->lm_head; a.S[0] = s->w->lm_head_scale; a.out[0] = s->logits;
+  a.stamp = s->stamp; a.d_epoch = &s->ctl->epoch; a.penalty = c.repetition_penalty;
+  return a;
+}
+
+// The decode step (src/model.cu:76-181), 5 launches per layer + 3:
+//   step_begin (embedding + penalty stamps)
+//   per layer: RMSNorm+QKV+bias+RoPE+KV store | attention | O-proj+residual |
+//              RMSNorm+gate/up+SwiGLU | down+residual
+//   final RMSNorm+lm_head+penalty | argmax (+ on-device step chaining)
+int step_body(cq_state* s) {
+  const cq_config& c = s->cfg;
+  hipStream_t st = s->stream;
+  CQ_TRY(launch_step_begin(s->w->embed, s->ctl, s->history, s->stamp, s->x, c.dim, c.vocab_size, st));
+  for (int l = 0; l < c.n_layers; ++l) {
+    GemvArgs qkv, o, m1, m2;
+    layer_gemvs(s, l, &qkv, &o, &m1, &m2);
+    CQ_TRY(launch_gemv(qkv, st));
+    CQ_TRY(launch_attention(layer_attn(s, l), st));
+    CQ_TRY(launch_gemv(o, st));
+    CQ_TRY(launch_gemv(m1, st));
+    CQ_TRY(launch_gemv(m2, st));
+  }
+  CQ_TRY(launch_gemv(lm_head_gemv(s), st));
+  CQ_TRY(launch_argmax(s->logits, c.vocab_size, s->argmax_ws, s->ctl, nullptr, s->history, s->tokens_dev, st));
+  return CQ_OK;
+}
+
+int ensure_graph(cq_state* s) {
+  if (s->exec) return CQ_OK;
+  CQ_HIP(hipStreamBeginCapture(s->stream, hipStreamCaptureModeThreadLocal));
+  const int rc = step_body(s);
+  hipGraph_t g = nullptr;
+  const hipError_t e = hipStreamEndCapture(s->stream, &g);
+  if (rc != CQ_OK) {
+    if (g) hipGraphDestroy(g);
+    return rc;
+  }
+  CQ_HIP(e);
+  s->graph = g;
+  CQ_HIP(hipGraphInstantiate(&s->exec, g, nullptr, nullptr, 0));
+  return CQ_OK;
+}
+
+// Writes the host-owned control words (token, pos, history_len, chain, step).
+int set_ctl(cq_state* s, int token, int pos, const int32_t* history, int history_len, int chain) {
+  int* h = s->host_pinned;
+  h[0] = token; h[1] = pos; h[2] = history_len; h[3] = chain; h[4] = 0;
+  CQ_HIP(hipMemcpyAsync(s->ctl, h, 5 * sizeof(int), hipMemcpyHostToDevice, s->stream));
+  if (history_len > 0) {
+    CQ_HIP(hipMemcpyAsync(s->history, history, (size_t)history_len * sizeof(int), hipMemcpyHostToDevice, s->stream));
+  }
+  return CQ_OK;
+}
+
+int check_step_args(const cq_state* s, int token, int pos, const int32_t* history, int history_len) {
+  if (pos < 0 || pos >= s->cfg.max_seq_len) return fail(CQ_ERANGE, "position outside [0, max_seq_len)");
+  if (token < 0 || token >= s->cfg.vocab_size) return fail(CQ_ERANGE, "token outside the vocabulary");
+  if (history_len < 0 || history_len > s->cfg.max_seq_len) return fail(CQ_ERANGE, "history_len outside [0, max_seq_len]");
+  if (history_len > 0 && !history) return fail(CQ_EINVAL, "null history with history_len > 0");
+  return CQ_OK;
+}
+
+__global__ void fill_kv_kernel(__half* kc, __half* vc, int n_layers, int n_kv, int n_pos, int max_seq, int hd,
+                               uint64_t seed, float mul) {
+  const int64_t per_head = (int64_t)n_pos * hd;
+  const int64_t total = (int64_t)n_layers * n_kv * per_head;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t e = i % per_head;
+    const int lh = (int)(i / per_head);
+    const int l = lh / n_kv, h = lh % n_kv;
+    const int t = (int)(e / hd), d = (int)(e % hd);
+    const size_t lo = (size_t)l * n_kv * max_seq * hd;
+    kc[lo + kv_k_offset(h, t, d, max_seq, hd)] = __ushort_as_half(synth_half(seed, kv_stream(l, h, 0), e, mul, 0.f));
+    vc[lo + kv_v_offset(h, t, d, max_seq, hd)] = __ushort_as_half(synth_half(seed, kv_stream(l, h, 1), e, mul, 0.f));
+  }
+}
+
+}  // namespace
+
+// ===================================================================== C ABI
+extern "C" int cq_load_weights(const char* path, const cq_config* expect, cq_config* cfg_out, cq_weights** out) {
+  if (!path || !out) return fail(CQ_EINVAL, "load_weights: null argument");
+  cq_config c{};
+  CQ_TRY(cq_read_header(path, &c));
+  if (expect) {
+    // load_weights.cpp:62-84: dims and quant type must match the expected config
+    if (c.vocab_size != expect->vocab_size || c.dim != expect->dim || c.intermediate_size != expect->intermediate_size ||
+        c.n_layers != expect->n_layers || c.n_heads != expect->n_heads || c.n_kv_heads != expect->n_kv_heads ||
+        c.head_dim != expect->head_dim)
+      return fail(CQ_EFORMAT, "binary header dimensions do not match the expected config");
+    if (c.quant_type != expect->quant_type) return fail(CQ_EFORMAT, "quantization mismatch between file and expected config");
+  }
+  std::unique_ptr<cq_weights> w(new cq_weights);
+  w->cfg = c;
+  CQ_TRY(weights_layout(w.get()));
+  FILE* f = std::fopen(path, "rb");
+  if (!f) {
+    hipFree(w->arena);
+    return fail(CQ_EIO, std::string("cannot open weight file: ") + path);
+  }
+  std::fseek(f, 256, SEEK_SET);
+  const size_t kChunk = 64u << 20;
+  void* staging = nullptr;
+  if (hipHostMalloc(&staging, kChunk, hipHostMallocDefault) != hipSuccess) {
+    std::fclose(f);
+    hipFree(w->arena);
+    return fail(CQ_ENOMEM, "load_weights: pinned staging allocation failed");
+  }
+  int rc = CQ_OK;
+  auto copy_segment = [&](size_t dst_off, int64_t bytes) -> int {
+    int64_t left = bytes;
+    size_t at = dst_off;
+    while (left > 0) {
+      const size_t n = (size_t)std::min<int64_t>(left, (int64_t)kChunk);
+      if (std::fread(staging, 1, n, f) != n) return fail(CQ_EIO, "unexpected end of file while reading tensor data");
+      if (hipMemcpy(w->arena + at, staging, n, hipMemcpyHostToDevice) != hipSuccess)
+        return fail(CQ_EHIP, "load_weights: hipMemcpy failed");
+      at += n;
+      left -= (int64_t)n;
+    }
+    return CQ_OK;
+  };
+  for (const auto& s : w->slots) {
+    rc = copy_segment(s.w_off, s.spec.weight_bytes);
+    if (rc == CQ_OK && s.spec.scale_bytes) rc = copy_segment(s.s_off, s.spec.scale_bytes);
+    if (rc != CQ_OK) break;
+  }
+  std::fclose(f);
+  hipHostFree(staging);
+  if (rc != CQ_OK) {
+    hipFree(w->arena);
+    return rc;
+  }
+  if (cfg_out) *cfg_out = c;
+  *out = w.release();
+  return CQ_OK;
+}
+
+extern "C" int cq_synth_weights(const cq_config* cfg, uint64_t seed, cq_weights** out) {
+  if (!cfg || !out) return fail(CQ_EINVAL, "synth_weights: null argument");
+  CQ_TRY(validate_config(*cfg));
+  std::unique_ptr<cq_weights> w(new cq_weights);
+  w->cfg = *cfg;
+  CQ_TRY(weights_layout(w.get()));
+  const int rc = synth_device(w.get(), seed);
+  if (rc != CQ_OK) {
+    hipFree(w->arena);
+    return rc;
+  }
+  *out = w.release();
+  return CQ_OK;
+}
+
+extern "C" int cq_free_weights(cq_weights* w) {
+  if (!w) return CQ_OK;
+  if (w->arena) CQ_HIP(hipFree(w->arena));
+  delete w;
+  return CQ_OK;
+}
+
+extern "C" int cq_weights_tensor(const cq_weights* w, const char* name, int32_t layer, void** dptr, size_t* bytes) {
+  if (!w || !name || !dptr) return fail(CQ_EINVAL, "weights_tensor: null argument");
+  struct N { const char* n; int kind; bool scale; };
+  static const N names[] = {{"embed", TK_EMBED, false}, {"final_norm", TK_FINAL_NORM, false},
+                            {"lm_head", TK_LM_HEAD, false}, {"lm_head_scale", TK_LM_HEAD, true},
+                            {"in_norm", TK_IN_NORM, false}, {"wq", TK_WQ, false}, {"sq", TK_WQ, true},
+                            {"bq", TK_BQ, false}, {"wk", TK_WK, false}, {"sk", TK_WK, true}, {"bk", TK_BK, false},
+                            {"wv", TK_WV, false}, {"sv", TK_WV, true}, {"bv", TK_BV, false}, {"wo", TK_WO, false},
+                            {"so", TK_WO, true}, {"post_norm", TK_POST_NORM, false}, {"wg", TK_WG, false},
+                            {"sg", TK_WG, true}, {"wu", TK_WU, false}, {"su", TK_WU, true}, {"wd", TK_WD, false},
+                            {"sd", TK_WD, true}};
+  for (const auto& n : names) {
+    if (std::strcmp(n.n, name)) continue;
+    for (const auto& s : w->slots) {
+      if (s.spec.kind != n.kind || (s.spec.layer >= 0 && s.spec.layer != layer)) continue;
+      if (n.scale && !s.spec.scale_bytes) return fail(CQ_EINVAL, "weights_tensor: tensor has no scales");
+      *dptr = w->arena + (n.scale ? s.s_off : s.w_off);
+      if (bytes) *bytes = (size_t)(n.scale ? s.spec.scale_bytes : s.spec.weight_bytes);
+      return CQ_OK;
+    }
+    if (n.kind == TK_LM_HEAD && !n.scale) {   // tied
+      *dptr = w->embed;
+      if (bytes) *bytes = (size_t)w->cfg.vocab_size * w->cfg.dim * 2;
+      return CQ_OK;
+    }
+    return fail(CQ_EINVAL, "weights_tensor: no such tensor for this layer / config");
+  }
+  return fail(CQ_EINVAL, std::string("weights_tensor: unknown name ") + name);
+}
+
+extern "C" int cq_state_create(const cq_config* cfg, const cq_weights* w, cq_state** out) {
+  if (!cfg || !w || !out) return fail(CQ_EINVAL, "state_create: null argument");
+  CQ_TRY(validate_config(*cfg));
+  if (std::memcmp(cfg, &w->cfg, offsetof(cq_config, norm_eps)) != 0)
+    return fail(CQ_EINVAL, "state_create: config does not match the weights");
+  std::unique_ptr<cq_state> s(new cq_state);
+  s->cfg = *cfg;
+  s->w = w;
+  const cq_config& c = *cfg;
+  const size_t d = c.dim, qd = (size_t)c.n_heads * c.head_dim, kvd = (size_t)c.n_kv_heads * c.head_dim;
+  s->layer_kv_halves = (size_t)c.n_kv_heads * c.max_seq_len * c.head_dim;
+  const size_t kv_bytes = (size_t)c.n_layers * s->layer_kv_halves * 2;
+  // one arena: small activations, control block, history, stamps, workspaces, K, V
+  size_t off = 0;
+  auto take = [&](size_t bytes) { size_t o = off; off = align_up(off + bytes); return o; };
+  const size_t o_x = take(d * 2), o_xb = take(qd * 2), o_q = take(qd * 2), o_k = take(kvd * 2), o_v = take(kvd * 2),
+               o_inter = take((size_t)c.intermediate_size * 2), o_logits = take((size_t)c.vocab_size * 2),
+               o_ctl = take(sizeof(StepCtl)), o_hist = take((size_t)c.max_seq_len * 4),
+               o_tok = take((size_t)c.max_seq_len * 4), o_stamp = take((size_t)c.vocab_size * 4),
+               o_attn = take(attention_workspace_bytes(c.n_heads, c.n_kv_heads, c.head_dim)),
+               o_arg = take(kArgmaxBlocks * 8 + 64);
+  const size_t small = off;
+  const size_t o_kc = take(kv_bytes), o_vc = take(kv_bytes);
+  if (hipMalloc(&s->arena, off) != hipSuccess) return fail(CQ_ENOMEM, "state_create: device allocation failed");
+  char* a = s->arena;
+  s->x = (__half*)(a + o_x); s->xb = (__half*)(a + o_xb); s->q = (__half*)(a + o_q); s->k = (__half*)(a + o_k);
+  s->v = (__half*)(a + o_v); s->inter = (__half*)(a + o_inter); s->logits = (__half*)(a + o_logits);
+  s->ctl = (StepCtl*)(a + o_ctl); s->history = (int*)(a + o_hist); s->tokens_dev = (int*)(a + o_tok);
+  s->stamp = (uint32_t*)(a + o_stamp); s->attn_ws = a + o_attn; s->argmax_ws = (unsigned long long*)(a + o_arg);
+  s->kcache = (__half*)(a + o_kc); s->vcache = (__half*)(a + o_vc);
+  int rc = CQ_OK;
+  auto chk = [&](hipError_t e, const char* what) {
+    if (e != hipSuccess && rc == CQ_OK) rc = fail(CQ_EHIP, std::string("state_create: ") + what + ": " + hipGetErrorString(e));
+  };
+  chk(hipMemset(a, 0, small), "hipMemset");
+  chk(hipMemset(a + o_kc, 0, kv_bytes), "hipMemset K");   // model.cu:37-38
+  chk(hipMemset(a + o_vc, 0, kv_bytes), "hipMemset V");
+  StepCtl init{};
+  init.epoch = 1u;
+  init.max_history = c.max_seq_len;
+  chk(hipMemcpy(s->ctl, &init, sizeof init, hipMemcpyHostToDevice), "hipMemcpy ctl");
+  chk(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking), "hipStreamCreate");
+  chk(hipHostMalloc((void**)&s->host_pinned, 64 * sizeof(int), hipHostMallocDefault), "hipHostMalloc");
+  chk(hipEventCreate(&s->ev0), "hipEventCreate");
+  chk(hipEventCreate(&s->ev1), "hipEventCreate");
+  if (rc != CQ_OK) {
+    cq_state_destroy(s.release());
+    return rc;
+  }
+  *out = s.release();
+  return CQ_OK;
+}
+
+extern "C" int cq_state_destroy(cq_state* s) {
+  if (!s) return CQ_OK;
+  if (s->stream) hipStreamSynchronize(s->stream);
+  if (s->exec) hipGraphExecDestroy(s->exec);
+  if (s->graph) hipGraphDestroy(s->graph);
+  if (s->ev0) hipEventDestroy(s->ev0);
+  if (s->ev1) hipEventDestroy(s->ev1);
+  if (s->host_pinned) hipHostFree(s->host_pinned);
+  if (s->stream) hipStreamDestroy(s->stream);
+  if (s->arena) hipFree(s->arena);
+  delete s;
+  return CQ_OK;
+}
+
+extern "C" int cq_forward(cq_state* s, int32_t token, int32_t pos, const int32_t* history, int32_t history_len,
+                          int32_t* token_out) {
+  if (!s) return fail(CQ_EINVAL, "forward: null state");
+  CQ_TRY(check_step_args(s, token, pos, history, history_len));
+  CQ_TRY(ensure_graph(s));
+  CQ_TRY(set_ctl(s, token, pos, history, history_len, 0));
+  CQ_HIP(hipGraphLaunch(s->exec, s->stream));
+  CQ_HIP(hipMemcpyAsync(s->host_pinned + 8, &s->ctl->sampled, sizeof(int), hipMemcpyDeviceToHost, s->stream));
+  CQ_HIP(hipStreamSynchronize(s->stream));
+  if (token_out) *token_out = s->host_pinned[8];
+  return CQ_OK;
+}
+
+extern "C" int cq_decode(cq_state* s, int32_t token, int32_t pos0, int32_t n_steps, const int32_t* history,
+                         int32_t history_len, int32_t* tokens_out) {
+  if (!s) return fail(CQ_EINVAL, "decode: null state");
+  CQ_TRY(check_step_args(s, token, pos0, history, history_len));
+  if (n_steps <= 0 || (int64_t)pos0 + n_steps > s->cfg.max_seq_len)
+    return fail(CQ_ERANGE, "decode: pos0 + n_steps exceeds max_seq_len");
+  CQ_TRY(ensure_graph(s));
+  CQ_TRY(set_ctl(s, token, pos0, history, history_len, 1));
+  CQ_HIP(hipEventRecord(s->ev0, s->stream));
+  for (int i = 0; i < n_steps; ++i) CQ_HIP(hipGraphLaunch(s->exec, s->stream));
+  CQ_HIP(hipEventRecord(s->ev1, s->stream));
+  if (tokens_out)
+    CQ_HIP(hipMemcpyAsync(tokens_out, s->tokens_dev, (size_t)n_steps * sizeof(int), hipMemcpyDeviceToHost, s->stream));
+  CQ_HIP(hipStreamSynchronize(s->stream));
+  float ms = 0.f;
+  CQ_HIP(hipEventElapsedTime(&ms, s->ev0, s->ev1));
+  s->last_us = (double)ms * 1000.0 / n_steps;
+  return CQ_OK;
+}
+
+extern "C" int cq_state_last_decode_us(cq_state* s, double* us) {
+  if (!s || !us) return fail(CQ_EINVAL, "null argument");
+  *us = s->last_us;
+  return CQ_OK;
+}
+
+extern "C" int cq_state_logits(cq_state* s, uint16_t* host_out) {
+  if (!s || !host_out) return fail(CQ_EINVAL, "state_logits: null argument");
+  CQ_HIP(hipMemcpyAsync(host_out, s->logits, (size_t)s->cfg.vocab_size * 2, hipMemcpyDeviceToHost, s->stream));
+  CQ_HIP(hipStreamSynchronize(s->stream));
+  return CQ_OK;
+}
+
+extern "C" int cq_state_fill_kv(cq_state* s, int32_t n_pos, uint64_t seed) {
+  if (!s) return fail(CQ_EINVAL, "fill_kv: null state");
+  if (n_pos < 0 || n_pos > s->cfg.max_seq_len) return fail(CQ_ERANGE, "fill_kv: n_pos outside [0, max_seq_len]");
+  if (n_pos == 0) return CQ_OK;
+  const cq_config& c = s->cfg;
+  hipLaunchKernelGGL(fill_kv_kernel, dim3(8192), dim3(256), 0, s->stream, s->kcache, s->vcache, c.n_layers,
+                     c.n_kv_heads, n_pos, c.max_seq_len, c.head_dim, seed, synth_mul(1.0));
+  CQ_HIP(hipGetLastError());
+  CQ_HIP(hipStreamSynchronize(s->stream));
+  return CQ_OK;
+}
+
+static int kv_slab(cq_state* s, int layer, int kv_head, int kind, int n_pos, __half** base, size_t* halves) {
+  const cq_config& c = s->cfg;
+  if (layer < 0 || layer >= c.n_layers || kv_head < 0 || kv_head >= c.n_kv_heads || (kind != 0 && kind != 1))
+    return fail(CQ_EINVAL, "kv access: bad layer / head / kind");
+  if (n_pos < 0 || n_pos > c.max_seq_len) return fail(CQ_ERANGE, "kv access: n_pos outside [0, max_seq_len]");
+  const int tile = kind == 0 ? 16 : 32;
+  const int tiles = (n_pos + tile - 1) / tile;
+  *halves = (size_t)tiles * tile * c.head_dim;
+  *base = (kind == 0 ? s->kcache : s->vcache) + (size_t)layer * s->layer_kv_halves +
+          (size_t)kv_head * c.max_seq_len * c.head_dim;
+  return CQ_OK;
+}
+
+extern "C" int cq_state_kv_read(cq_state* s, int32_t layer, int32_t kv_head, int32_t kind, int32_t n_pos,
+                                uint16_t* host_out) {
+  if (!s || !host_out) return fail(CQ_EINVAL, "kv_read: null argument");
+  __half* base;
+  size_t halves;
+  CQ_TRY(kv_slab(s, layer, kv_head, kind, n_pos, &base, &halves));
+  std::vector<uint16_t> tmp(halves);
+  CQ_HIP(hipStreamSynchronize(s->stream));
+  CQ_HIP(hipMemcpy(tmp.data(), base, halves * 2, hipMemcpyDeviceToHost));
+  const int hd = s->cfg.head_dim, ms = s->cfg.max_seq_len;
+  for (int t = 0; t < n_pos; ++t)
+    for (int d = 0; d < hd; ++d)
+      host_out[(size_t)t * hd + d] = tmp[(size_t)(kind == 0 ? kv_k_offset(0, t, d, ms, hd) : kv_v_offset(0, t, d, ms, hd))];
+  return CQ_OK;
+}
+
+extern "C" int cq_state_kv_write(cq_state* s, int32_t layer, int32_t kv_head, int32_t kind, int32_t n_pos,
+                                 const uint16_t* host_in) {
+  if (!s || !host_in) return fail(CQ_EINVAL, "kv_write: null argument");
+  __half* base;
+  size_t halves;
+  CQ_TRY(kv_slab(s, layer, kv_head, kind, n_pos, &base, &halves));
+  std::vector<uint16_t> tmp(halves);
+  CQ_HIP(hipStreamSynchronize(s->stream));
+  CQ_HIP(hipMemcpy(tmp.data(), base, halves * 2, hipMemcpyDeviceToHost));
+  const int hd = s->cfg.head_dim, ms = s->cfg.max_seq_len;
+  for (int t = 0; t < n_pos; ++t)
+    for (int d = 0; d < hd; ++d)
+      tmp[(size_t)(kind == 0 ? kv_k_offset(0, t, d, ms, hd) : kv_v_offset(0, t, d, ms, hd))] = host_in[(size_t)t * hd + d];
+  CQ_HIP(hipMemcpy(base, tmp.data(), halves * 2, hipMemcpyHostToDevice));
+  return CQ_OK;
+}
+
+// ------------------------------------------------------------ profiling
+extern "C" int cq_state_profile(cq_state* s, int32_t pos, int32_t iters, int32_t max_kernels, char* names,
+                                double* us_per_launch, double* bytes_per_launch, int32_t* n_kernels) {
+  if (!s || !names || !us_per_launch || !bytes_per_launch || !n_kernels || iters <= 0)
+    return fail(CQ_EINVAL, "profile: bad arguments");
+  if (pos < 0 || pos >= s->cfg.max_seq_len) return fail(CQ_ERANGE, "profile: pos outside [0, max_seq_len)");
+  const cq_config& c = s->cfg;
+  CQ_TRY(set_ctl(s, 0, pos, nullptr, 0, 0));
+  CQ_HIP(hipStreamSynchronize(s->stream));
+  const double d = c.dim, I = c.intermediate_size, qd = (double)c.n_heads * c.head_dim,
+               kvd = (double)c.n_kv_heads * c.head_dim, V = c.vocab_size;
+  auto wbytes = [&](int quant, double rows, double cols) {
+    return quant == CQ_QUANT_INT4 ? rows * cols / 2 + 2 * rows * cols / 128
+         : quant == CQ_QUANT_INT8 ? rows * cols + 2 * rows * cols / 128 : 2 * rows * cols;
+  };
+  const int qt = c.quant_type;
+  const int lmq = c.lm_head_fmt == CQ_LMHEAD_INT8 ? CQ_QUANT_INT8 : CQ_QUANT_FP16;
+  const double T = pos + 1;
+  struct K { const char* name; double bytes; int kind; };
+  // bytes: weights + scales + activations in/out (+ bias, residual)
+  const K ks[] = {
+      {"qkv_rope_kvstore", wbytes(qt, qd + 2 * kvd, d) + 2 * d * 2 + 2 * (qd + 2 * kvd) * 2, 0},
+      {"attention", 2.0 * c.n_kv_heads * T * c.head_dim * 2 + 2 * qd * 2, 1},
+      {"o_proj_residual", wbytes(qt, d, qd) + 2 * qd + 2 * d * 2, 2},
+      {"gate_up_swiglu", wbytes(qt, 2 * I, d) + 2 * d * 2 + 2 * I, 3},
+      {"down_residual", wbytes(qt, d, I) + 2 * I + 2 * d * 2, 4},
+      {"lm_head", wbytes(lmq, V, d) + 2 * d * 2 + 2 * V, 5},
+      {"argmax", 2 * V, 6},
+  };
+  const int nk = (int)(sizeof ks / sizeof ks[0]);
+  int n = 0;
+  for (int i = 0; i < nk && n < max_kernels; ++i, ++n) {
+    const K& k = ks[i];
+    const bool per_layer = k.kind <= 4;
+    const int reps = per_layer ? c.n_layers : 1;
+    auto run = [&]() -> int {
+      for (int l = 0; l < reps; ++l) {
+        GemvArgs qkv, o, m1, m2;
+        layer_gemvs(s, l, &qkv, &o, &m1, &m2);
+        switch (k.kind) {
+          case 0: CQ_TRY(launch_gemv(qkv, s->stream)); break;
+          case 1: CQ_TRY(launch_attention(layer_attn(s, l), s->stream)); break;
+          case 2: CQ_TRY(launch_gemv(o, s->stream)); break;
+          case 3: CQ_TRY(launch_gemv(m1, s->stream)); break;
+          case 4: CQ_TRY(launch_gemv(m2, s->stream)); break;
+          case 5: CQ_TRY(launch_gemv(lm_head_gemv(s), s->stream)); break;
+          case 6: CQ_TRY(launch_argmax(s->logits, c.vocab_size, s->argmax_ws, nullptr, nullptr, nullptr, nullptr, s->stream)); break;
+        }
+      }
+      return CQ_OK;
+    };
+    CQ_TRY(run());   // warm-up
+    CQ_HIP(hipEventRecord(s->ev0, s->stream));
+    for (int it = 0; it < iters; ++it) CQ_TRY(run());
+    CQ_HIP(hipEventRecord(s->ev1, s->stream));
+    CQ_HIP(hipEventSynchronize(s->ev1));
+    float ms = 0.f;
+    CQ_HIP(hipEventElapsedTime(&ms, s->ev0, s->ev1));
+    std::snprintf(names + 32 * n, 32, "%s", k.name);
+    us_per_launch[n] = (double)ms * 1000.0 / ((double)iters * reps);
+    bytes_per_launch[n] = k.bytes;
+  }
+  *n_kernels = n;
+  return CQ_OK;
+}

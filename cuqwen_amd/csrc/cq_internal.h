@@ -1,0 +1,96 @@
+// Internal (C++) launch interface between the kernels and the engine / C ABI.
+#pragma once
+
+#include "cq_common.h"
+
+namespace cq {
+
+enum GemvMode { GM_STORE = 0, GM_RESID = 1, GM_SWIGLU = 2, GM_QKV = 3 };
+
+struct GemvArgs {
+  int mode = GM_STORE;
+  int quant = CQ_QUANT_FP16;
+  int group = kGroup;           // 128, or 0 for one scale per row
+  const __half* x = nullptr;    // input vector [K]
+  const __half* norm_w = nullptr;  // fused RMSNorm weight (nullptr: x is used as is)
+  float eps = 1e-6f;
+  int K = 0;                    // contraction length
+  int N = 0;                    // output rows (SWIGLU: inter rows; QKV: qd + 2 kvd)
+  const void* W[3] = {nullptr, nullptr, nullptr};      // QKV: q,k,v  SWIGLU: gate, up
+  const __half* S[3] = {nullptr, nullptr, nullptr};    // fp16 scales (quantized only)
+  const __half* bias[3] = {nullptr, nullptr, nullptr};
+  __half* out[3] = {nullptr, nullptr, nullptr};        // RESID: out[0] is read and written
+  // QKV / RoPE / KV store
+  int n_heads = 0, n_kv = 0, head_dim = 0;
+  const int* d_pos = nullptr;
+  float rope_theta = 1e6f;
+  __half* kcache = nullptr;     // layer slice, tiled layout (kv_k_offset)
+  __half* vcache = nullptr;
+  int max_seq = 0;
+  // repetition penalty applied to the stored value (logits)
+  const uint32_t* stamp = nullptr;
+  const uint32_t* d_epoch = nullptr;
+  float penalty = 1.f;
+};
+
+// Validates shapes and launches; returns CQ_OK or an error code.
+int launch_gemv(const GemvArgs& a, hipStream_t stream);
+int gemv_check(const GemvArgs& a);
+
+int launch_dequant(int quant, int group, const void* W, const __half* S, float* out, int rows, int cols,
+                   hipStream_t stream);
+
+// ---------------------------------------------------------------- attention
+struct AttnArgs {
+  const __half* q = nullptr;    // [n_heads * hd] (after RoPE)
+  const __half* kcache = nullptr;  // layer slice
+  const __half* vcache = nullptr;
+  __half* out = nullptr;        // [n_heads * hd]
+  const int* d_pos = nullptr;
+  int n_heads = 0, n_kv = 0, head_dim = 0, max_seq = 0;
+  void* workspace = nullptr;
+};
+size_t attention_workspace_bytes(int n_heads, int n_kv, int head_dim);
+int launch_attention(const AttnArgs& a, hipStream_t stream);
+int attention_max_parts(int n_kv);
+
+// --------------------------------------------------------------- misc ops
+int launch_embedding(const __half* embed, const int* d_token, __half* out, int dim, hipStream_t stream);
+int launch_rmsnorm(const __half* x, const __half* w, __half* out, int dim, float eps, hipStream_t stream);
+int launch_kv_store(const __half* k, const __half* v, __half* kc, __half* vc, const int* d_pos, int n_kv,
+                    int max_seq, int hd, hipStream_t stream);
+// Marks ids d_history[0..*d_history_len) in `stamp` with the value *d_epoch.
+int launch_stamp_history(uint32_t* stamp, const int* d_history, const int* d_history_len, int vocab,
+                         const uint32_t* d_epoch, hipStream_t stream);
+// Penalty on logits for stamped ids (stand-alone form of the lm_head epilogue).
+int launch_penalty_apply(__half* logits, const uint32_t* stamp, const uint32_t* d_epoch, int vocab,
+                         float penalty, hipStream_t stream);
+
+// Decode-step control block in device memory.
+struct StepCtl {
+  // written by the host before a step / a chained decode (first 5 ints)
+  int token;        // input token of the next step
+  int pos;          // position of the next step
+  int history_len;  // ids in the history buffer
+  int chain;        // 1: the argmax feeds the next step (token, pos+1, history append)
+  int step;         // index into tokens_out for chained decode
+  // maintained on the device
+  int sampled;      // id sampled by the last step
+  int max_history;  // history buffer capacity
+  uint32_t epoch;   // penalty stamp epoch of the current step
+};
+
+// Argmax over fp16 logits (ties -> lowest index).  `partials` holds
+// kArgmaxBlocks uint64 keys; `ctl` (optional) receives the token and, when
+// ctl->chain, advances the step; `tokens_out` (optional) records the token at
+// ctl->step.
+constexpr int kArgmaxBlocks = 256;
+int launch_argmax(const __half* logits, int vocab, unsigned long long* partials, StepCtl* ctl,
+                  int* d_token_out, int* history, int* tokens_out, hipStream_t stream);
+
+// Step prologue: embedding of ctl->token into x, stamp the history with a new
+// epoch.
+int launch_step_begin(const __half* embed, StepCtl* ctl, const int* history, uint32_t* stamp, __half* x,
+                      int dim, int vocab, hipStream_t stream);
+
+}  // namespace cq

@@ -1,0 +1,46 @@
+"""Helpers shared by the GPU tests."""
+import numpy as np
+
+import cuqwen_amd as cq
+
+D = cq.DeviceBuffer
+
+
+def dev(a):
+    return D.from_array(np.ascontiguousarray(a))
+
+
+def dev_i32(v):
+    return D.from_array(np.array(v, dtype=np.int32).reshape(-1))
+
+
+def rel_err(got, want):
+    got = np.asarray(got, dtype=np.float64)
+    want = np.asarray(want, dtype=np.float64)
+    return float(np.max(np.abs(got - want)) / max(np.max(np.abs(want)), 1e-30))
+
+
+def k_offsets(n_kv, T, hd, max_seq):
+    """Vectorised kv_k_offset (cq_common.h) for [n_kv][T][hd]."""
+    h, t, d = np.meshgrid(np.arange(n_kv), np.arange(T), np.arange(hd), indexing="ij")
+    kk, j, e = d >> 5, (d >> 3) & 3, d & 7
+    return h * max_seq * hd + (t >> 4) * 16 * hd + ((kk * 64 + j * 16 + (t & 15)) * 8 + e)
+
+
+def v_offsets(n_kv, T, hd, max_seq):
+    h, t, d = np.meshgrid(np.arange(n_kv), np.arange(T), np.arange(hd), indexing="ij")
+    dt, dl = d >> 4, d & 15
+    t32 = t & 31
+    j = (t32 & 15) >> 2
+    e = (t32 & 3) + ((t32 >> 4) << 2)
+    return h * max_seq * hd + (t >> 5) * 32 * hd + ((dt * 64 + j * 16 + dl) * 8 + e)
+
+
+def tile_kv(K, V, max_seq):
+    """Head-major K, V [n_kv][T][hd] -> the device cache layout."""
+    n_kv, T, hd = K.shape
+    kc = np.zeros(n_kv * max_seq * hd, dtype=np.float16)
+    vc = np.zeros(n_kv * max_seq * hd, dtype=np.float16)
+    kc[k_offsets(n_kv, T, hd, max_seq).ravel()] = K.ravel()
+    vc[v_offsets(n_kv, T, hd, max_seq).ravel()] = V.ravel()
+    return kc, vc
