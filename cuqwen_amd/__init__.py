@@ -231,8 +231,14 @@ class DeviceBuffer:
     def value(self):
         return self.ptr.value
 
+    @property
+    def _as_parameter_(self):
+        return self.ptr
+
     def free(self):
         if self.ptr:
+            # kernels queued on this memory must finish before it is released
+            lib.cq_synchronize()
             lib.cq_free(self.ptr)
             self.ptr = ctypes.c_void_p()
 

@@ -6,12 +6,36 @@ import cuqwen_amd as cq
 D = cq.DeviceBuffer
 
 
-def dev(a):
-    return D.from_array(np.ascontiguousarray(a))
+class Pool:
+    """Owns every device buffer of one test until the test ends, so no
+    pointer handed to a kernel can be released while the kernel may run."""
 
+    def __init__(self):
+        self.bufs = []
 
-def dev_i32(v):
-    return D.from_array(np.array(v, dtype=np.int32).reshape(-1))
+    def put(self, a):
+        """Upload `a` (None -> NULL); returns the device pointer."""
+        if a is None:
+            return None
+        b = D.from_array(np.ascontiguousarray(a))
+        self.bufs.append(b)
+        return b.ptr
+
+    def i32(self, v):
+        return self.put(np.array(v, dtype=np.int32).reshape(-1))
+
+    def empty(self, nbytes, zero=False):
+        b = D(nbytes)
+        if zero:
+            b.zero()
+        self.bufs.append(b)
+        return b
+
+    def close(self):
+        cq.synchronize()
+        for b in self.bufs:
+            b.free()
+        self.bufs = []
 
 
 def rel_err(got, want):

@@ -2,17 +2,22 @@
 ABI.  Tolerances: bit-exact for unpacking / indexing / integer work; max
 relative error <= 1e-2 (max|y - y*| / max|y*|) for fp16-output float work
 versus the oracle's fp32 mode."""
-import math
-
 import numpy as np
 import pytest
 
 import cuqwen_amd as cq
 from oracle import oracle as orc
-from tests.gpu_util import D, dev, dev_i32, rel_err, tile_kv, k_offsets, v_offsets
+from tests.gpu_util import Pool, rel_err, tile_kv, k_offsets, v_offsets
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-2
+
+
+@pytest.fixture
+def g():
+    pool = Pool()
+    yield pool
+    pool.close()
 
 
 def _weights(quant, rows, cols, seed, group=128):
@@ -33,38 +38,36 @@ def test_layout_helpers_match_library():
 
 @pytest.mark.parametrize("quant", [1, 2])
 @pytest.mark.parametrize("group", [128, 0])
-def test_dequant_bit_exact(quant, group):
+def test_dequant_bit_exact(g, quant, group):
     """Device unpack (in-register int8/int4 -> fp16 pairs) equals q * scale
     with the exporter's layout (export_weights.py:197-199, kernels.cu:11-42)."""
     rows, cols = 67, 1024
     q, s = _weights(quant, rows, cols, 1, group)
-    # also every nibble / byte value including -8 and -128
-    if quant == 2:
-        q[0, :128] = np.arange(256, dtype=np.uint32)[:128].astype(np.uint8)
+    if quant == 2:   # every byte value, so every nibble incl. -8 in both halves
+        q[0, :128] = np.arange(128).astype(np.uint8)
         q[1, :128] = np.arange(128, 256).astype(np.uint8)
     else:
         q[0, :256] = np.arange(256).astype(np.uint8)
-    out = D(rows * cols * 4)
-    cq.check(cq.lib.cq_dequantize(quant, group, dev(q).ptr, dev(s).ptr, out.ptr, rows, cols, None))
+    out = g.empty(rows * cols * 4)
+    cq.check(cq.lib.cq_dequantize(quant, group, g.put(q), g.put(s), out.ptr, rows, cols, None))
     got = out.to_array(np.float32, (rows, cols))
     if quant == 1:
         vals = q.view(np.int8).astype(np.float32)
     else:
         nib = np.stack([q & 0xF, q >> 4], axis=-1).reshape(rows, cols).astype(np.int32)
         vals = ((nib ^ 8) - 8).astype(np.float32)
-    g = group if group else cols
-    want = vals * np.repeat(s.astype(np.float32), g, axis=1)
+    gs = group if group else cols
+    want = vals * np.repeat(s.astype(np.float32), gs, axis=1)
     assert np.array_equal(got, want)
 
 
 @pytest.mark.parametrize("quant", [0, 1, 2])
 @pytest.mark.parametrize("rows,cols", [(896, 4864), (37, 640), (1000, 3584), (5, 128)])
-def test_gemv_parity(quant, rows, cols):
+def test_gemv_parity(g, quant, rows, cols):
     W, S = _weights(quant, rows, cols, rows + cols)
     x = np.random.default_rng(7).standard_normal(cols).astype(np.float16)
-    y = D(rows * 2)
-    cq.check(cq.lib.cq_gemv(quant, 128, dev(W).ptr, dev(S).ptr if S is not None else None, dev(x).ptr, y.ptr,
-                            rows, cols, None))
+    y = g.empty(rows * 2)
+    cq.check(cq.lib.cq_gemv(quant, 128, g.put(W), g.put(S), g.put(x), y.ptr, rows, cols, None))
     got = y.to_array(np.float16)
     want = orc.gemv(quant, W, S, x, rows, cols, 128, mode=1)
     assert rel_err(got, want) <= TOL
@@ -73,19 +76,19 @@ def test_gemv_parity(quant, rows, cols):
 
 
 @pytest.mark.parametrize("quant", [1, 2])
-def test_gemv_per_row_scale_variant(quant):
+def test_gemv_per_row_scale_variant(g, quant):
     """BASELINE config 1 with one scale per row (group = K)."""
     rows, cols = 896, 4864
     W, S = _weights(quant, rows, cols, 3, group=0)
     x = np.random.default_rng(8).standard_normal(cols).astype(np.float16)
-    y = D(rows * 2)
-    cq.check(cq.lib.cq_gemv(quant, 0, dev(W).ptr, dev(S).ptr, dev(x).ptr, y.ptr, rows, cols, None))
+    y = g.empty(rows * 2)
+    cq.check(cq.lib.cq_gemv(quant, 0, g.put(W), g.put(S), g.put(x), y.ptr, rows, cols, None))
     want = orc.gemv(quant, W, S, x, rows, cols, 0, mode=1)
     assert rel_err(y.to_array(np.float16), want) <= TOL
 
 
 @pytest.mark.parametrize("quant", [0, 1, 2])
-def test_gemv_integer_inputs_bit_exact(quant):
+def test_gemv_integer_inputs_bit_exact(g, quant):
     """Integer weights, x and unit scales make every partial sum exact, so the
     output must equal the integer dot product whatever the order: this pins
     the unpack and the row/column indexing bit for bit."""
@@ -104,30 +107,29 @@ def test_gemv_integer_inputs_bit_exact(quant):
     x = rng.integers(-1, 2, cols).astype(np.float16)
     exact = qv @ x.astype(np.int64)
     assert np.max(np.abs(exact)) < 2048
-    y = D(rows * 2)
-    cq.check(cq.lib.cq_gemv(quant, 128, dev(W).ptr, dev(S).ptr if S is not None else None, dev(x).ptr, y.ptr,
-                            rows, cols, None))
+    y = g.empty(rows * 2)
+    cq.check(cq.lib.cq_gemv(quant, 128, g.put(W), g.put(S), g.put(x), y.ptr, rows, cols, None))
     assert np.array_equal(y.to_array(np.float16).astype(np.int64), exact)
 
 
 @pytest.mark.parametrize("quant", [0, 1, 2])
-def test_gemv_add_residual(quant):
+def test_gemv_add_residual(g, quant):
     """kernels.cu:640-687: x[r] = half(float(x[r]) + W[r].in)."""
     rows, cols = 896, 896
     W, S = _weights(quant, rows, cols, 11)
     rng = np.random.default_rng(12)
     inp = rng.standard_normal(cols).astype(np.float16)
     x0 = rng.standard_normal(rows).astype(np.float16)
-    xb = dev(x0)
-    cq.check(cq.lib.cq_gemv_add(quant, dev(W).ptr, dev(S).ptr if S is not None else None, dev(inp).ptr, xb.ptr,
-                                rows, cols, None))
+    xb = g.empty(rows * 2)
+    xb.upload(x0)
+    cq.check(cq.lib.cq_gemv_add(quant, g.put(W), g.put(S), g.put(inp), xb.ptr, rows, cols, None))
     want = x0.astype(np.float32) + orc.gemv(quant, W, S, inp, rows, cols, 128, mode=1)
     assert rel_err(xb.to_array(np.float16), want) <= TOL
 
 
 @pytest.mark.parametrize("quant", [0, 1, 2])
 @pytest.mark.parametrize("norm", [False, True])
-def test_mlp_stage1_swiglu(quant, norm):
+def test_mlp_stage1_swiglu(g, quant, norm):
     """kernels.cu:523-569 (+ the rmsnorm of kernels.cu:689-751 when fused)."""
     d, I = 896, 4864
     Wg, Sg = _weights(quant, I, d, 21)
@@ -135,20 +137,19 @@ def test_mlp_stage1_swiglu(quant, norm):
     rng = np.random.default_rng(23)
     x = rng.standard_normal(d).astype(np.float16)
     nw = (1 + 0.02 * rng.standard_normal(d)).astype(np.float16)
-    out = D(I * 2)
-    cq.check(cq.lib.cq_fused_mlp_stage1(quant, dev(x).ptr, dev(nw).ptr if norm else None, dev(Wg).ptr, dev(Wu).ptr,
-                                        dev(Sg).ptr if Sg is not None else None,
-                                        dev(Su).ptr if Su is not None else None, out.ptr, d, I, 1e-6, None))
+    out = g.empty(I * 2)
+    cq.check(cq.lib.cq_fused_mlp_stage1(quant, g.put(x), g.put(nw) if norm else None, g.put(Wg), g.put(Wu),
+                                        g.put(Sg), g.put(Su), out.ptr, d, I, 1e-6, None))
     xn = orc.rmsnorm(x, nw) if norm else x
-    g = orc.gemv(quant, Wg, Sg, xn, I, d, mode=1).astype(np.float64)
+    gg = orc.gemv(quant, Wg, Sg, xn, I, d, mode=1).astype(np.float64)
     u = orc.gemv(quant, Wu, Su, xn, I, d, mode=1).astype(np.float64)
-    want = g / (1 + np.exp(-g)) * u
+    want = gg / (1 + np.exp(-gg)) * u
     assert rel_err(out.to_array(np.float16), want) <= TOL
 
 
 @pytest.mark.parametrize("quant", [0, 1, 2])
 @pytest.mark.parametrize("H,KV,hd,d", [(14, 2, 64, 896), (28, 4, 128, 3584), (12, 2, 128, 1536)])
-def test_fused_attn_block_qkv_rope(quant, H, KV, hd, d):
+def test_fused_attn_block_qkv_rope(g, quant, H, KV, hd, d):
     """kernels.cu:402-519: q/k/v = half(W x + b), NeoX RoPE on q, k at *d_pos."""
     qd, kvd = H * hd, KV * hd
     Wq, Sq = _weights(quant, qd, d, 31)
@@ -158,12 +159,11 @@ def test_fused_attn_block_qkv_rope(quant, H, KV, hd, d):
     bq, bk, bv = [(0.02 * rng.standard_normal(n)).astype(np.float16) for n in (qd, kvd, kvd)]
     x = rng.standard_normal(d).astype(np.float16)
     pos = 30001
-    q, k, v = D(qd * 2), D(kvd * 2), D(kvd * 2)
-    p = lambda a: dev(a).ptr if a is not None else None   # noqa: E731
-    keep = [dev(a) for a in (x, Wq, Wk, Wv, bq, bk, bv)]
-    cq.check(cq.lib.cq_fused_attn_block(quant, keep[0].ptr, None, keep[1].ptr, keep[2].ptr, keep[3].ptr,
-                                        p(Sq), p(Sk), p(Sv), keep[4].ptr, keep[5].ptr, keep[6].ptr,
-                                        q.ptr, k.ptr, v.ptr, d, H, KV, hd, dev_i32(pos).ptr, 1e6, 1e-6, None))
+    q, k, v = g.empty(qd * 2), g.empty(kvd * 2), g.empty(kvd * 2)
+    cq.check(cq.lib.cq_fused_attn_block(quant, g.put(x), None, g.put(Wq), g.put(Wk), g.put(Wv),
+                                        g.put(Sq), g.put(Sk), g.put(Sv), g.put(bq), g.put(bk), g.put(bv),
+                                        q.ptr, k.ptr, v.ptr, d, H, KV, hd, g.i32(pos), 1e6, 1e-6, None))
+
     def proj(W, S, b, rows):
         return (orc.gemv(quant, W, S, x, rows, d, mode=1) + b.astype(np.float32)).astype(np.float16)
     wq, wk, wv = proj(Wq, Sq, bq, qd), proj(Wk, Sk, bk, kvd), proj(Wv, Sv, bv, kvd)
@@ -173,36 +173,35 @@ def test_fused_attn_block_qkv_rope(quant, H, KV, hd, d):
 
 
 @pytest.mark.parametrize("lmq", [0, 1])
-def test_compute_logits(lmq):
+def test_compute_logits(g, lmq):
     V, d = 151936, 896
     W, S = _weights(lmq, V, d, 41)
     x = np.random.default_rng(42).standard_normal(d).astype(np.float16)
-    out = D(V * 2)
-    cq.check(cq.lib.cq_compute_logits(lmq, dev(x).ptr, dev(W).ptr, dev(S).ptr if S is not None else None, out.ptr,
-                                      V, d, None))
+    out = g.empty(V * 2)
+    cq.check(cq.lib.cq_compute_logits(lmq, g.put(x), g.put(W), g.put(S), out.ptr, V, d, None))
     assert rel_err(out.to_array(np.float16), orc.gemv(lmq, W, S, x, V, d, mode=1)) <= TOL
 
 
-def test_rmsnorm_and_embedding():
+def test_rmsnorm_and_embedding(g):
     rng = np.random.default_rng(51)
     d = 3584
     x = rng.standard_normal(d).astype(np.float16)
     w = (1 + 0.02 * rng.standard_normal(d)).astype(np.float16)
-    out = D(d * 2)
-    cq.check(cq.lib.cq_rmsnorm(dev(x).ptr, dev(w).ptr, out.ptr, d, 1e-6, None))
+    out = g.empty(d * 2)
+    cq.check(cq.lib.cq_rmsnorm(g.put(x), g.put(w), out.ptr, d, 1e-6, None))
     assert rel_err(out.to_array(np.float16), orc.rmsnorm(x, w, mode=1)) <= TOL
     table = rng.standard_normal((100, d)).astype(np.float16)
-    cq.check(cq.lib.cq_embedding_lookup(dev(table).ptr, dev_i32(77).ptr, out.ptr, d, None))
+    cq.check(cq.lib.cq_embedding_lookup(g.put(table), g.i32(77), out.ptr, d, None))
     assert np.array_equal(out.to_array(np.float16), table[77])
 
 
-def test_kv_cache_store_layout():
+def test_kv_cache_store_layout(g):
     KV, hd, ms, pos = 4, 128, 256, 77
     rng = np.random.default_rng(61)
     k = rng.standard_normal(KV * hd).astype(np.float16)
     v = rng.standard_normal(KV * hd).astype(np.float16)
-    kc, vc = D(KV * ms * hd * 2).zero(), D(KV * ms * hd * 2).zero()
-    cq.check(cq.lib.cq_kv_cache_store(dev(k).ptr, dev(v).ptr, kc.ptr, vc.ptr, dev_i32(pos).ptr, KV, ms, hd, None))
+    kc, vc = g.empty(KV * ms * hd * 2, zero=True), g.empty(KV * ms * hd * 2, zero=True)
+    cq.check(cq.lib.cq_kv_cache_store(g.put(k), g.put(v), kc.ptr, vc.ptr, g.i32(pos), KV, ms, hd, None))
     K = kc.to_array(np.float16)[k_offsets(KV, ms, hd, ms)]
     Vv = vc.to_array(np.float16)[v_offsets(KV, ms, hd, ms)]
     assert np.array_equal(K[:, pos], k.reshape(KV, hd)) and np.array_equal(Vv[:, pos], v.reshape(KV, hd))
@@ -213,7 +212,7 @@ def test_kv_cache_store_layout():
 
 @pytest.mark.parametrize("H,KV,hd", [(14, 2, 64), (28, 4, 128), (12, 2, 128), (40, 8, 128), (16, 2, 128)])
 @pytest.mark.parametrize("T", [1, 2, 31, 32, 33, 257, 1000, 4096, 9000])
-def test_attention_parity(H, KV, hd, T):
+def test_attention_parity(g, H, KV, hd, T):
     """FlashDecoding split-K GQA (kernels.cu:105-324) vs softmax(qK^T/sqrt(hd))V."""
     ms = ((T + 31) // 32) * 32 + 64
     rng = np.random.default_rng(T * 7 + H)
@@ -221,19 +220,19 @@ def test_attention_parity(H, KV, hd, T):
     K = rng.standard_normal((KV, T, hd)).astype(np.float16)
     Vv = rng.standard_normal((KV, T, hd)).astype(np.float16)
     kc, vc = tile_kv(K, Vv, ms)
-    # garbage beyond T must not leak into the result
-    kcd, vcd = dev(kc), dev(vc)
-    ws = D(cq.lib.cq_attention_workspace_bytes(H, KV, hd)).zero()
-    out = D(H * hd * 2)
-    for _ in range(2):   # second call checks the self-resetting merge tickets
-        cq.check(cq.lib.cq_gqa_attention_decode(dev(q).ptr, kcd.ptr, vcd.ptr, out.ptr, dev_i32(T - 1).ptr, H, KV, hd,
-                                                ms, ws.ptr, None))
+    pk, pv, pq, pp = g.put(kc), g.put(vc), g.put(q), g.i32(T - 1)
+    ws = g.empty(cq.lib.cq_attention_workspace_bytes(H, KV, hd), zero=True)
+    out = g.empty(H * hd * 2)
+    want1 = orc.attention(q, K, Vv, H, KV, hd, T, mode=1)
+    want0 = orc.attention(q, K, Vv, H, KV, hd, T, mode=0)
+    for _ in range(2):   # the second call checks the self-resetting merge tickets
+        cq.check(cq.lib.cq_gqa_attention_decode(pq, pk, pv, out.ptr, pp, H, KV, hd, ms, ws.ptr, None))
         got = out.to_array(np.float16)
-        assert rel_err(got, orc.attention(q, K, Vv, H, KV, hd, T, mode=1)) <= TOL
-        assert rel_err(got, orc.attention(q, K, Vv, H, KV, hd, T, mode=0)) <= TOL
+        assert rel_err(got, want1) <= TOL
+        assert rel_err(got, want0) <= TOL
 
 
-def test_attention_ignores_stale_cache_tail():
+def test_attention_ignores_stale_cache_tail(g):
     H, KV, hd, T, ms = 14, 2, 64, 45, 128
     rng = np.random.default_rng(5)
     q = rng.standard_normal(H * hd).astype(np.float16)
@@ -242,32 +241,33 @@ def test_attention_ignores_stale_cache_tail():
     Vv[:, T:] = np.inf
     K[:, T:] = np.nan
     kc, vc = tile_kv(K, Vv, ms)
-    ws = D(cq.lib.cq_attention_workspace_bytes(H, KV, hd)).zero()
-    out = D(H * hd * 2)
-    cq.check(cq.lib.cq_gqa_attention_decode(dev(q).ptr, dev(kc).ptr, dev(vc).ptr, out.ptr, dev_i32(T - 1).ptr, H, KV,
-                                            hd, ms, ws.ptr, None))
+    ws = g.empty(cq.lib.cq_attention_workspace_bytes(H, KV, hd), zero=True)
+    out = g.empty(H * hd * 2)
+    cq.check(cq.lib.cq_gqa_attention_decode(g.put(q), g.put(kc), g.put(vc), out.ptr, g.i32(T - 1), H, KV, hd, ms,
+                                            ws.ptr, None))
     got = out.to_array(np.float16)
     assert np.all(np.isfinite(got))
     assert rel_err(got, orc.attention(q, K[:, :T], Vv[:, :T], H, KV, hd, T, mode=1)) <= TOL
 
 
-def test_argmax_and_penalty():
+def test_argmax_and_penalty(g):
     V = 152064
     rng = np.random.default_rng(71)
     l = rng.standard_normal(V).astype(np.float16)
     l[[5, 100000, 152000]] = 9.0     # ties -> lowest index
-    ws = D(cq.lib.cq_argmax_workspace_bytes(V)).zero()
-    tok = D(4)
-    ld = dev(l)
+    ws = g.empty(cq.lib.cq_argmax_workspace_bytes(V), zero=True)
+    tok = g.empty(4)
+    ld = g.empty(V * 2)
+    ld.upload(l)
     for _ in range(2):
         cq.check(cq.lib.cq_argmax(ld.ptr, tok.ptr, V, ws.ptr, None))
         assert tok.to_array(np.int32)[0] == orc.argmax(l) == 5
     l2 = l.copy()
     l2[77] = np.nan
-    cq.check(cq.lib.cq_argmax(dev(l2).ptr, tok.ptr, V, ws.ptr, None))
+    cq.check(cq.lib.cq_argmax(g.put(l2), tok.ptr, V, ws.ptr, None))
     assert tok.to_array(np.int32)[0] == 77
     hist = np.array([5, 5, 100000, 3, -1, V + 5, 5], dtype=np.int32)
-    pws = D(cq.lib.cq_penalty_workspace_bytes(V)).zero()
-    cq.check(cq.lib.cq_apply_repetition_penalty(ld.ptr, dev(hist).ptr, dev_i32(hist.size).ptr, V, 1.1, pws.ptr, None))
+    pws = g.empty(cq.lib.cq_penalty_workspace_bytes(V), zero=True)
+    cq.check(cq.lib.cq_apply_repetition_penalty(ld.ptr, g.put(hist), g.i32(hist.size), V, 1.1, pws.ptr, None))
     got = ld.to_array(np.float16)
     assert np.array_equal(got.view(np.uint16), orc.penalty(l, hist).view(np.uint16))
