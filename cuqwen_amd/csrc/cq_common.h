@@ -36,7 +36,38 @@ int fail(int code, const std::string& msg);
 namespace cq {
 
 // ------------------------------------------------------- fp16 bit helpers
-CQ_HD uint16_t f2h_bits(float f) { return __half_as_ushort(__float2half_rn(f)); }
+CQ_HD uint32_t float_bits(float f) {
+#ifdef __HIP_DEVICE_COMPILE__
+  return __float_as_uint(f);
+#else
+  uint32_t u;
+  __builtin_memcpy(&u, &f, 4);
+  return u;
+#endif
+}
+// float -> IEEE binary16, round to nearest even, in integer arithmetic only,
+// so the generator and the quantizer give the same bits on host and device
+// whatever the hardware's fp16 denormal mode.
+CQ_HD uint16_t f2h_bits(float f) {
+  const uint32_t x = float_bits(f);
+  const uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
+  const uint32_t ax = x & 0x7FFFFFFFu;
+  if (ax >= 0x7F800000u) return sign | (ax > 0x7F800000u ? 0x7E00u : 0x7C00u);
+  if (ax >= 0x477FF000u) return sign | 0x7C00u;            // rounds to >= 65520: inf
+  if (ax >= 0x38800000u) {                                 // normal fp16
+    uint32_t h = (((ax >> 23) - 112u) << 10) | ((ax & 0x7FFFFFu) >> 13);
+    const uint32_t rem = ax & 0x1FFFu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) ++h;
+    return (uint16_t)(sign | h);
+  }
+  if (ax <= 0x33000000u) return sign;                      // <= 2^-25: rounds to zero
+  const uint32_t e = ax >> 23, m = (ax & 0x7FFFFFu) | 0x800000u;
+  const uint32_t shift = 126u - e;                         // 14..24: units of 2^-24
+  uint32_t q = m >> shift;
+  const uint32_t rem = m & ((1u << shift) - 1u), half = 1u << (shift - 1u);
+  if (rem > half || (rem == half && (q & 1u))) ++q;
+  return (uint16_t)(sign | q);
+}
 CQ_HD float h2f_bits(uint16_t h) { return __half2float(__ushort_as_half(h)); }
 
 // -------------------------------------------------- synthetic generator
