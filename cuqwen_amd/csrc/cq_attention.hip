@@ -2,21 +2,24 @@
 //
 // Reference: gqa_attention_wmma_ksplit_stage1_kernel + stage2
 // (src/kernels.cu:105-324).  Design here:
-//   * grid = (partitions, kv heads); a partition is a run of 32-key tiles,
-//     sized at run time from *d_pos so one recorded graph serves every
+//   * stage 1: grid = (partitions, kv heads); a partition is a run of 32-key
+//     tiles, sized at run time from *d_pos so one recorded graph serves every
 //     position; blocks past the last partition exit at once;
-//   * 8 waves per block, each wave takes every 8th tile of the partition and
-//     keeps an online softmax (running max / sum) and its O accumulator in
-//     matrix-core registers;
+//   * 8 waves per block, each wave takes every 8th tile of the partition,
+//     double-buffered in registers (the next tile's K and V are in flight
+//     while the current one is computed), and keeps an online softmax
+//     (running max / sum) and its O accumulator in matrix-core registers;
 //   * S^T = K Q^T with v_mfma_f32_16x16x32_f16 (keys as rows, the group's
 //     query heads as columns, padded to 16), then O^T += V^T P^T with the
 //     same instruction.  The K and V tiles are stored in the cache in exactly
 //     the operand order the instruction consumes (cq_common.h), so every
 //     tile is streamed with contiguous 16-byte-per-lane loads and the score
 //     tile feeds the P^T operand without any cross-lane movement;
-//   * the 8 waves merge in LDS, write one (m, l, O) partial per partition,
-//     and the last block of each kv head (atomic ticket) performs the
-//     log-sum-exp merge (kernels.cu:222-288) and resets its ticket.
+//   * the 8 waves merge in LDS and the block writes one (m, l, O) partial
+//     (or, with a single partition, the output itself);
+//   * stage 2: one block per query head merges the partials with the
+//     log-sum-exp rule (kernels.cu:222-288).  A separate launch is cheaper on
+//     this part than an in-kernel completion ticket plus device-scope fences.
 // Rounding follows the reference: scores are rounded to fp16 after the
 // 1/sqrt(hd) scale (kernels.cu:171), probabilities are rounded to fp16 for
 // the PV product while the row sum uses the unrounded values (:185-186).
@@ -35,17 +38,100 @@ constexpr int kTileKeys = 32;
 
 int attention_max_parts(int n_kv) { return (kAttnBlocksTarget + n_kv - 1) / n_kv; }
 
-// Workspace: [64 counters (256 B)] [m: n_kv*P*16] [l: n_kv*P*16] [o: n_kv*P*16*hd] floats.
+// Workspace: [m: n_kv*P*16] [l: n_kv*P*16] [o: n_kv*P*16*hd] floats.
 size_t attention_workspace_bytes(int n_heads, int n_kv, int head_dim) {
   (void)n_heads;
   const size_t P = (size_t)attention_max_parts(n_kv);
-  return 256 + (size_t)n_kv * P * 16 * (2 + (size_t)head_dim) * sizeof(float);
+  return (size_t)n_kv * P * 16 * (2 + (size_t)head_dim) * sizeof(float);
 }
 
 template <int HD>
-__global__ __launch_bounds__(kAttnThreads) void attention_kernel(const AttnArgs a, unsigned* counters) {
-  constexpr int KK = HD / 32;   // mfma k-steps over head_dim for S^T
-  constexpr int DT = HD / 16;   // 16-row d tiles of O^T
+struct KVTile {
+  h8_t ka[2][HD / 32];
+  h8_t va[HD / 16];
+};
+
+template <int HD>
+__device__ __forceinline__ void load_tile(KVTile<HD>& t, const _Float16* kbase, const _Float16* vbase, int ti,
+                                          int lane) {
+  const _Float16* kt = kbase + (int64_t)ti * kTileKeys * HD;
+  const _Float16* vt = vbase + (int64_t)ti * kTileKeys * HD;
+#pragma unroll
+  for (int st = 0; st < 2; ++st)
+#pragma unroll
+    for (int kk = 0; kk < HD / 32; ++kk)
+      t.ka[st][kk] = __builtin_bit_cast(h8_t, load_u4(kt + st * 16 * HD + (kk * 64 + lane) * 8));
+#pragma unroll
+  for (int dt = 0; dt < HD / 16; ++dt) t.va[dt] = __builtin_bit_cast(h8_t, load_u4(vt + (dt * 64 + lane) * 8));
+}
+
+// One 32-key tile of the online softmax for this wave.
+template <int HD>
+__device__ __forceinline__ void attend_tile(KVTile<HD>& t, const h8_t* qb, int ti, int T, float scale, int j,
+                                            float& m, float& l, f4_t* o) {
+  constexpr int KK = HD / 32, DT = HD / 16;
+  f4_t s[2];
+#pragma unroll
+  for (int st = 0; st < 2; ++st) {
+    s[st] = f4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) s[st] = __builtin_amdgcn_mfma_f32_16x16x32_f16(t.ka[st][kk], qb[kk], s[st], 0, 0, 0);
+  }
+  // lane holds S^T[key = ti*32 + st*16 + 4j + i][head]
+  const int key0 = ti * kTileKeys + 4 * j;
+  const bool tail = (ti + 1) * kTileKeys > T;
+  float sv[8];
+  float mt = -INFINITY;
+#pragma unroll
+  for (int st = 0; st < 2; ++st)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float v = (float)(_Float16)(s[st][i] * scale);
+      if (tail && key0 + st * 16 + i >= T) v = -INFINITY;
+      sv[st * 4 + i] = v;
+      mt = fmaxf(mt, v);
+    }
+  mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
+  mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
+  const float mn = fmaxf(m, mt);
+  const float alpha = __expf(m - mn);
+  m = mn;
+  l *= alpha;
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
+  h8_t pb;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float p = __expf(sv[e] - mn);
+    l += p;
+    pb[e] = (_Float16)p;
+  }
+  if (tail) {
+    // keys past the end may hold anything; keep them out of P*V
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int key = ti * kTileKeys + (e < 4 ? 4 * j + e : 16 + 4 * j + e - 4);
+        if (key >= T) t.va[dt][e] = (_Float16)0.f;
+      }
+  }
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(t.va[dt], pb, o[dt], 0, 0, 0);
+}
+
+__device__ __forceinline__ int attn_nparts(int T, int P, int* tpp_out) {
+  const int n_tiles = (T + kTileKeys - 1) / kTileKeys;
+  int tpp = (n_tiles + P - 1) / P;
+  if (tpp < kMinTilesPerPart) tpp = kMinTilesPerPart;
+  *tpp_out = tpp;
+  return (n_tiles + tpp - 1) / tpp;
+}
+
+template <int HD>
+__global__ __launch_bounds__(kAttnThreads) void attention_stage1(const AttnArgs a) {
+  constexpr int KK = HD / 32;
+  constexpr int DT = HD / 16;
   const int kvh = blockIdx.y;
   const int part = blockIdx.x;
   const int lane = threadIdx.x & (kWave - 1);
@@ -53,10 +139,8 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const AttnArgs 
   const int g = a.n_heads / a.n_kv;
   const int T = *a.d_pos + 1;
   const int n_tiles = (T + kTileKeys - 1) / kTileKeys;
-  const int P = gridDim.x;
-  int tpp = (n_tiles + P - 1) / P;
-  if (tpp < kMinTilesPerPart) tpp = kMinTilesPerPart;
-  const int nparts = (n_tiles + tpp - 1) / tpp;
+  int tpp;
+  const int nparts = attn_nparts(T, gridDim.x, &tpp);
   if (part >= nparts) return;
   const int tile0 = part * tpp;
   const int tile1 = min(tile0 + tpp, n_tiles);
@@ -64,6 +148,13 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const AttnArgs 
   const int h = lane & 15;        // query head column of this lane
   const int j = lane >> 4;        // k-slot group of this lane
   const float scale = 1.0f / sqrtf((float)HD);
+
+  const _Float16* kbase = reinterpret_cast<const _Float16*>(a.kcache) + (int64_t)kvh * a.max_seq * HD;
+  const _Float16* vbase = reinterpret_cast<const _Float16*>(a.vcache) + (int64_t)kvh * a.max_seq * HD;
+
+  KVTile<HD> A, B;
+  int ti = tile0 + wave;
+  if (ti < tile1) load_tile<HD>(A, kbase, vbase, ti, lane);
 
   // Q^T as the B operand: lane holds q[h][kk*32 + j*8 .. +8]
   h8_t qb[KK];
@@ -76,76 +167,18 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const AttnArgs 
     }
   }
 
-  const _Float16* kbase = reinterpret_cast<const _Float16*>(a.kcache) + (int64_t)kvh * a.max_seq * HD;
-  const _Float16* vbase = reinterpret_cast<const _Float16*>(a.vcache) + (int64_t)kvh * a.max_seq * HD;
-
   float m = -INFINITY, l = 0.f;
   f4_t o[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) o[dt] = f4_t{0.f, 0.f, 0.f, 0.f};
 
-  for (int ti = tile0 + wave; ti < tile1; ti += kAttnWaves) {
-    const _Float16* kt = kbase + (int64_t)ti * kTileKeys * HD;
-    const _Float16* vt = vbase + (int64_t)ti * kTileKeys * HD;
-    h8_t ka[2][KK];
-    h8_t va[DT];
-#pragma unroll
-    for (int st = 0; st < 2; ++st)
-#pragma unroll
-      for (int kk = 0; kk < KK; ++kk)
-        ka[st][kk] = __builtin_bit_cast(h8_t, load_u4(kt + st * 16 * HD + (kk * 64 + lane) * 8));
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) va[dt] = __builtin_bit_cast(h8_t, load_u4(vt + (dt * 64 + lane) * 8));
-
-    f4_t s[2];
-#pragma unroll
-    for (int st = 0; st < 2; ++st) {
-      s[st] = f4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kk = 0; kk < KK; ++kk)
-        s[st] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[st][kk], qb[kk], s[st], 0, 0, 0);
-    }
-    // lane holds S^T[key = ti*32 + st*16 + 4j + i][head h]
-    const int key0 = ti * kTileKeys + 4 * j;
-    const bool tail = (ti + 1) * kTileKeys > T;
-    float sv[8];
-    float mt = -INFINITY;
-#pragma unroll
-    for (int st = 0; st < 2; ++st)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float v = (float)(_Float16)(s[st][i] * scale);
-        if (tail && key0 + st * 16 + i >= T) v = -INFINITY;
-        sv[st * 4 + i] = v;
-        mt = fmaxf(mt, v);
-      }
-    mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
-    mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
-    const float mn = fmaxf(m, mt);
-    const float alpha = __expf(m - mn);
-    m = mn;
-    l *= alpha;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
-    h8_t pb;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float p = __expf(sv[e] - mn);
-      l += p;
-      pb[e] = (_Float16)p;
-    }
-    if (tail) {
-      // keys past the end may hold anything; keep them out of P*V
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int key = ti * kTileKeys + (e < 4 ? 4 * j + e : 16 + 4 * j + e - 4);
-          if (key >= T) va[dt][e] = (_Float16)0.f;
-        }
-    }
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[dt], pb, o[dt], 0, 0, 0);
+  for (; ti < tile1; ti += 2 * kAttnWaves) {
+    const int t1 = ti + kAttnWaves;
+    if (t1 < tile1) load_tile<HD>(B, kbase, vbase, t1, lane);
+    attend_tile<HD>(A, qb, ti, T, scale, j, m, l, o);
+    if (t1 >= tile1) break;
+    if (t1 + kAttnWaves < tile1) load_tile<HD>(A, kbase, vbase, t1 + kAttnWaves, lane);
+    attend_tile<HD>(B, qb, t1, T, scale, j, m, l, o);
   }
   l += __shfl_xor(l, 16, kWave);
   l += __shfl_xor(l, 32, kWave);
@@ -160,19 +193,20 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const AttnArgs 
     for (int i = 0; i < 4; ++i) wo[wave][h][dt * 16 + 4 * j + i] = o[dt][i];
   __syncthreads();
 
-  float* ws_m = reinterpret_cast<float*>(reinterpret_cast<char*>(a.workspace) + 256);
+  float* ws_m = reinterpret_cast<float*>(a.workspace);
   const int Pmax = gridDim.x;
   float* ws_l = ws_m + (size_t)a.n_kv * Pmax * 16;
   float* ws_o = ws_l + (size_t)a.n_kv * Pmax * 16;
   const size_t pslot = (size_t)kvh * Pmax + part;
   _Float16* out = reinterpret_cast<_Float16*>(a.out);
 
-  // block-level (m, l) per head, then O
   for (int idx = threadIdx.x; idx < g * HD; idx += kAttnThreads) {
     const int hh = idx / HD, d = idx % HD;
     float M = -INFINITY;
+#pragma unroll
     for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, wm[w][hh]);
     float L = 0.f, O = 0.f;
+#pragma unroll
     for (int w = 0; w < kAttnWaves; ++w) {
       const float f = wm[w][hh] == -INFINITY ? 0.f : __expf(wm[w][hh] - M);
       L += wl[w][hh] * f;
@@ -185,39 +219,57 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const AttnArgs 
       if (d == 0) { ws_m[pslot * 16 + hh] = M; ws_l[pslot * 16 + hh] = L; }
     }
   }
-  if (nparts == 1) return;
+}
 
-  // ---- last block of this kv head merges all partitions
-  __shared__ unsigned ticket;
-  __threadfence();
+// One block per query head: log-sum-exp merge of the partitions
+// (kernels.cu:222-288) with 1/(L + 1e-9).
+constexpr int kMergeThreads = 256;
+template <int HD>
+__global__ __launch_bounds__(kMergeThreads) void attention_stage2(const AttnArgs a, int Pmax) {
+  const int T = *a.d_pos + 1;
+  int tpp;
+  const int nparts = attn_nparts(T, Pmax, &tpp);
+  if (nparts == 1) return;   // stage 1 wrote the output
+  const int hq = blockIdx.x;
+  const int g = a.n_heads / a.n_kv;
+  const int kvh = hq / g, hh = hq % g;
+  const float* ws_m = reinterpret_cast<const float*>(a.workspace);
+  const float* ws_l = ws_m + (size_t)a.n_kv * Pmax * 16;
+  const float* ws_o = ws_l + (size_t)a.n_kv * Pmax * 16;
+  __shared__ float pw[kAttnBlocksTarget];
+  __shared__ float red[16];
+  __shared__ float part_o[kMergeThreads / HD][HD];
+  // global max and weights (nparts <= Pmax <= 256 = blockDim)
+  const int p = threadIdx.x;
+  const float mp = p < nparts ? ws_m[((size_t)kvh * Pmax + p) * 16 + hh] : -INFINITY;
+  float M = wave_max(mp);
+  if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = M;
   __syncthreads();
-  if (threadIdx.x == 0) ticket = atomicAdd(&counters[kvh], 1u);
+  M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float wgt = p < nparts ? __expf(mp - M) : 0.f;
+  if (p < kAttnBlocksTarget) pw[p] = wgt;
+  const float lw = p < nparts ? ws_l[((size_t)kvh * Pmax + p) * 16 + hh] * wgt : 0.f;
   __syncthreads();
-  if (ticket != (unsigned)(nparts - 1)) return;
-  __threadfence();
-
-  __shared__ float pw[16][kAttnBlocksTarget];   // per-head partition weights
-  __shared__ float pinv[16];
-  for (int idx = threadIdx.x; idx < g; idx += kAttnThreads) {
-    float M = -INFINITY;
-    for (int p = 0; p < nparts; ++p) M = fmaxf(M, ws_m[((size_t)kvh * Pmax + p) * 16 + idx]);
-    float L = 0.f;
-    for (int p = 0; p < nparts; ++p) {
-      const size_t sl = ((size_t)kvh * Pmax + p) * 16 + idx;
-      const float f = __expf(ws_m[sl] - M);
-      pw[idx][p] = f;
-      L += ws_l[sl] * f;
-    }
-    pinv[idx] = 1.0f / (L + 1e-9f);
+  const float L = block_sum(lw, red);
+  // O: thread (pg, d) sums partitions pg, pg + PG, ...
+  constexpr int PG = kMergeThreads / HD;
+  const int d = threadIdx.x % HD, pg = threadIdx.x / HD;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  int q = pg;
+  for (; q + 3 * PG < nparts; q += 4 * PG) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      acc[u] += ws_o[(((size_t)kvh * Pmax + q + u * PG) * 16 + hh) * HD + d] * pw[q + u * PG];
   }
+  for (; q < nparts; q += PG) acc[0] += ws_o[(((size_t)kvh * Pmax + q) * 16 + hh) * HD + d] * pw[q];
+  part_o[pg][d] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
   __syncthreads();
-  for (int idx = threadIdx.x; idx < g * HD; idx += kAttnThreads) {
-    const int hh = idx / HD, d = idx % HD;
+  if (pg == 0) {
     float O = 0.f;
-    for (int p = 0; p < nparts; ++p) O += ws_o[(((size_t)kvh * Pmax + p) * 16 + hh) * HD + d] * pw[hh][p];
-    out[(int64_t)(kvh * g + hh) * HD + d] = (_Float16)(O * pinv[hh]);
+#pragma unroll
+    for (int i = 0; i < PG; ++i) O += part_o[i][d];
+    reinterpret_cast<_Float16*>(a.out)[(int64_t)hq * HD + d] = (_Float16)(O * (1.0f / (L + 1e-9f)));
   }
-  if (threadIdx.x == 0) counters[kvh] = 0u;
 }
 
 int launch_attention(const AttnArgs& a, hipStream_t stream) {
@@ -227,12 +279,15 @@ int launch_attention(const AttnArgs& a, hipStream_t stream) {
   if (a.max_seq <= 0 || a.max_seq % kTileKeys) return fail(CQ_EINVAL, "attention: max_seq_len must be a multiple of 32");
   if (!a.q || !a.kcache || !a.vcache || !a.out || !a.d_pos || !a.workspace)
     return fail(CQ_EINVAL, "attention: null pointer");
-  const dim3 grid(attention_max_parts(a.n_kv), a.n_kv);
-  unsigned* counters = reinterpret_cast<unsigned*>(a.workspace);
-  if (a.head_dim == 128)
-    hipLaunchKernelGGL(attention_kernel<128>, grid, dim3(kAttnThreads), 0, stream, a, counters);
-  else
-    hipLaunchKernelGGL(attention_kernel<64>, grid, dim3(kAttnThreads), 0, stream, a, counters);
+  const int P = attention_max_parts(a.n_kv);
+  const dim3 grid(P, a.n_kv);
+  if (a.head_dim == 128) {
+    hipLaunchKernelGGL(attention_stage1<128>, grid, dim3(kAttnThreads), 0, stream, a);
+    hipLaunchKernelGGL(attention_stage2<128>, dim3(a.n_heads), dim3(kMergeThreads), 0, stream, a, P);
+  } else {
+    hipLaunchKernelGGL(attention_stage1<64>, grid, dim3(kAttnThreads), 0, stream, a);
+    hipLaunchKernelGGL(attention_stage2<64>, dim3(a.n_heads), dim3(kMergeThreads), 0, stream, a, P);
+  }
   CQ_HIP(hipGetLastError());
   return CQ_OK;
 }

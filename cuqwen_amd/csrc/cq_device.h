@@ -26,24 +26,39 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
 // Int4 (export_weights.py:197-199): byte k of a 32-bit word holds element 2k
 // in its low nibble and 2k+1 in its high nibble; the nibble is a 4-bit two's
 // complement value q in [-8, 7] (kernels.cu:35-37 sign-extends ((n^8)-8)).
-// After w ^= 0x88888888 each nibble is n' = q + 8 in [0, 15], and
-// (w' >> 4i) & 0x000F000F | 0x64006400 is the fp16 pair
-// (1024 + n'_{i}, 1024 + n'_{i+4}) -- exact, since fp16 spacing is 1 on
-// [1024, 2048).  So the word's 8 weights become 4 fp16 pairs holding
-// elements (0,4) (1,5) (2,6) (3,7), each equal to 1032 + q.
+// After w ^= 0x88888888 each nibble is n = q + 8 in [0, 15].  OR-ing the
+// fp16 exponent pattern 0x6400 (1024.0; fp16 spacing is 1 on [1024, 2048))
+// onto a nibble left where it is gives an exact fp16:
+//   (w' & 0x000F000F) | 0x64006400        -> (1024 + n0, 1024 + n4)
+//   (w' & 0x00F000F0) | 0x64006400        -> (1024 + 16 n1, 1024 + 16 n5)
+//   ((w' >> 8) & 0x000F000F) | 0x64006400 -> (1024 + n2, 1024 + n6)
+//   ((w' >> 8) & 0x00F000F0) | 0x64006400 -> (1024 + 16 n3, 1024 + 16 n7)
+// The staged x plane pairs each with (x0, x4), (x1/16, x5/16), (x2, x6),
+// (x3/16, x7/16), so that (1024 + n) x = q x + 1032 x and
+// (1024 + 16 n) x / 16 = q x + 72 x: one shift, four and-or and four dot2 per
+// eight weights; the 1032 / 72 terms are removed once per chunk.
 constexpr uint32_t kInt4Flip = 0x88888888u;
-constexpr float kInt4Bias = 1032.0f;
-__device__ __forceinline__ uint32_t int4_pair(uint32_t flipped, int i) {
-  return ((flipped >> (4 * i)) & 0x000F000Fu) | 0x64006400u;
-}
+constexpr float kInt4BiasLo = 1032.0f;
+constexpr float kInt4BiasHi = 72.0f;
 // Int8: byte b of a word is q in [-128, 127]; u = q ^ 0x80 = q + 128 and the
 // fp16 with bits 0x64uu is 1024 + u = 1152 + q.  v_perm_b32 builds the pair
 // (byte 2i, byte 2i+1) with 0x64 high bytes in one instruction.
 constexpr uint32_t kInt8Flip = 0x80808080u;
 constexpr float kInt8Bias = 1152.0f;
-__device__ __forceinline__ uint32_t int8_pair(uint32_t flipped, int i) {
+
+// A constant held in a VGPR: gfx9 VOP3 instructions read at most one scalar
+// operand, so v_and_or_b32 / v_perm_b32 with two constants would otherwise
+// be split into two instructions.
+__device__ __forceinline__ uint32_t vgpr_const(uint32_t c) {
+  uint32_t v;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(v) : "s"(c));
+  return v;
+}
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask_v, uint32_t c) { return (a & mask_v) | c; }
+
+__device__ __forceinline__ uint32_t int8_pair(uint32_t flipped, uint32_t magic_v, int i) {
   // selector bytes 0-3 pick bytes of src1 (flipped), 4-7 bytes of src0.
-  return __builtin_amdgcn_perm(0x64646464u, flipped, i == 0 ? 0x04010400u : 0x04030402u);
+  return __builtin_amdgcn_perm(magic_v, flipped, i == 0 ? 0x04010400u : 0x04030402u);
 }
 
 // ------------------------------------------------------------- reductions

@@ -6,58 +6,105 @@
 
 namespace cq {
 
-constexpr int kBlock = 256;
-constexpr int kWavesPerBlock = kBlock / kWave;
-constexpr int kUnroll = 2;       // 16-byte chunks per lane in flight per row
-constexpr int kMaxGemvBlocks = 2048;
+constexpr int kNumCUs = 256;   // MI355X
 
 template <int Q> __device__ __forceinline__ constexpr bool quantized() { return Q != CQ_QUANT_FP16; }
 
-// Stage x (optionally RMS-normalised) into LDS as PLANES planes of 16-byte
-// chunk slices, plus the per-chunk sum of x for the unpack bias.
+// x staging.  Each thread owns chunks c = tid + i*BLK (i < XB) of a
+// batch; all of a batch's x (and norm-weight) loads are issued at once, so
+// the prologue costs one memory round trip per batch (one batch whenever the
+// RMSNorm is fused: K <= 16384).  The LDS image is PLANES planes of 16-byte
+// chunk slices (bank-conflict-free 16-byte reads in the main loop) plus the
+// per-chunk sum of x for the unpack bias.
 template <int Q, bool NORM>
-__device__ __forceinline__ void stage_x(const GemvArgs& a, u4_t* xs, float* sx, float* red) {
+struct XStage {
+  static constexpr int P = QTraits<Q>::PLANES;
+  static constexpr int XB = 8 / P;   // chunks per thread per batch (64 elements)
+  u4_t x[XB][P];
+  u4_t w[NORM ? XB : 1][P];
+};
+
+template <int Q, bool NORM, int BLK>
+__device__ __forceinline__ void stage_issue(const GemvArgs& a, XStage<Q, NORM>& st, int batch, int NC) {
   using T = QTraits<Q>;
-  const int K = a.K, NC = K / T::EPC;
   const _Float16* x = reinterpret_cast<const _Float16*>(a.x);
   const _Float16* nw = reinterpret_cast<const _Float16*>(a.norm_w);
+#pragma unroll
+  for (int i = 0; i < XStage<Q, NORM>::XB; ++i) {
+    const int c = (batch * XStage<Q, NORM>::XB + i) * BLK + threadIdx.x;
+    if (c < NC) {
+#pragma unroll
+      for (int p = 0; p < T::PLANES; ++p) {
+        st.x[i][p] = load_u4(x + c * T::EPC + p * 8);
+        if constexpr (NORM) st.w[i][p] = load_u4(nw + c * T::EPC + p * 8);
+      }
+    }
+  }
+}
+
+template <int Q, bool NORM, int BLK>
+__device__ __forceinline__ void stage_write(const XStage<Q, NORM>& st, int batch, int NC, float inv, u4_t* xs,
+                                            float* sx) {
+  using T = QTraits<Q>;
+#pragma unroll
+  for (int i = 0; i < XStage<Q, NORM>::XB; ++i) {
+    const int c = (batch * XStage<Q, NORM>::XB + i) * BLK + threadIdx.x;
+    if (c < NC) {
+      float corr = 0.f;
+#pragma unroll
+      for (int p = 0; p < T::PLANES; ++p) {
+        const h8_t xv = __builtin_bit_cast(h8_t, st.x[i][p]);
+        float v[8];
+        if constexpr (NORM) {
+          const h8_t wv = __builtin_bit_cast(h8_t, st.w[i][p]);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[e] = (float)(_Float16)(((float)xv[e] * inv) * (float)wv[e]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[e] = (float)xv[e];
+        }
+        _Float16 o[8];
+        corr += plane_order<Q>(v, o);
+        h8_t ov;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ov[e] = o[e];
+        xs[p * NC + c] = __builtin_bit_cast(u4_t, ov);
+      }
+      if constexpr (quantized<Q>()) sx[c] = corr;
+    }
+  }
+}
+
+// Finishes the staging whose batch 0 was issued with stage_issue.
+template <int Q, bool NORM, int BLK>
+__device__ __forceinline__ void stage_finish(const GemvArgs& a, XStage<Q, NORM>& st, int NC, u4_t* xs, float* sx,
+                                             float* red) {
+  using T = QTraits<Q>;
   float inv = 1.f;
   if constexpr (NORM) {
+    // one batch holds all of x (host-checked); RMSNorm (kernels.cu:689-751)
     float ss = 0.f;
-    for (int i = threadIdx.x; i < K / 8; i += kBlock) {
-      const h8_t v = __builtin_bit_cast(h8_t, load_u4(x + 8 * i));
 #pragma unroll
-      for (int e = 0; e < 8; ++e) ss += (float)v[e] * (float)v[e];
+    for (int i = 0; i < XStage<Q, NORM>::XB; ++i) {
+      const int c = i * BLK + threadIdx.x;
+      if (c < NC) {
+#pragma unroll
+        for (int p = 0; p < T::PLANES; ++p) {
+          const h8_t xv = __builtin_bit_cast(h8_t, st.x[i][p]);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) ss += (float)xv[e] * (float)xv[e];
+        }
+      }
     }
     ss = block_sum(ss, red);
-    // eps travels as fp16 in the reference (kernels.cu:726, model.cu:96).
-    inv = rsqrtf(ss / (float)K + (float)(_Float16)a.eps);
+    // eps travels as fp16 in the reference (kernels.cu:726, model.cu:96)
+    inv = rsqrtf(ss / (float)a.K + (float)(_Float16)a.eps);
   }
-  for (int c = threadIdx.x; c < NC; c += kBlock) {
-    float s = 0.f;
-#pragma unroll
-    for (int p = 0; p < T::PLANES; ++p) {
-      const int e0 = c * T::EPC + p * 8;
-      const h8_t xv = __builtin_bit_cast(h8_t, load_u4(x + e0));
-      float v[8];
-      if constexpr (NORM) {
-        const h8_t wv = __builtin_bit_cast(h8_t, load_u4(nw + e0));
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = (float)(_Float16)(((float)xv[e] * inv) * (float)wv[e]);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = (float)xv[e];
-      }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) s += v[e];
-      _Float16 o[8];
-      plane_order<Q>(v, o);
-      h8_t ov;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) ov[e] = o[e];
-      xs[p * NC + c] = __builtin_bit_cast(u4_t, ov);
-    }
-    if constexpr (quantized<Q>()) sx[c] = s;
+  stage_write<Q, NORM, BLK>(st, 0, NC, inv, xs, sx);
+  const int per_batch = XStage<Q, NORM>::XB * BLK;
+  for (int b = 1; b * per_batch < NC; ++b) {
+    stage_issue<Q, NORM, BLK>(a, st, b, NC);
+    stage_write<Q, NORM, BLK>(st, b, NC, inv, xs, sx);
   }
   __syncthreads();
 }
@@ -106,160 +153,210 @@ __device__ __forceinline__ RowRef row_of(const GemvArgs& a, int unit, int r) {
   return rr;
 }
 
-template <int R>
-__device__ __forceinline__ float pick(const float (&acc)[R], int i) {
-  float v = acc[0];
+// Per-wave register buffer of one k-step: kUnroll 16-byte chunks of R rows.
+template <int R, int U>
+struct StepBuf {
+  u4_t w[U][R];
+  _Float16 sc[U][R];   // converted at use, so the issue of the next step's loads never waits on them
+};
+
+template <int Q, int MODE, int R, int U, bool G128>
+__device__ __forceinline__ void load_step(const GemvArgs& a, StepBuf<R, U>& b, int unit, int kb, int NC, int lane) {
+  using T = QTraits<Q>;
+  const int64_t rbytes = (int64_t)NC * 16;
+  const int sstride = G128 ? a.K / kGroup : 1;
 #pragma unroll
-  for (int r = 1; r < R; ++r)
-    if (i == r) v = acc[r];
-  return v;
+  for (int r = 0; r < R; ++r) {
+    const RowRef rr = row_of<MODE, R>(a, unit, r);
+    const char* rp = reinterpret_cast<const char*>(a.W[rr.mat]) + (int64_t)rr.row * rbytes;
+    const _Float16* sp = nullptr;
+    if constexpr (quantized<Q>()) sp = reinterpret_cast<const _Float16*>(a.S[rr.mat]) + (int64_t)rr.row * sstride;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = min(kb * (kWave * U) + u * kWave + lane, NC - 1);
+      b.w[u][r] = load_u4_stream(rp + (int64_t)c * 16);
+      if constexpr (quantized<Q>()) b.sc[u][r] = sp[G128 ? (c * T::EPC) / kGroup : 0];
+    }
+  }
 }
 
-template <int Q, int MODE, int R, bool NORM, bool G128>
-__global__ __launch_bounds__(kBlock) void gemv_kernel(const GemvArgs a) {
+template <int Q, int R, int U>
+__device__ __forceinline__ void compute_step(const StepBuf<R, U>& b, float (&acc)[R], const u4_t* xs, const float* sx,
+                                             int kb, int NC, int lane, const UnpackRegs& k) {
+  using T = QTraits<Q>;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int c = kb * (kWave * U) + u * kWave + lane;
+    if (c < NC) {
+      u4_t xv[T::PLANES];
+#pragma unroll
+      for (int p = 0; p < T::PLANES; ++p) xv[p] = xs[p * NC + c];
+      if constexpr (quantized<Q>()) {
+        const float corr = sx[c];
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] = fmaf((float)b.sc[u][r], chunk_dot<Q>(b.w[u][r], xv, k) - corr, acc[r]);
+      } else {
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] += chunk_dot<Q>(b.w[u][r], xv, k);
+      }
+    }
+  }
+}
+
+// Epilogue of one output row (STORE / RESID modes).
+template <int MODE, int R>
+__device__ __forceinline__ void store_row(const GemvArgs& a, float v, int unit, int r) {
+  const RowRef me = row_of<MODE, R>(a, unit, r);
+  if (!me.valid) return;
+  _Float16* out = reinterpret_cast<_Float16*>(a.out[0]);
+  if constexpr (MODE == GM_RESID) {
+    v = (float)out[me.row] + v;          // residual stays fp16 (kernels.cu:621, :671)
+  } else if (a.bias[0]) {
+    v += (float)reinterpret_cast<const _Float16*>(a.bias[0])[me.row];
+  }
+  _Float16 h = (_Float16)v;
+  if (MODE == GM_STORE && a.stamp && a.stamp[me.row] == *a.d_epoch) {
+    // repetition penalty on the fp16 logit (kernels.cu:885-888)
+    const float pen = (float)(_Float16)a.penalty;
+    const float l = (float)h;
+    h = (_Float16)(l < 0.f ? l * pen : l / pen);
+  }
+  out[me.row] = h;
+}
+
+// QKV epilogue of one rotation pair (rows i and i + hd/2 of a head): bias,
+// fp16, NeoX RoPE on q/k, k/v into the cache.
+template <int MODE, int R>
+__device__ __forceinline__ void qkv_pair(const GemvArgs& a, float y0, float y1, int unit, int i_pair) {
+  constexpr int PP = R / 2;
+  const RowRef r0 = row_of<MODE, R>(a, unit, i_pair);
+  const RowRef r1 = row_of<MODE, R>(a, unit, i_pair + PP);
+  const _Float16* b = reinterpret_cast<const _Float16*>(a.bias[r0.mat]);
+  if (b) { y0 += (float)b[r0.row]; y1 += (float)b[r1.row]; }
+  y0 = (float)(_Float16)y0;            // q/k/v are fp16 before RoPE (kernels.cu:470)
+  y1 = (float)(_Float16)y1;
+  const int pos = *a.d_pos;
+  const int hd = a.head_dim;
+  const int i = r0.row % hd;           // rotation index in [0, hd/2)
+  if (r0.mat < 2) {
+    // NeoX rotation of (i, i + hd/2) (kernels.cu:370-398); the angle is
+    // evaluated in double precision.
+    const double freq = 1.0 / pow((double)a.rope_theta, (2.0 * i) / (double)hd);
+    double sn, cs;
+    sincos((double)pos * freq, &sn, &cs);
+    const float c = (float)cs, s = (float)sn;
+    const float o0 = add_rn(mul_rn(y0, c), -mul_rn(y1, s));
+    const float o1 = add_rn(mul_rn(y1, c), mul_rn(y0, s));
+    y0 = o0;
+    y1 = o1;
+  }
+  const _Float16 h0 = (_Float16)y0, h1 = (_Float16)y1;
+  _Float16* out = reinterpret_cast<_Float16*>(a.out[r0.mat]);
+  if (out) { out[r0.row] = h0; out[r1.row] = h1; }
+  if (r0.mat > 0 && a.kcache) {
+    const int kvh = r0.row / hd, d0 = r0.row % hd, d1 = r1.row % hd;
+    _Float16* cache = reinterpret_cast<_Float16*>(r0.mat == 1 ? a.kcache : a.vcache);
+    if (r0.mat == 1) {
+      cache[kv_k_offset(kvh, pos, d0, a.max_seq, hd)] = h0;
+      cache[kv_k_offset(kvh, pos, d1, a.max_seq, hd)] = h1;
+    } else {
+      cache[kv_v_offset(kvh, pos, d0, a.max_seq, hd)] = h0;
+      cache[kv_v_offset(kvh, pos, d1, a.max_seq, hd)] = h1;
+    }
+  }
+}
+
+// Reduce the wave's R row sums and run the epilogue; lane r handles row r
+// (static register indices only, so nothing goes through scratch).
+template <int MODE, int R>
+__device__ __forceinline__ void finish_unit(const GemvArgs& a, float (&acc)[R], int unit, int lane) {
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
+  if constexpr (MODE == GM_STORE || MODE == GM_RESID) {
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      if (lane == r) store_row<MODE, R>(a, acc[r], unit, r);
+  } else if constexpr (MODE == GM_SWIGLU) {
+#pragma unroll
+    for (int r = 0; r < R / 2; ++r) {
+      if (lane == r) {
+        const RowRef me = row_of<MODE, R>(a, unit, r);
+        if (me.valid) {
+          const float g = acc[r], u = acc[r + R / 2];
+          const float sig = 1.f / (1.f + expf(-g));    // kernels.cu:566
+          reinterpret_cast<_Float16*>(a.out[0])[me.row] = (_Float16)((g * sig) * u);
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < R / 2; ++r)
+      if (lane == r) qkv_pair<MODE, R>(a, acc[r], acc[r + R / 2], unit, r);
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = 0.f;
+}
+
+// Persistent GEMV: wave w owns units w, w + W, w + 2W, ... (W = waves in
+// the grid) and streams its (unit, k-step) sequence; a step is U 16-byte
+// chunks per lane of each of the unit's R rows, all requested before any is
+// used.  The first step is requested before the LDS staging so the input
+// vector prologue overlaps the first HBM round trip.  PIPE additionally
+// requests step s+1 before computing step s.
+template <int Q, int MODE, int R, int U, bool NORM, bool G128, bool PIPE, int BLK>
+__global__ __launch_bounds__(BLK) void gemv_kernel(const GemvArgs a) {
   using T = QTraits<Q>;
   extern __shared__ u4_t smem[];
   __shared__ float red[16];
   const int NC = a.K / T::EPC;
   u4_t* xs = smem;
   float* sx = reinterpret_cast<float*>(smem + T::PLANES * NC);
-
-  stage_x<Q, NORM>(a, xs, sx, red);
-
   const int lane = threadIdx.x & (kWave - 1);
   const int n_units = units_total<MODE, R>(a);
-  const int64_t rbytes = (int64_t)NC * 16;
-  const int sstride = G128 ? a.K / kGroup : 1;
+  constexpr int WPB = BLK / kWave;
+  const int first = blockIdx.x * WPB + threadIdx.x / kWave;
+  const int stride = gridDim.x * WPB;
+  const int NB = (NC + kWave * U - 1) / (kWave * U);
+  const int my_units = first < n_units ? (n_units - first + stride - 1) / stride : 0;
+  const int S = my_units * NB;
 
-  for (int unit = blockIdx.x * kWavesPerBlock + threadIdx.x / kWave; unit < n_units;
-       unit += gridDim.x * kWavesPerBlock) {
-    const char* rp[R];
-    const _Float16* sp[R];
-    RowRef rr[R];
+  XStage<Q, NORM> st;
+  stage_issue<Q, NORM, BLK>(a, st, 0, NC);
+  StepBuf<R, U> A;
+  if (S > 0) load_step<Q, MODE, R, U, G128>(a, A, first, 0, NC, lane);
+  stage_finish<Q, NORM, BLK>(a, st, NC, xs, sx, red);
+
+  const UnpackRegs uk = unpack_regs();
+  float acc[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      rr[r] = row_of<MODE, R>(a, unit, r);
-      rp[r] = reinterpret_cast<const char*>(a.W[rr[r].mat]) + (int64_t)rr[r].row * rbytes;
-      if constexpr (quantized<Q>())
-        sp[r] = reinterpret_cast<const _Float16*>(a.S[rr[r].mat]) + (int64_t)rr[r].row * sstride;
+  for (int r = 0; r < R; ++r) acc[r] = 0.f;
+  if constexpr (!PIPE) {
+    for (int s = 0; s < S; ++s) {
+      const int unit = first + (s / NB) * stride, kb = s % NB;
+      if (s > 0) load_step<Q, MODE, R, U, G128>(a, A, unit, kb, NC, lane);
+      compute_step<Q, R, U>(A, acc, xs, sx, kb, NC, lane, uk);
+      if (kb == NB - 1) finish_unit<MODE, R>(a, acc, unit, lane);
     }
-
-    float acc[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) acc[r] = 0.f;
-
-    for (int base = 0; base < NC; base += kWave * kUnroll) {
-      u4_t w[kUnroll][R];
-      float sc[kUnroll][R];
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const int c = min(base + u * kWave + lane, NC - 1);
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-          w[u][r] = load_u4_stream(rp[r] + (int64_t)c * 16);
-          if constexpr (quantized<Q>()) sc[u][r] = (float)sp[r][G128 ? (c * T::EPC) / kGroup : 0];
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const int c = base + u * kWave + lane;
-        if (c < NC) {
-          u4_t xv[T::PLANES];
-#pragma unroll
-          for (int p = 0; p < T::PLANES; ++p) xv[p] = xs[p * NC + c];
-          if constexpr (quantized<Q>()) {
-            const float corr = T::BIAS * sx[c];
-#pragma unroll
-            for (int r = 0; r < R; ++r) acc[r] = fmaf(sc[u][r], chunk_dot<Q>(w[u][r], xv) - corr, acc[r]);
-          } else {
-#pragma unroll
-            for (int r = 0; r < R; ++r) acc[r] += chunk_dot<Q>(w[u][r], xv);
-          }
-        }
-      }
-    }
-#pragma unroll
-    for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
-
-    // ------------------------------------------------------------ epilogue
-    if constexpr (MODE == GM_STORE || MODE == GM_RESID) {
-      if (lane < R) {
-        const RowRef me = row_of<MODE, R>(a, unit, lane);
-        if (me.valid) {
-          float v = pick<R>(acc, lane);
-          _Float16* out = reinterpret_cast<_Float16*>(a.out[0]);
-          if constexpr (MODE == GM_RESID) {
-            v = (float)out[me.row] + v;          // residual stays fp16 (kernels.cu:621, :671)
-          } else if (a.bias[0]) {
-            v += (float)reinterpret_cast<const _Float16*>(a.bias[0])[me.row];
-          }
-          _Float16 h = (_Float16)v;
-          if (MODE == GM_STORE && a.stamp && a.stamp[me.row] == *a.d_epoch) {
-            // repetition penalty on the fp16 logit (kernels.cu:885-888)
-            const float pen = (float)(_Float16)a.penalty;
-            const float l = (float)h;
-            h = (_Float16)(l < 0.f ? l * pen : l / pen);
-          }
-          out[me.row] = h;
-        }
-      }
-    } else if constexpr (MODE == GM_SWIGLU) {
-      if (lane < R / 2) {
-        const RowRef me = row_of<MODE, R>(a, unit, lane);
-        if (me.valid) {
-          const float g = pick<R>(acc, lane), u = pick<R>(acc, lane + R / 2);
-          const float sig = 1.f / (1.f + expf(-g));    // kernels.cu:566
-          reinterpret_cast<_Float16*>(a.out[0])[me.row] = (_Float16)((g * sig) * u);
-        }
-      }
-    } else {  // GM_QKV: bias, RoPE on q/k, k/v into the cache
-      constexpr int PP = R / 2;
-      if (lane < PP) {
-        const RowRef r0 = row_of<MODE, R>(a, unit, lane);
-        const RowRef r1 = row_of<MODE, R>(a, unit, lane + PP);
-        const _Float16* b = reinterpret_cast<const _Float16*>(a.bias[r0.mat]);
-        float y0 = pick<R>(acc, lane), y1 = pick<R>(acc, lane + PP);
-        if (b) { y0 += (float)b[r0.row]; y1 += (float)b[r1.row]; }
-        y0 = (float)(_Float16)y0;            // q/k/v are fp16 before RoPE (kernels.cu:470)
-        y1 = (float)(_Float16)y1;
-        const int pos = *a.d_pos;
-        const int hd = a.head_dim;
-        const int i = r0.row % hd;           // rotation index in [0, hd/2)
-        if (r0.mat < 2) {
-          // NeoX rotation of (i, i + hd/2) (kernels.cu:370-398); the angle is
-          // evaluated in double precision.
-          const double freq = 1.0 / pow((double)a.rope_theta, (2.0 * i) / (double)hd);
-          double sn, cs;
-          sincos((double)pos * freq, &sn, &cs);
-          const float c = (float)cs, s = (float)sn;
-          const float o0 = add_rn(mul_rn(y0, c), -mul_rn(y1, s));
-          const float o1 = add_rn(mul_rn(y1, c), mul_rn(y0, s));
-          y0 = o0;
-          y1 = o1;
-        }
-        const _Float16 h0 = (_Float16)y0, h1 = (_Float16)y1;
-        _Float16* out = reinterpret_cast<_Float16*>(a.out[r0.mat]);
-        if (out) { out[r0.row] = h0; out[r1.row] = h1; }
-        if (r0.mat > 0 && a.kcache) {
-          const int kvh = r0.row / hd, d0 = r0.row % hd, d1 = r1.row % hd;
-          _Float16* cache = reinterpret_cast<_Float16*>(r0.mat == 1 ? a.kcache : a.vcache);
-          if (r0.mat == 1) {
-            cache[kv_k_offset(kvh, pos, d0, a.max_seq, hd)] = h0;
-            cache[kv_k_offset(kvh, pos, d1, a.max_seq, hd)] = h1;
-          } else {
-            cache[kv_v_offset(kvh, pos, d0, a.max_seq, hd)] = h0;
-            cache[kv_v_offset(kvh, pos, d1, a.max_seq, hd)] = h1;
-          }
-        }
-      }
+  } else {
+    StepBuf<R, U> B;
+    for (int s = 0; s < S; s += 2) {
+      const int u0 = first + (s / NB) * stride, kb0 = s % NB;
+      const bool has1 = s + 1 < S;
+      const int u1 = first + ((s + 1) / NB) * stride, kb1 = (s + 1) % NB;
+      if (has1) load_step<Q, MODE, R, U, G128>(a, B, u1, kb1, NC, lane);
+      __builtin_amdgcn_sched_barrier(0);
+      compute_step<Q, R, U>(A, acc, xs, sx, kb0, NC, lane, uk);
+      if (kb0 == NB - 1) finish_unit<MODE, R>(a, acc, u0, lane);
+      if (!has1) break;
+      if (s + 2 < S) load_step<Q, MODE, R, U, G128>(a, A, first + ((s + 2) / NB) * stride, (s + 2) % NB, NC, lane);
+      __builtin_amdgcn_sched_barrier(0);
+      compute_step<Q, R, U>(B, acc, xs, sx, kb1, NC, lane, uk);
+      if (kb1 == NB - 1) finish_unit<MODE, R>(a, acc, u1, lane);
     }
   }
 }
 
 // ------------------------------------------------------------------ host
-static constexpr int rows_per_wave(int mode) {
-  return mode == GM_STORE ? 4 : mode == GM_RESID ? 2 : mode == GM_SWIGLU ? 4 : 2;
-}
 
 int gemv_check(const GemvArgs& a) {
   if (a.quant < 0 || a.quant > 2) return fail(CQ_EINVAL, "gemv: bad quant type");
@@ -283,23 +380,45 @@ int gemv_check(const GemvArgs& a) {
   const int epc = a.quant == CQ_QUANT_INT4 ? 32 : a.quant == CQ_QUANT_INT8 ? 16 : 8;
   const size_t lds = (size_t)planes * (a.K / epc) * 16 + (a.quant ? (size_t)(a.K / epc) * 4 : 0);
   if (lds > 60 * 1024) return fail(CQ_EINVAL, "gemv: input vector too long for LDS staging");
+  if (a.norm_w && a.K > 16384) return fail(CQ_EINVAL, "gemv: fused RMSNorm supports K <= 16384");
   return CQ_OK;
 }
 
-template <int Q, int MODE, bool NORM, bool G128>
-static int launch_t(const GemvArgs& a, hipStream_t stream) {
+// Tuning of one launch (measured on MI355X at the Qwen2.5-7B INT4 shapes):
+// rows per wave, 16-byte chunks per lane per step, software pipelining,
+// threads per block, and resident blocks per CU of the persistent grid.
+// Fat 1024-thread blocks stage x once per CU for the long GEMVs; the short
+// QKV projection prefers more, smaller blocks.
+template <int MODE> struct GemvTune;
+template <> struct GemvTune<GM_STORE> { static constexpr int R = 4, U = 1, BLK = 1024, PER_CU = 1; static constexpr bool PIPE = false; };
+template <> struct GemvTune<GM_RESID> { static constexpr int R = 1, U = 2, BLK = 1024, PER_CU = 1; static constexpr bool PIPE = false; };
+template <> struct GemvTune<GM_SWIGLU> { static constexpr int R = 2, U = 2, BLK = 1024, PER_CU = 1; static constexpr bool PIPE = false; };
+template <> struct GemvTune<GM_QKV> { static constexpr int R = 2, U = 2, BLK = 256, PER_CU = 4; static constexpr bool PIPE = false; };
+
+template <int Q, int MODE, int R, int U, bool NORM, bool G128, bool PIPE, int BLK = 256>
+int launch_variant(const GemvArgs& a, hipStream_t stream, int max_blocks) {
+  constexpr int kWavesPerBlock = BLK / kWave;
   using T = QTraits<Q>;
-  constexpr int R = rows_per_wave(MODE);
   const int NC = a.K / T::EPC;
   const size_t lds = (size_t)T::PLANES * NC * 16 + (Q != CQ_QUANT_FP16 ? (size_t)NC * 4 : 0);
   int units;
   if (MODE == GM_SWIGLU) units = (a.N + R / 2 - 1) / (R / 2);
   else if (MODE == GM_QKV) units = (a.n_heads + 2 * a.n_kv) * (a.head_dim / 2) / (R / 2);
   else units = (a.N + R - 1) / R;
-  const int blocks = std::min((units + kWavesPerBlock - 1) / kWavesPerBlock, kMaxGemvBlocks);
-  hipLaunchKernelGGL((gemv_kernel<Q, MODE, R, NORM, G128>), dim3(blocks), dim3(kBlock), lds, stream, a);
+  // balanced persistent grid: every wave gets ceil(units / max_waves) units
+  const int max_waves = max_blocks * kWavesPerBlock;
+  const int per_wave = (units + max_waves - 1) / max_waves;
+  const int waves = (units + per_wave - 1) / per_wave;
+  const int blocks = (waves + kWavesPerBlock - 1) / kWavesPerBlock;
+  hipLaunchKernelGGL((gemv_kernel<Q, MODE, R, U, NORM, G128, PIPE, BLK>), dim3(blocks), dim3(BLK), lds, stream, a);
   CQ_HIP(hipGetLastError());
   return CQ_OK;
+}
+
+template <int Q, int MODE, bool NORM, bool G128>
+static int launch_t(const GemvArgs& a, hipStream_t stream) {
+  using TN = GemvTune<MODE>;
+  return launch_variant<Q, MODE, TN::R, TN::U, NORM, G128, TN::PIPE, TN::BLK>(a, stream, TN::PER_CU * kNumCUs);
 }
 
 template <int Q, int MODE>
@@ -350,16 +469,22 @@ __global__ void dequant_kernel(const char* W, const _Float16* S, float* out, int
   const float s = group ? (float)S[(int64_t)r * (cols / group) + (c * T::EPC) / group] : (float)S[r];
   float* o = out + (int64_t)r * cols + (int64_t)c * T::EPC;
   const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+  const UnpackRegs k = unpack_regs();
   if constexpr (Q == CQ_QUANT_INT4) {
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
-      const uint32_t f = words[p] ^ kInt4Flip;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const h2_t h = as_h2(int4_pair(f, i));
-        o[8 * p + i] = ((float)h.x - kInt4Bias) * s;
-        o[8 * p + i + 4] = ((float)h.y - kInt4Bias) * s;
-      }
+      const uint32_t f = words[p] ^ kInt4Flip, f8 = f >> 8;
+      const h2_t a0 = as_h2(and_or(f, k.m_lo, 0x64006400u)), a1 = as_h2(and_or(f, k.m_hi, 0x64006400u));
+      const h2_t a2 = as_h2(and_or(f8, k.m_lo, 0x64006400u)), a3 = as_h2(and_or(f8, k.m_hi, 0x64006400u));
+      // (1024 + n) - 1032 = q ; (1024 + 16 n) / 16 - 72 = q
+      o[8 * p + 0] = ((float)a0.x - kInt4BiasLo) * s;
+      o[8 * p + 4] = ((float)a0.y - kInt4BiasLo) * s;
+      o[8 * p + 1] = ((float)a1.x * 0.0625f - kInt4BiasHi) * s;
+      o[8 * p + 5] = ((float)a1.y * 0.0625f - kInt4BiasHi) * s;
+      o[8 * p + 2] = ((float)a2.x - kInt4BiasLo) * s;
+      o[8 * p + 6] = ((float)a2.y - kInt4BiasLo) * s;
+      o[8 * p + 3] = ((float)a3.x * 0.0625f - kInt4BiasHi) * s;
+      o[8 * p + 7] = ((float)a3.y * 0.0625f - kInt4BiasHi) * s;
     }
   } else {
 #pragma unroll
@@ -367,7 +492,7 @@ __global__ void dequant_kernel(const char* W, const _Float16* S, float* out, int
       const uint32_t f = words[p] ^ kInt8Flip;
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
-        const h2_t h = as_h2(int8_pair(f, i));
+        const h2_t h = as_h2(int8_pair(f, k.magic, i));
         o[4 * p + 2 * i] = ((float)h.x - kInt8Bias) * s;
         o[4 * p + 2 * i + 1] = ((float)h.y - kInt8Bias) * s;
       }

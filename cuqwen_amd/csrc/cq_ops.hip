@@ -126,11 +126,12 @@ __device__ __forceinline__ unsigned long long block_max_u64(unsigned long long v
   return b;
 }
 
-__global__ __launch_bounds__(256) void argmax_kernel(const _Float16* logits, int vocab,
-                                                     unsigned long long* partials, unsigned* counter, StepCtl* ctl,
-                                                     int* d_token_out, int* history, int* tokens_out) {
+// Stage 1: each block writes its best key; stage 2 (one block) reduces them
+// and does the step bookkeeping (kernels.cu:915-950).  Two launches cost
+// less here than one launch with a completion ticket and device-scope fences.
+__global__ __launch_bounds__(256) void argmax_stage1(const _Float16* logits, int vocab,
+                                                     unsigned long long* partials) {
   __shared__ unsigned long long red[16];
-  __shared__ unsigned ticket;
   unsigned long long best = 0ull;
   for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < vocab; i += gridDim.x * blockDim.x) {
     const unsigned long long k = argmax_key((float)logits[i], i);
@@ -138,18 +139,14 @@ __global__ __launch_bounds__(256) void argmax_kernel(const _Float16* logits, int
   }
   best = block_max_u64(best, red);
   if (threadIdx.x == 0) partials[blockIdx.x] = best;
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) ticket = atomicAdd(counter, 1u);
-  __syncthreads();
-  if (ticket != gridDim.x - 1) return;
-  __threadfence();
-  unsigned long long b = 0ull;
-  for (int i = threadIdx.x; i < (int)gridDim.x; i += blockDim.x) b = partials[i] > b ? partials[i] : b;
-  b = block_max_u64(b, red);
+}
+
+__global__ __launch_bounds__(kArgmaxBlocks) void argmax_stage2(const unsigned long long* partials, StepCtl* ctl,
+                                                               int* d_token_out, int* history, int* tokens_out) {
+  __shared__ unsigned long long red[16];
+  const unsigned long long b = block_max_u64(partials[threadIdx.x], red);
   if (threadIdx.x == 0) {
     const int token = (int)(~(uint32_t)(b & 0xffffffffu));
-    *counter = 0u;
     if (d_token_out) *d_token_out = token;
     if (ctl) {
       ctl->sampled = token;
@@ -171,10 +168,10 @@ __global__ __launch_bounds__(256) void argmax_kernel(const _Float16* logits, int
 int launch_argmax(const __half* logits, int vocab, unsigned long long* partials, StepCtl* ctl, int* d_token_out,
                   int* history, int* tokens_out, hipStream_t stream) {
   if (!logits || vocab <= 0 || !partials) return fail(CQ_EINVAL, "argmax: bad arguments");
-  // partials: kArgmaxBlocks keys followed by the ticket counter.
-  unsigned* counter = reinterpret_cast<unsigned*>(partials + kArgmaxBlocks);
-  hipLaunchKernelGGL(argmax_kernel, dim3(kArgmaxBlocks), dim3(256), 0, stream, (const _Float16*)logits, vocab,
-                     partials, counter, ctl, d_token_out, history, tokens_out);
+  hipLaunchKernelGGL(argmax_stage1, dim3(kArgmaxBlocks), dim3(256), 0, stream, (const _Float16*)logits, vocab,
+                     partials);
+  hipLaunchKernelGGL(argmax_stage2, dim3(1), dim3(kArgmaxBlocks), 0, stream, partials, ctl, d_token_out, history,
+                     tokens_out);
   CQ_HIP(hipGetLastError());
   return CQ_OK;
 }
