@@ -72,7 +72,7 @@ class Config(ctypes.Structure):
 def _load():
     if not os.path.exists(LIB_PATH):
         raise ImportError(
-            f"{LIB_PATH} is not built; run `python -m cuqwen_amd.build` (or __graft_entry__.build())")
+            f"{LIB_PATH} is not built; run `python cuqwen_amd/build.py` (or __graft_entry__.build())")
     lib = ctypes.CDLL(LIB_PATH)
     P, I32, U64, SZ, F = ctypes.c_void_p, ctypes.c_int32, ctypes.c_uint64, ctypes.c_size_t, ctypes.c_float
     CP = ctypes.POINTER(Config)

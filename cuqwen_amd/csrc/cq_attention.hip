@@ -60,9 +60,9 @@ __device__ __forceinline__ void load_tile(KVTile<HD>& t, const _Float16* kbase, 
   for (int st = 0; st < 2; ++st)
 #pragma unroll
     for (int kk = 0; kk < HD / 32; ++kk)
-      t.ka[st][kk] = __builtin_bit_cast(h8_t, load_u4(kt + st * 16 * HD + (kk * 64 + lane) * 8));
+      t.ka[st][kk] = __builtin_bit_cast(h8_t, load_u4_stream(kt + st * 16 * HD + (kk * 64 + lane) * 8));
 #pragma unroll
-  for (int dt = 0; dt < HD / 16; ++dt) t.va[dt] = __builtin_bit_cast(h8_t, load_u4(vt + (dt * 64 + lane) * 8));
+  for (int dt = 0; dt < HD / 16; ++dt) t.va[dt] = __builtin_bit_cast(h8_t, load_u4_stream(vt + (dt * 64 + lane) * 8));
 }
 
 // One 32-key tile of the online softmax for this wave.
@@ -222,10 +222,14 @@ __global__ __launch_bounds__(kAttnThreads) void attention_stage1(const AttnArgs 
 }
 
 // One block per query head: log-sum-exp merge of the partitions
-// (kernels.cu:222-288) with 1/(L + 1e-9).
+// (kernels.cu:222-288) with 1/(L + 1e-9).  Every partial this block needs
+// (m, l and its share of O) is requested up front, so the merge costs one
+// memory round trip.
 constexpr int kMergeThreads = 256;
 template <int HD>
 __global__ __launch_bounds__(kMergeThreads) void attention_stage2(const AttnArgs a, int Pmax) {
+  constexpr int PG = kMergeThreads / HD;            // partition groups (2 for hd 128, 4 for hd 64)
+  constexpr int MAXQ = 32;                          // partitions per thread per round
   const int T = *a.d_pos + 1;
   int tpp;
   const int nparts = attn_nparts(T, Pmax, &tpp);
@@ -236,33 +240,48 @@ __global__ __launch_bounds__(kMergeThreads) void attention_stage2(const AttnArgs
   const float* ws_m = reinterpret_cast<const float*>(a.workspace);
   const float* ws_l = ws_m + (size_t)a.n_kv * Pmax * 16;
   const float* ws_o = ws_l + (size_t)a.n_kv * Pmax * 16;
+  const size_t base = (size_t)kvh * Pmax;
+  const int p = threadIdx.x;
+  const int d = threadIdx.x % HD, pg = threadIdx.x / HD;
+  // issue every load first
+  const float mp = p < nparts ? ws_m[(base + p) * 16 + hh] : -INFINITY;
+  const float lp = p < nparts ? ws_l[(base + p) * 16 + hh] : 0.f;
+  float ov[MAXQ];
+#pragma unroll
+  for (int i = 0; i < MAXQ; ++i) {
+    const int q = pg + i * PG;
+    ov[i] = q < nparts ? ws_o[((base + q) * 16 + hh) * HD + d] : 0.f;
+  }
+  // (one round covers nparts <= 32 * PG; larger counts take more rounds below)
   __shared__ float pw[kAttnBlocksTarget];
   __shared__ float red[16];
-  __shared__ float part_o[kMergeThreads / HD][HD];
-  // global max and weights (nparts <= Pmax <= 256 = blockDim)
-  const int p = threadIdx.x;
-  const float mp = p < nparts ? ws_m[((size_t)kvh * Pmax + p) * 16 + hh] : -INFINITY;
+  __shared__ float part_o[PG][HD];
   float M = wave_max(mp);
   if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = M;
   __syncthreads();
   M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   const float wgt = p < nparts ? __expf(mp - M) : 0.f;
-  if (p < kAttnBlocksTarget) pw[p] = wgt;
-  const float lw = p < nparts ? ws_l[((size_t)kvh * Pmax + p) * 16 + hh] * wgt : 0.f;
-  __syncthreads();
-  const float L = block_sum(lw, red);
-  // O: thread (pg, d) sums partitions pg, pg + PG, ...
-  constexpr int PG = kMergeThreads / HD;
-  const int d = threadIdx.x % HD, pg = threadIdx.x / HD;
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
-  int q = pg;
-  for (; q + 3 * PG < nparts; q += 4 * PG) {
+  pw[p] = wgt;
+  const float L = block_sum(lp * wgt, red);   // its first barrier also publishes pw
+  float acc = 0.f;
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
-      acc[u] += ws_o[(((size_t)kvh * Pmax + q + u * PG) * 16 + hh) * HD + d] * pw[q + u * PG];
+  for (int i = 0; i < MAXQ; ++i) {
+    const int q = pg + i * PG;
+    if (q < nparts) acc += ov[i] * pw[q];
   }
-  for (; q < nparts; q += PG) acc[0] += ws_o[(((size_t)kvh * Pmax + q) * 16 + hh) * HD + d] * pw[q];
-  part_o[pg][d] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+  for (int r0 = MAXQ * PG; r0 < nparts; r0 += MAXQ * PG) {
+#pragma unroll
+    for (int i = 0; i < MAXQ; ++i) {
+      const int q = r0 + pg + i * PG;
+      ov[i] = q < nparts ? ws_o[((base + q) * 16 + hh) * HD + d] : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < MAXQ; ++i) {
+      const int q = r0 + pg + i * PG;
+      if (q < nparts) acc += ov[i] * pw[q];
+    }
+  }
+  part_o[pg][d] = acc;
   __syncthreads();
   if (pg == 0) {
     float O = 0.f;

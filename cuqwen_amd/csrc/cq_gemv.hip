@@ -15,7 +15,13 @@ template <int Q> __device__ __forceinline__ constexpr bool quantized() { return 
 // the prologue costs one memory round trip per batch (one batch whenever the
 // RMSNorm is fused: K <= 16384).  The LDS image is PLANES planes of 16-byte
 // chunk slices (bank-conflict-free 16-byte reads in the main loop) plus the
-// per-chunk sum of x for the unpack bias.
+// per-chunk unpack-bias term.
+//
+// Fused RMSNorm (kernels.cu:689-751): the staged vector is half(x * w) and
+// the scalar rsqrt(mean(x^2) + eps) multiplies each finished row sum, so the
+// block reduction of x^2 rides on the staging barrier instead of adding a
+// dependent step before the weights can be consumed.  (The reference rounds
+// x * inv * w to fp16; here x * w is rounded and inv applied in fp32.)
 template <int Q, bool NORM>
 struct XStage {
   static constexpr int P = QTraits<Q>::PLANES;
@@ -43,8 +49,7 @@ __device__ __forceinline__ void stage_issue(const GemvArgs& a, XStage<Q, NORM>& 
 }
 
 template <int Q, bool NORM, int BLK>
-__device__ __forceinline__ void stage_write(const XStage<Q, NORM>& st, int batch, int NC, float inv, u4_t* xs,
-                                            float* sx) {
+__device__ __forceinline__ void stage_write(const XStage<Q, NORM>& st, int batch, int NC, u4_t* xs, float* sx) {
   using T = QTraits<Q>;
 #pragma unroll
   for (int i = 0; i < XStage<Q, NORM>::XB; ++i) {
@@ -58,7 +63,7 @@ __device__ __forceinline__ void stage_write(const XStage<Q, NORM>& st, int batch
         if constexpr (NORM) {
           const h8_t wv = __builtin_bit_cast(h8_t, st.w[i][p]);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) v[e] = (float)(_Float16)(((float)xv[e] * inv) * (float)wv[e]);
+          for (int e = 0; e < 8; ++e) v[e] = (float)(_Float16)((float)xv[e] * (float)wv[e]);
         } else {
 #pragma unroll
           for (int e = 0; e < 8; ++e) v[e] = (float)xv[e];
@@ -75,14 +80,14 @@ __device__ __forceinline__ void stage_write(const XStage<Q, NORM>& st, int batch
   }
 }
 
-// Finishes the staging whose batch 0 was issued with stage_issue.
+// Finishes the staging whose batch 0 was issued with stage_issue; returns
+// the RMSNorm scale (1 without NORM).  `red` holds BLK/64 floats of LDS.
 template <int Q, bool NORM, int BLK>
-__device__ __forceinline__ void stage_finish(const GemvArgs& a, XStage<Q, NORM>& st, int NC, u4_t* xs, float* sx,
-                                             float* red) {
+__device__ __forceinline__ float stage_finish(const GemvArgs& a, XStage<Q, NORM>& st, int NC, u4_t* xs, float* sx,
+                                              float* red) {
   using T = QTraits<Q>;
-  float inv = 1.f;
   if constexpr (NORM) {
-    // one batch holds all of x (host-checked); RMSNorm (kernels.cu:689-751)
+    // one batch holds all of x (host-checked)
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < XStage<Q, NORM>::XB; ++i) {
@@ -96,17 +101,24 @@ __device__ __forceinline__ void stage_finish(const GemvArgs& a, XStage<Q, NORM>&
         }
       }
     }
-    ss = block_sum(ss, red);
-    // eps travels as fp16 in the reference (kernels.cu:726, model.cu:96)
-    inv = rsqrtf(ss / (float)a.K + (float)(_Float16)a.eps);
+    ss = wave_sum(ss);
+    if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = ss;
   }
-  stage_write<Q, NORM, BLK>(st, 0, NC, inv, xs, sx);
+  stage_write<Q, NORM, BLK>(st, 0, NC, xs, sx);
   const int per_batch = XStage<Q, NORM>::XB * BLK;
   for (int b = 1; b * per_batch < NC; ++b) {
     stage_issue<Q, NORM, BLK>(a, st, b, NC);
-    stage_write<Q, NORM, BLK>(st, b, NC, inv, xs, sx);
+    stage_write<Q, NORM, BLK>(st, b, NC, xs, sx);
   }
   __syncthreads();
+  if constexpr (NORM) {
+    float ss = 0.f;
+#pragma unroll
+    for (int w = 0; w < BLK / kWave; ++w) ss += red[w];
+    // eps travels as fp16 in the reference (kernels.cu:726, model.cu:96)
+    return rsqrtf(ss / (float)a.K + (float)(_Float16)a.eps);
+  }
+  return 1.f;
 }
 
 // Rows handled by one wave unit.
@@ -203,17 +215,42 @@ __device__ __forceinline__ void compute_step(const StepBuf<R, U>& b, float (&acc
   }
 }
 
+// Epilogue operands fetched together with a unit's first weights, so the
+// epilogue does not start a dependent memory round trip: lane r < R holds
+// the residual x[row] (RESID) or the bias (STORE); in QKV mode lane i < R/2
+// holds the biases of its rotation pair.
+struct EpiPre {
+  float a = 0.f, b = 0.f;
+};
+
+template <int MODE, int R>
+__device__ __forceinline__ EpiPre epi_prefetch(const GemvArgs& a, int unit, int lane) {
+  EpiPre e;
+  if constexpr (MODE == GM_STORE || MODE == GM_RESID) {
+    if (lane < R) {
+      const RowRef me = row_of<MODE, R>(a, unit, lane);
+      if constexpr (MODE == GM_RESID) e.a = (float)reinterpret_cast<const _Float16*>(a.out[0])[me.row];
+      else if (a.bias[0]) e.a = (float)reinterpret_cast<const _Float16*>(a.bias[0])[me.row];
+    }
+  } else if constexpr (MODE == GM_QKV) {
+    constexpr int PP = R / 2;
+    if (lane < PP) {
+      const RowRef r0 = row_of<MODE, R>(a, unit, lane);
+      const RowRef r1 = row_of<MODE, R>(a, unit, lane + PP);
+      const _Float16* b = reinterpret_cast<const _Float16*>(a.bias[r0.mat]);
+      if (b) { e.a = (float)b[r0.row]; e.b = (float)b[r1.row]; }
+    }
+  }
+  return e;
+}
+
 // Epilogue of one output row (STORE / RESID modes).
 template <int MODE, int R>
-__device__ __forceinline__ void store_row(const GemvArgs& a, float v, int unit, int r) {
+__device__ __forceinline__ void store_row(const GemvArgs& a, float v, float pre, int unit, int r) {
   const RowRef me = row_of<MODE, R>(a, unit, r);
   if (!me.valid) return;
   _Float16* out = reinterpret_cast<_Float16*>(a.out[0]);
-  if constexpr (MODE == GM_RESID) {
-    v = (float)out[me.row] + v;          // residual stays fp16 (kernels.cu:621, :671)
-  } else if (a.bias[0]) {
-    v += (float)reinterpret_cast<const _Float16*>(a.bias[0])[me.row];
-  }
+  v += pre;   // residual (kernels.cu:621, :671: it stays fp16) or bias
   _Float16 h = (_Float16)v;
   if (MODE == GM_STORE && a.stamp && a.stamp[me.row] == *a.d_epoch) {
     // repetition penalty on the fp16 logit (kernels.cu:885-888)
@@ -225,26 +262,26 @@ __device__ __forceinline__ void store_row(const GemvArgs& a, float v, int unit, 
 }
 
 // QKV epilogue of one rotation pair (rows i and i + hd/2 of a head): bias,
-// fp16, NeoX RoPE on q/k, k/v into the cache.
+// fp16, NeoX RoPE on q/k, k/v into the cache.  inv_freq[i] = theta^(-2i/hd)
+// in double; the angle pos * inv_freq is reduced modulo 2 pi in double and
+// its sine and cosine taken in fp32.
 template <int MODE, int R>
-__device__ __forceinline__ void qkv_pair(const GemvArgs& a, float y0, float y1, int unit, int i_pair) {
+__device__ __forceinline__ void qkv_pair(const GemvArgs& a, float y0, float y1, const EpiPre& pre, int unit,
+                                         int i_pair, const double* inv_freq) {
   constexpr int PP = R / 2;
   const RowRef r0 = row_of<MODE, R>(a, unit, i_pair);
   const RowRef r1 = row_of<MODE, R>(a, unit, i_pair + PP);
-  const _Float16* b = reinterpret_cast<const _Float16*>(a.bias[r0.mat]);
-  if (b) { y0 += (float)b[r0.row]; y1 += (float)b[r1.row]; }
-  y0 = (float)(_Float16)y0;            // q/k/v are fp16 before RoPE (kernels.cu:470)
-  y1 = (float)(_Float16)y1;
+  y0 = (float)(_Float16)(y0 + pre.a);   // q/k/v are fp16 before RoPE (kernels.cu:470)
+  y1 = (float)(_Float16)(y1 + pre.b);
   const int pos = *a.d_pos;
   const int hd = a.head_dim;
-  const int i = r0.row % hd;           // rotation index in [0, hd/2)
   if (r0.mat < 2) {
-    // NeoX rotation of (i, i + hd/2) (kernels.cu:370-398); the angle is
-    // evaluated in double precision.
-    const double freq = 1.0 / pow((double)a.rope_theta, (2.0 * i) / (double)hd);
-    double sn, cs;
-    sincos((double)pos * freq, &sn, &cs);
-    const float c = (float)cs, s = (float)sn;
+    // NeoX rotation of (i, i + hd/2) (kernels.cu:370-398)
+    const double ang = (double)pos * inv_freq[r0.row % hd];
+    const double k = rint(ang * 0.15915494309189535);                        // 1 / (2 pi)
+    const double rd = fma(-k, 6.283185307179586232e+00, ang) - k * 2.4492935982947064e-16;   // 2 pi hi + lo
+    float s, c;
+    sincosf((float)rd, &s, &c);
     const float o0 = add_rn(mul_rn(y0, c), -mul_rn(y1, s));
     const float o1 = add_rn(mul_rn(y1, c), mul_rn(y0, s));
     y0 = o0;
@@ -266,16 +303,18 @@ __device__ __forceinline__ void qkv_pair(const GemvArgs& a, float y0, float y1, 
   }
 }
 
-// Reduce the wave's R row sums and run the epilogue; lane r handles row r
-// (static register indices only, so nothing goes through scratch).
+// Reduce the wave's R row sums, apply the RMSNorm scale, run the epilogue;
+// lane r handles row r (static register indices only, so nothing goes
+// through scratch).
 template <int MODE, int R>
-__device__ __forceinline__ void finish_unit(const GemvArgs& a, float (&acc)[R], int unit, int lane) {
+__device__ __forceinline__ void finish_unit(const GemvArgs& a, float (&acc)[R], int unit, int lane, float scale,
+                                            const EpiPre& pre, const double* inv_freq) {
 #pragma unroll
-  for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
+  for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]) * scale;
   if constexpr (MODE == GM_STORE || MODE == GM_RESID) {
 #pragma unroll
     for (int r = 0; r < R; ++r)
-      if (lane == r) store_row<MODE, R>(a, acc[r], unit, r);
+      if (lane == r) store_row<MODE, R>(a, acc[r], pre.a, unit, r);
   } else if constexpr (MODE == GM_SWIGLU) {
 #pragma unroll
     for (int r = 0; r < R / 2; ++r) {
@@ -291,7 +330,7 @@ __device__ __forceinline__ void finish_unit(const GemvArgs& a, float (&acc)[R], 
   } else {
 #pragma unroll
     for (int r = 0; r < R / 2; ++r)
-      if (lane == r) qkv_pair<MODE, R>(a, acc[r], acc[r + R / 2], unit, r);
+      if (lane == r) qkv_pair<MODE, R>(a, acc[r], acc[r + R / 2], pre, unit, r, inv_freq);
   }
 #pragma unroll
   for (int r = 0; r < R; ++r) acc[r] = 0.f;
@@ -300,14 +339,15 @@ __device__ __forceinline__ void finish_unit(const GemvArgs& a, float (&acc)[R], 
 // Persistent GEMV: wave w owns units w, w + W, w + 2W, ... (W = waves in
 // the grid) and streams its (unit, k-step) sequence; a step is U 16-byte
 // chunks per lane of each of the unit's R rows, all requested before any is
-// used.  The first step is requested before the LDS staging so the input
-// vector prologue overlaps the first HBM round trip.  PIPE additionally
-// requests step s+1 before computing step s.
-template <int Q, int MODE, int R, int U, bool NORM, bool G128, bool PIPE, int BLK>
+// used.  The first step (and its epilogue operands) is requested before the
+// LDS staging so the input-vector prologue overlaps the first HBM round
+// trip.
+template <int Q, int MODE, int R, int U, bool NORM, bool G128, int BLK>
 __global__ __launch_bounds__(BLK) void gemv_kernel(const GemvArgs a) {
   using T = QTraits<Q>;
   extern __shared__ u4_t smem[];
-  __shared__ float red[16];
+  __shared__ float red[BLK / kWave];
+  __shared__ double inv_freq[MODE == GM_QKV ? kMaxHeadDim / 2 : 1];
   const int NC = a.K / T::EPC;
   u4_t* xs = smem;
   float* sx = reinterpret_cast<float*>(smem + T::PLANES * NC);
@@ -323,41 +363,33 @@ __global__ __launch_bounds__(BLK) void gemv_kernel(const GemvArgs a) {
   XStage<Q, NORM> st;
   stage_issue<Q, NORM, BLK>(a, st, 0, NC);
   StepBuf<R, U> A;
-  if (S > 0) load_step<Q, MODE, R, U, G128>(a, A, first, 0, NC, lane);
-  stage_finish<Q, NORM, BLK>(a, st, NC, xs, sx, red);
+  EpiPre pre;
+  if (S > 0) {
+    load_step<Q, MODE, R, U, G128>(a, A, first, 0, NC, lane);
+    pre = epi_prefetch<MODE, R>(a, first, lane);
+  }
+  if constexpr (MODE == GM_QKV) {
+    if (threadIdx.x < a.head_dim / 2)
+      inv_freq[threadIdx.x] = 1.0 / pow((double)a.rope_theta, (2.0 * threadIdx.x) / (double)a.head_dim);
+  }
+  const float scale = stage_finish<Q, NORM, BLK>(a, st, NC, xs, sx, red);
 
   const UnpackRegs uk = unpack_regs();
   float acc[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) acc[r] = 0.f;
-  if constexpr (!PIPE) {
-    for (int s = 0; s < S; ++s) {
-      const int unit = first + (s / NB) * stride, kb = s % NB;
-      if (s > 0) load_step<Q, MODE, R, U, G128>(a, A, unit, kb, NC, lane);
-      compute_step<Q, R, U>(A, acc, xs, sx, kb, NC, lane, uk);
-      if (kb == NB - 1) finish_unit<MODE, R>(a, acc, unit, lane);
+  for (int s = 0; s < S; ++s) {
+    const int unit = first + (s / NB) * stride, kb = s % NB;
+    if (s > 0) {
+      load_step<Q, MODE, R, U, G128>(a, A, unit, kb, NC, lane);
+      if (kb == 0) pre = epi_prefetch<MODE, R>(a, unit, lane);
     }
-  } else {
-    StepBuf<R, U> B;
-    for (int s = 0; s < S; s += 2) {
-      const int u0 = first + (s / NB) * stride, kb0 = s % NB;
-      const bool has1 = s + 1 < S;
-      const int u1 = first + ((s + 1) / NB) * stride, kb1 = (s + 1) % NB;
-      if (has1) load_step<Q, MODE, R, U, G128>(a, B, u1, kb1, NC, lane);
-      __builtin_amdgcn_sched_barrier(0);
-      compute_step<Q, R, U>(A, acc, xs, sx, kb0, NC, lane, uk);
-      if (kb0 == NB - 1) finish_unit<MODE, R>(a, acc, u0, lane);
-      if (!has1) break;
-      if (s + 2 < S) load_step<Q, MODE, R, U, G128>(a, A, first + ((s + 2) / NB) * stride, (s + 2) % NB, NC, lane);
-      __builtin_amdgcn_sched_barrier(0);
-      compute_step<Q, R, U>(B, acc, xs, sx, kb1, NC, lane, uk);
-      if (kb1 == NB - 1) finish_unit<MODE, R>(a, acc, u1, lane);
-    }
+    compute_step<Q, R, U>(A, acc, xs, sx, kb, NC, lane, uk);
+    if (kb == NB - 1) finish_unit<MODE, R>(a, acc, unit, lane, scale, pre, inv_freq);
   }
 }
 
 // ------------------------------------------------------------------ host
-
 int gemv_check(const GemvArgs& a) {
   if (a.quant < 0 || a.quant > 2) return fail(CQ_EINVAL, "gemv: bad quant type");
   if (a.K <= 0 || a.N <= 0) return fail(CQ_EINVAL, "gemv: empty shape");
@@ -372,6 +404,7 @@ int gemv_check(const GemvArgs& a) {
     if (a.head_dim % 4 || a.head_dim > kMaxHeadDim || a.n_heads <= 0 || a.n_kv <= 0 || a.n_heads % a.n_kv)
       return fail(CQ_EINVAL, "gemv: bad head configuration");
     if (!a.W[1] || !a.W[2] || !a.d_pos) return fail(CQ_EINVAL, "gemv: qkv needs q, k, v weights and d_pos");
+    if (a.quant != CQ_QUANT_FP16 && (!a.S[1] || !a.S[2])) return fail(CQ_EINVAL, "gemv: qkv needs q, k, v scales");
     if (a.kcache && a.max_seq % 32) return fail(CQ_EINVAL, "gemv: max_seq must be a multiple of 32");
   } else if (!a.out[0]) {
     return fail(CQ_EINVAL, "gemv: null output");
@@ -385,17 +418,17 @@ int gemv_check(const GemvArgs& a) {
 }
 
 // Tuning of one launch (measured on MI355X at the Qwen2.5-7B INT4 shapes):
-// rows per wave, 16-byte chunks per lane per step, software pipelining,
-// threads per block, and resident blocks per CU of the persistent grid.
+// rows per wave, 16-byte chunks per lane per step, threads per block, and
+// resident blocks per CU of the persistent grid.
 // Fat 1024-thread blocks stage x once per CU for the long GEMVs; the short
 // QKV projection prefers more, smaller blocks.
 template <int MODE> struct GemvTune;
-template <> struct GemvTune<GM_STORE> { static constexpr int R = 4, U = 1, BLK = 1024, PER_CU = 1; static constexpr bool PIPE = false; };
-template <> struct GemvTune<GM_RESID> { static constexpr int R = 1, U = 2, BLK = 1024, PER_CU = 1; static constexpr bool PIPE = false; };
-template <> struct GemvTune<GM_SWIGLU> { static constexpr int R = 2, U = 2, BLK = 1024, PER_CU = 1; static constexpr bool PIPE = false; };
-template <> struct GemvTune<GM_QKV> { static constexpr int R = 2, U = 2, BLK = 256, PER_CU = 4; static constexpr bool PIPE = false; };
+template <> struct GemvTune<GM_STORE> { static constexpr int R = 4, U = 1, BLK = 1024, PER_CU = 1; };
+template <> struct GemvTune<GM_RESID> { static constexpr int R = 1, U = 2, BLK = 1024, PER_CU = 1; };
+template <> struct GemvTune<GM_SWIGLU> { static constexpr int R = 2, U = 2, BLK = 1024, PER_CU = 1; };
+template <> struct GemvTune<GM_QKV> { static constexpr int R = 2, U = 2, BLK = 256, PER_CU = 4; };
 
-template <int Q, int MODE, int R, int U, bool NORM, bool G128, bool PIPE, int BLK = 256>
+template <int Q, int MODE, int R, int U, bool NORM, bool G128, int BLK = 256>
 int launch_variant(const GemvArgs& a, hipStream_t stream, int max_blocks) {
   constexpr int kWavesPerBlock = BLK / kWave;
   using T = QTraits<Q>;
@@ -410,7 +443,7 @@ int launch_variant(const GemvArgs& a, hipStream_t stream, int max_blocks) {
   const int per_wave = (units + max_waves - 1) / max_waves;
   const int waves = (units + per_wave - 1) / per_wave;
   const int blocks = (waves + kWavesPerBlock - 1) / kWavesPerBlock;
-  hipLaunchKernelGGL((gemv_kernel<Q, MODE, R, U, NORM, G128, PIPE, BLK>), dim3(blocks), dim3(BLK), lds, stream, a);
+  hipLaunchKernelGGL((gemv_kernel<Q, MODE, R, U, NORM, G128, BLK>), dim3(blocks), dim3(BLK), lds, stream, a);
   CQ_HIP(hipGetLastError());
   return CQ_OK;
 }
@@ -418,13 +451,19 @@ int launch_variant(const GemvArgs& a, hipStream_t stream, int max_blocks) {
 template <int Q, int MODE, bool NORM, bool G128>
 static int launch_t(const GemvArgs& a, hipStream_t stream) {
   using TN = GemvTune<MODE>;
-  return launch_variant<Q, MODE, TN::R, TN::U, NORM, G128, TN::PIPE, TN::BLK>(a, stream, TN::PER_CU * kNumCUs);
+  return launch_variant<Q, MODE, TN::R, TN::U, NORM, G128, TN::BLK>(a, stream, TN::PER_CU * kNumCUs);
 }
 
 template <int Q, int MODE>
 static int launch_q(const GemvArgs& a, hipStream_t stream) {
   const bool norm = a.norm_w != nullptr;
   if constexpr (MODE == GM_STORE) {
+    // Short matrices (e.g. the 896-row down-projection shape of BASELINE
+    // config 1) need more, smaller blocks than the 150K-row lm_head.
+    if (a.N < 16384 && !norm) {
+      if (a.group == 0) return launch_variant<Q, MODE, 2, 2, false, false, 256>(a, stream, 4 * kNumCUs);
+      return launch_variant<Q, MODE, 2, 2, false, true, 256>(a, stream, 4 * kNumCUs);
+    }
     if (a.group == 0) return norm ? launch_t<Q, MODE, true, false>(a, stream) : launch_t<Q, MODE, false, false>(a, stream);
     return norm ? launch_t<Q, MODE, true, true>(a, stream) : launch_t<Q, MODE, false, true>(a, stream);
   } else if constexpr (MODE == GM_RESID) {
