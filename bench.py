@@ -35,11 +35,26 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-profile", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="also run a 256 MiB device-to-device copy (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     return ap.parse_args()
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
+
+
+def measured_traffic(kernel, model, quant):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc
+    summary for this workload, or None."""
+    path = os.path.join(ROOT, "profiles", f"hbm_traffic_{model.lower()}_{quant}_32k.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        f = line.split()
+        if len(f) == 2 and f[0] == kernel:
+            return int(f[1])
+    return None
 
 
 def gemv_config1(cq, np):
@@ -141,8 +156,9 @@ def main():
         per_tok = {k["kernel"]: k["bytes"] * (cfg.n_layers if k["kernel"] not in ("lm_head", "argmax") else 1)
                    for k in kernels}
         dom = max(kernels, key=lambda k: per_tok[k["kernel"]])
+        traffic = measured_traffic(dom["kernel"], args.model, args.quant) if args.ctx == 32768 else None
         roof = {"bound": "hbm", "kernel": dom["kernel"], "achieved": dom["GBps"], "peak": PEAK_GBPS,
-                "unit": "GB/s", "frac": dom["frac"], "traffic": None,
+                "unit": "GB/s", "frac": dom["frac"], "traffic": traffic,
                 "bytes_per_launch": dom["bytes"], "us_per_launch": dom["us"]}
     g1 = None
     if not args.no_profile:
@@ -150,6 +166,15 @@ def main():
         log(f"[bench] config-1 GEMV: {g1}")
     st.free()
     w.free()
+    if args.calib_copy:
+        n = 256 << 20
+        src, dst = cq.DeviceBuffer(n), cq.DeviceBuffer(n)
+        src.zero()
+        for _ in range(3):
+            cq.check(cq.lib.cq_memcpy_d2d(dst.ptr, src.ptr, n))
+        log(f"[bench] calibration copy: 3 x {n} bytes device-to-device")
+        src.free()
+        dst.free()
 
     cpu = None
     if not args.no_cpu_baseline:

@@ -106,6 +106,7 @@ def _load():
         "cq_memcpy_h2d": (I32, [P, P, SZ]),
         "cq_memcpy_d2h": (I32, [P, P, SZ]),
         "cq_memset": (I32, [P, ctypes.c_int, SZ]),
+        "cq_memcpy_d2d": (I32, [P, P, SZ]),
         "cq_synchronize": (I32, []),
         "cq_embedding_lookup": (I32, [P, P, P, I32, P]),
         "cq_rmsnorm": (I32, [P, P, P, I32, F, P]),
@@ -143,7 +144,7 @@ EXPORTED = [
     "cq_synth_weights", "cq_free_weights", "cq_weights_tensor", "cq_state_create", "cq_state_destroy",
     "cq_forward", "cq_decode", "cq_state_logits", "cq_state_fill_kv", "cq_state_kv_read", "cq_state_kv_write",
     "cq_state_last_decode_us", "cq_synth_normal", "cq_synth_uniform", "cq_tensor_stream_id", "cq_kv_stream_id",
-    "cq_quantize", "cq_device_count", "cq_malloc", "cq_free", "cq_memcpy_h2d", "cq_memcpy_d2h", "cq_memset",
+    "cq_quantize", "cq_device_count", "cq_malloc", "cq_free", "cq_memcpy_h2d", "cq_memcpy_d2h", "cq_memset", "cq_memcpy_d2d",
     "cq_synchronize", "cq_embedding_lookup", "cq_rmsnorm", "cq_gemv", "cq_gemv_add", "cq_fused_attn_block",
     "cq_fused_mlp_stage1", "cq_fused_mlp_stage2", "cq_compute_logits", "cq_apply_repetition_penalty",
     "cq_penalty_workspace_bytes", "cq_argmax", "cq_argmax_workspace_bytes", "cq_kv_k_offset", "cq_kv_v_offset",

@@ -32,6 +32,10 @@ extern "C" int cq_memcpy_d2h(void* dst, const void* src, size_t bytes) {
   CQ_HIP(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
   return CQ_OK;
 }
+extern "C" int cq_memcpy_d2d(void* dst, const void* src, size_t bytes) {
+  CQ_HIP(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToDevice));
+  return CQ_OK;
+}
 extern "C" int cq_memset(void* p, int value, size_t bytes) {
   CQ_HIP(hipMemset(p, value, bytes));
   return CQ_OK;

@@ -174,6 +174,7 @@ int cq_free(void* dptr);
 int cq_memcpy_h2d(void* dst, const void* src, size_t bytes);
 int cq_memcpy_d2h(void* dst, const void* src, size_t bytes);
 int cq_memset(void* dptr, int value, size_t bytes);
+int cq_memcpy_d2d(void* dst, const void* src, size_t bytes);
 int cq_synchronize(void);
 
 /* ------------------------------------------------------------ op level */
