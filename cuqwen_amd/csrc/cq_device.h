@@ -62,15 +62,37 @@ __device__ __forceinline__ uint32_t int8_pair(uint32_t flipped, uint32_t magic_v
 }
 
 // ------------------------------------------------------------- reductions
+// Wave-wide reductions on DPP lane moves: four in-row steps (quad swaps,
+// half-row and row mirrors) leave every lane of a 16-lane row holding the
+// row's result, then the four row results are combined through scalar
+// registers.  Every lane ends with the bitwise-identical value (each step
+// combines the same two operands on both lanes of a pair), and nothing goes
+// through LDS, unlike a shuffle (ds_bpermute) butterfly.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float lane_of(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+constexpr int kDppQuadSwap1 = 0xB1;      // quad_perm [1,0,3,2]
+constexpr int kDppQuadSwap2 = 0x4E;      // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppRowMirror = 0x140;
+
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
-  return v;
+  v += dpp_mov<kDppQuadSwap1>(v);
+  v += dpp_mov<kDppQuadSwap2>(v);
+  v += dpp_mov<kDppRowHalfMirror>(v);
+  v += dpp_mov<kDppRowMirror>(v);
+  return (lane_of(v, 0) + lane_of(v, 16)) + (lane_of(v, 32) + lane_of(v, 48));
 }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
-  return v;
+  v = fmaxf(v, dpp_mov<kDppQuadSwap1>(v));
+  v = fmaxf(v, dpp_mov<kDppQuadSwap2>(v));
+  v = fmaxf(v, dpp_mov<kDppRowHalfMirror>(v));
+  v = fmaxf(v, dpp_mov<kDppRowMirror>(v));
+  return fmaxf(fmaxf(lane_of(v, 0), lane_of(v, 16)), fmaxf(lane_of(v, 32), lane_of(v, 48)));
 }
 
 // Block-wide sum for blockDim.x a multiple of 64 (<= 1024); `red` holds 16

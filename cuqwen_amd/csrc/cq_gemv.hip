@@ -10,35 +10,47 @@ constexpr int kNumCUs = 256;   // MI355X
 
 template <int Q> __device__ __forceinline__ constexpr bool quantized() { return Q != CQ_QUANT_FP16; }
 
-// x staging.  Each thread owns chunks c = tid + i*BLK (i < XB) of a
-// batch; all of a batch's x (and norm-weight) loads are issued at once, so
-// the prologue costs one memory round trip per batch (one batch whenever the
-// RMSNorm is fused: K <= 16384).  The LDS image is PLANES planes of 16-byte
-// chunk slices (bank-conflict-free 16-byte reads in the main loop) plus the
-// per-chunk unpack-bias term.
+// x staging.  Thread t owns chunks c = t + i*BLK (i < XB) of a batch; all
+// of a batch's x (and norm-weight) loads are issued at once, so the prologue
+// costs one memory round trip per batch (one batch whenever the RMSNorm is
+// fused: K <= kNormMaxK).  A wave whose chunks all lie past the end skips
+// its loads (a wave-uniform branch); in the wave that holds the end, lanes
+// past it re-read the last chunk, so the code inside stays straight-line.
+// The LDS image is PLANES planes of 16-byte chunk slices (bank-conflict-free
+// 16-byte reads in the main loop) plus the per-chunk unpack-bias term.
 //
 // Fused RMSNorm (kernels.cu:689-751): the staged vector is half(x * w) and
 // the scalar rsqrt(mean(x^2) + eps) multiplies each finished row sum, so the
 // block reduction of x^2 rides on the staging barrier instead of adding a
 // dependent step before the weights can be consumed.  (The reference rounds
 // x * inv * w to fp16; here x * w is rounded and inv applied in fp32.)
-template <int Q, bool NORM>
+constexpr int kNormMaxK = 16384;
+
+template <int Q, bool NORM, int BLK>
 struct XStage {
   static constexpr int P = QTraits<Q>::PLANES;
-  static constexpr int XB = 8 / P;   // chunks per thread per batch (64 elements)
+  static constexpr int XB = NORM ? (kNormMaxK / QTraits<Q>::EPC + BLK - 1) / BLK : 1;
   u4_t x[XB][P];
   u4_t w[NORM ? XB : 1][P];
 };
 
+// first chunk of slot i of `batch` for the calling wave (wave-uniform)
 template <int Q, bool NORM, int BLK>
-__device__ __forceinline__ void stage_issue(const GemvArgs& a, XStage<Q, NORM>& st, int batch, int NC) {
+__device__ __forceinline__ int stage_base(int batch, int i) {
+  return (batch * XStage<Q, NORM, BLK>::XB + i) * BLK + __builtin_amdgcn_readfirstlane(threadIdx.x & ~(kWave - 1));
+}
+
+template <int Q, bool NORM, int BLK>
+__device__ __forceinline__ void stage_issue(const GemvArgs& a, XStage<Q, NORM, BLK>& st, int batch, int NC) {
   using T = QTraits<Q>;
   const _Float16* x = reinterpret_cast<const _Float16*>(a.x);
   const _Float16* nw = reinterpret_cast<const _Float16*>(a.norm_w);
+  const int lane = threadIdx.x & (kWave - 1);
 #pragma unroll
-  for (int i = 0; i < XStage<Q, NORM>::XB; ++i) {
-    const int c = (batch * XStage<Q, NORM>::XB + i) * BLK + threadIdx.x;
-    if (c < NC) {
+  for (int i = 0; i < XStage<Q, NORM, BLK>::XB; ++i) {
+    const int c0 = stage_base<Q, NORM, BLK>(batch, i);
+    if (c0 < NC) {
+      const int c = min(c0 + lane, NC - 1);
 #pragma unroll
       for (int p = 0; p < T::PLANES; ++p) {
         st.x[i][p] = load_u4(x + c * T::EPC + p * 8);
@@ -49,50 +61,57 @@ __device__ __forceinline__ void stage_issue(const GemvArgs& a, XStage<Q, NORM>& 
 }
 
 template <int Q, bool NORM, int BLK>
-__device__ __forceinline__ void stage_write(const XStage<Q, NORM>& st, int batch, int NC, u4_t* xs, float* sx) {
+__device__ __forceinline__ void stage_write(const XStage<Q, NORM, BLK>& st, int batch, int NC, u4_t* xs, float* sx) {
   using T = QTraits<Q>;
+  const int lane = threadIdx.x & (kWave - 1);
 #pragma unroll
-  for (int i = 0; i < XStage<Q, NORM>::XB; ++i) {
-    const int c = (batch * XStage<Q, NORM>::XB + i) * BLK + threadIdx.x;
-    if (c < NC) {
-      float corr = 0.f;
+  for (int i = 0; i < XStage<Q, NORM, BLK>::XB; ++i) {
+    const int c0 = stage_base<Q, NORM, BLK>(batch, i);
+    if (c0 >= NC) continue;
+    // lanes past the end write chunk NC-1 again with the identical value
+    const int c = min(c0 + lane, NC - 1);
+    float corr = 0.f;
+    u4_t planes[T::PLANES];
 #pragma unroll
-      for (int p = 0; p < T::PLANES; ++p) {
-        const h8_t xv = __builtin_bit_cast(h8_t, st.x[i][p]);
-        float v[8];
-        if constexpr (NORM) {
-          const h8_t wv = __builtin_bit_cast(h8_t, st.w[i][p]);
+    for (int p = 0; p < T::PLANES; ++p) {
+      const h8_t xv = __builtin_bit_cast(h8_t, st.x[i][p]);
+      float v[8];
+      if constexpr (NORM) {
+        const h8_t wv = __builtin_bit_cast(h8_t, st.w[i][p]);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) v[e] = (float)(_Float16)((float)xv[e] * (float)wv[e]);
-        } else {
+        for (int e = 0; e < 8; ++e) v[e] = (float)(_Float16)((float)xv[e] * (float)wv[e]);
+      } else {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) v[e] = (float)xv[e];
-        }
-        _Float16 o[8];
-        corr += plane_order<Q>(v, o);
-        h8_t ov;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) ov[e] = o[e];
-        xs[p * NC + c] = __builtin_bit_cast(u4_t, ov);
+        for (int e = 0; e < 8; ++e) v[e] = (float)xv[e];
       }
-      if constexpr (quantized<Q>()) sx[c] = corr;
+      _Float16 o[8];
+      corr += plane_order<Q>(v, o);
+      h8_t ov;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ov[e] = o[e];
+      planes[p] = __builtin_bit_cast(u4_t, ov);
     }
+#pragma unroll
+    for (int p = 0; p < T::PLANES; ++p) xs[p * NC + c] = planes[p];
+    if constexpr (quantized<Q>()) sx[c] = corr;
   }
 }
 
 // Finishes the staging whose batch 0 was issued with stage_issue; returns
 // the RMSNorm scale (1 without NORM).  `red` holds BLK/64 floats of LDS.
 template <int Q, bool NORM, int BLK>
-__device__ __forceinline__ float stage_finish(const GemvArgs& a, XStage<Q, NORM>& st, int NC, u4_t* xs, float* sx,
+__device__ __forceinline__ float stage_finish(const GemvArgs& a, XStage<Q, NORM, BLK>& st, int NC, u4_t* xs, float* sx,
                                               float* red) {
   using T = QTraits<Q>;
+  using XS = XStage<Q, NORM, BLK>;
   if constexpr (NORM) {
     // one batch holds all of x (host-checked)
+    const int lane = threadIdx.x & (kWave - 1);
     float ss = 0.f;
 #pragma unroll
-    for (int i = 0; i < XStage<Q, NORM>::XB; ++i) {
-      const int c = i * BLK + threadIdx.x;
-      if (c < NC) {
+    for (int i = 0; i < XS::XB; ++i) {
+      const int c0 = stage_base<Q, NORM, BLK>(0, i);
+      if (c0 < NC && c0 + lane < NC) {
 #pragma unroll
         for (int p = 0; p < T::PLANES; ++p) {
           const h8_t xv = __builtin_bit_cast(h8_t, st.x[i][p]);
@@ -102,11 +121,10 @@ __device__ __forceinline__ float stage_finish(const GemvArgs& a, XStage<Q, NORM>
       }
     }
     ss = wave_sum(ss);
-    if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = ss;
+    if (lane == 0) red[threadIdx.x / kWave] = ss;
   }
   stage_write<Q, NORM, BLK>(st, 0, NC, xs, sx);
-  const int per_batch = XStage<Q, NORM>::XB * BLK;
-  for (int b = 1; b * per_batch < NC; ++b) {
+  for (int b = 1; b * XS::XB * BLK < NC; ++b) {
     stage_issue<Q, NORM, BLK>(a, st, b, NC);
     stage_write<Q, NORM, BLK>(st, b, NC, xs, sx);
   }
@@ -127,6 +145,15 @@ __device__ __forceinline__ int units_total(const GemvArgs& a) {
   if constexpr (MODE == GM_SWIGLU) return (a.N + R / 2 - 1) / (R / 2);
   else if constexpr (MODE == GM_QKV) return (a.n_heads + 2 * a.n_kv) * (a.head_dim / 2) / (R / 2);
   else return (a.N + R - 1) / R;
+}
+
+// Pointer `i` of a 3-entry kernel-argument array.  Written as selects so the
+// pointers stay in scalar registers; indexing the array with a run-time
+// value makes the compiler re-load it from kernarg memory with a vector load
+// and a full vmcnt(0) wait, which would serialise the prologue's loads.
+template <typename T>
+__device__ __forceinline__ T sel3(T const (&arr)[3], int i) {
+  return i == 0 ? arr[0] : (i == 1 ? arr[1] : arr[2]);
 }
 
 struct RowRef {
@@ -180,9 +207,9 @@ __device__ __forceinline__ void load_step(const GemvArgs& a, StepBuf<R, U>& b, i
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const RowRef rr = row_of<MODE, R>(a, unit, r);
-    const char* rp = reinterpret_cast<const char*>(a.W[rr.mat]) + (int64_t)rr.row * rbytes;
+    const char* rp = reinterpret_cast<const char*>(sel3(a.W, rr.mat)) + (int64_t)rr.row * rbytes;
     const _Float16* sp = nullptr;
-    if constexpr (quantized<Q>()) sp = reinterpret_cast<const _Float16*>(a.S[rr.mat]) + (int64_t)rr.row * sstride;
+    if constexpr (quantized<Q>()) sp = reinterpret_cast<const _Float16*>(sel3(a.S, rr.mat)) + (int64_t)rr.row * sstride;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int c = min(kb * (kWave * U) + u * kWave + lane, NC - 1);
@@ -220,26 +247,31 @@ __device__ __forceinline__ void compute_step(const StepBuf<R, U>& b, float (&acc
 // the residual x[row] (RESID) or the bias (STORE); in QKV mode lane i < R/2
 // holds the biases of its rotation pair.
 struct EpiPre {
-  float a = 0.f, b = 0.f;
+  uint32_t a = 0, b = 0;   // raw fp16 bits, zero-extended; converted where used
 };
+__device__ __forceinline__ float epi_f(uint32_t bits) { return (float)__builtin_bit_cast(_Float16, (uint16_t)bits); }
+__device__ __forceinline__ uint32_t ld_u16(const void* p) { return *reinterpret_cast<const uint16_t*>(p); }
 
 template <int MODE, int R>
 __device__ __forceinline__ EpiPre epi_prefetch(const GemvArgs& a, int unit, int lane) {
+  // Every lane loads from a valid address (lanes past R re-read row R-1;
+  // a missing bias reads x[0] and is ignored at use), so the loads are
+  // unconditional and the compiler's load counters stay exact.
   EpiPre e;
   if constexpr (MODE == GM_STORE || MODE == GM_RESID) {
-    if (lane < R) {
-      const RowRef me = row_of<MODE, R>(a, unit, lane);
-      if constexpr (MODE == GM_RESID) e.a = (float)reinterpret_cast<const _Float16*>(a.out[0])[me.row];
-      else if (a.bias[0]) e.a = (float)reinterpret_cast<const _Float16*>(a.bias[0])[me.row];
-    }
+    const RowRef me = row_of<MODE, R>(a, unit, min(lane, R - 1));
+    if constexpr (MODE == GM_RESID) e.a = ld_u16(reinterpret_cast<const _Float16*>(a.out[0]) + me.row);
+    else e.a = ld_u16(a.bias[0] ? reinterpret_cast<const _Float16*>(a.bias[0]) + me.row
+                                : reinterpret_cast<const _Float16*>(a.x));
   } else if constexpr (MODE == GM_QKV) {
     constexpr int PP = R / 2;
-    if (lane < PP) {
-      const RowRef r0 = row_of<MODE, R>(a, unit, lane);
-      const RowRef r1 = row_of<MODE, R>(a, unit, lane + PP);
-      const _Float16* b = reinterpret_cast<const _Float16*>(a.bias[r0.mat]);
-      if (b) { e.a = (float)b[r0.row]; e.b = (float)b[r1.row]; }
-    }
+    const int i = min(lane, PP - 1);
+    const RowRef r0 = row_of<MODE, R>(a, unit, i);
+    const RowRef r1 = row_of<MODE, R>(a, unit, i + PP);
+    const _Float16* b = reinterpret_cast<const _Float16*>(sel3(a.bias, r0.mat));
+    const _Float16* x0 = reinterpret_cast<const _Float16*>(a.x);
+    e.a = ld_u16(b ? b + r0.row : x0);
+    e.b = ld_u16(b ? b + r1.row : x0);
   }
   return e;
 }
@@ -271,8 +303,9 @@ __device__ __forceinline__ void qkv_pair(const GemvArgs& a, float y0, float y1, 
   constexpr int PP = R / 2;
   const RowRef r0 = row_of<MODE, R>(a, unit, i_pair);
   const RowRef r1 = row_of<MODE, R>(a, unit, i_pair + PP);
-  y0 = (float)(_Float16)(y0 + pre.a);   // q/k/v are fp16 before RoPE (kernels.cu:470)
-  y1 = (float)(_Float16)(y1 + pre.b);
+  const bool has_bias = sel3(a.bias, r0.mat) != nullptr;
+  y0 = (float)(_Float16)(y0 + (has_bias ? epi_f(pre.a) : 0.f));   // q/k/v are fp16 before RoPE (kernels.cu:470)
+  y1 = (float)(_Float16)(y1 + (has_bias ? epi_f(pre.b) : 0.f));
   const int pos = *a.d_pos;
   const int hd = a.head_dim;
   if (r0.mat < 2) {
@@ -288,7 +321,7 @@ __device__ __forceinline__ void qkv_pair(const GemvArgs& a, float y0, float y1, 
     y1 = o1;
   }
   const _Float16 h0 = (_Float16)y0, h1 = (_Float16)y1;
-  _Float16* out = reinterpret_cast<_Float16*>(a.out[r0.mat]);
+  _Float16* out = reinterpret_cast<_Float16*>(sel3(a.out, r0.mat));
   if (out) { out[r0.row] = h0; out[r1.row] = h1; }
   if (r0.mat > 0 && a.kcache) {
     const int kvh = r0.row / hd, d0 = r0.row % hd, d1 = r1.row % hd;
@@ -314,7 +347,8 @@ __device__ __forceinline__ void finish_unit(const GemvArgs& a, float (&acc)[R], 
   if constexpr (MODE == GM_STORE || MODE == GM_RESID) {
 #pragma unroll
     for (int r = 0; r < R; ++r)
-      if (lane == r) store_row<MODE, R>(a, acc[r], pre.a, unit, r);
+      if (lane == r)
+        store_row<MODE, R>(a, acc[r], (MODE == GM_RESID || a.bias[0]) ? epi_f(pre.a) : 0.f, unit, r);
   } else if constexpr (MODE == GM_SWIGLU) {
 #pragma unroll
     for (int r = 0; r < R / 2; ++r) {
@@ -338,10 +372,13 @@ __device__ __forceinline__ void finish_unit(const GemvArgs& a, float (&acc)[R], 
 
 // Persistent GEMV: wave w owns units w, w + W, w + 2W, ... (W = waves in
 // the grid) and streams its (unit, k-step) sequence; a step is U 16-byte
-// chunks per lane of each of the unit's R rows, all requested before any is
-// used.  The first step (and its epilogue operands) is requested before the
-// LDS staging so the input-vector prologue overlaps the first HBM round
-// trip.
+// chunks per lane of each of the unit's R rows.  Two step buffers rotate:
+// while one step is reduced the next one's loads are in flight, so a wave
+// always has a step outstanding instead of paying one HBM round trip per
+// step.  The first two steps (and their epilogue operands) are requested
+// before the LDS staging so the input-vector prologue overlaps them.  Every
+// load is unconditional (step indices are clamped to the wave's last step),
+// keeping the code straight-line and the compiler's load counters exact.
 template <int Q, int MODE, int R, int U, bool NORM, bool G128, int BLK>
 __global__ __launch_bounds__(BLK) void gemv_kernel(const GemvArgs a) {
   using T = QTraits<Q>;
@@ -354,20 +391,28 @@ __global__ __launch_bounds__(BLK) void gemv_kernel(const GemvArgs a) {
   const int lane = threadIdx.x & (kWave - 1);
   const int n_units = units_total<MODE, R>(a);
   constexpr int WPB = BLK / kWave;
-  const int first = blockIdx.x * WPB + threadIdx.x / kWave;
+  // wave index through readfirstlane: the compiler then knows every
+  // per-unit quantity is wave-uniform and keeps the unit / k-step / row
+  // address arithmetic in scalar registers (and the loop a scalar loop)
+  const int first = blockIdx.x * WPB + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int stride = gridDim.x * WPB;
   const int NB = (NC + kWave * U - 1) / (kWave * U);
   const int my_units = first < n_units ? (n_units - first + stride - 1) / stride : 0;
   const int S = my_units * NB;
+  // (unit, k-step) of step s, clamped to the wave's last step (a wave with
+  // no work reads the last unit's first step)
+  const int s_max = max(S - 1, 0);
+  const int base = S > 0 ? first : n_units - 1;
+  auto unit_of = [&](int s) { return base + (min(s, s_max) / NB) * stride; };
+  auto kb_of = [&](int s) { return min(s, s_max) % NB; };
 
-  XStage<Q, NORM> st;
+  XStage<Q, NORM, BLK> st;
   stage_issue<Q, NORM, BLK>(a, st, 0, NC);
-  StepBuf<R, U> A;
-  EpiPre pre;
-  if (S > 0) {
-    load_step<Q, MODE, R, U, G128>(a, A, first, 0, NC, lane);
-    pre = epi_prefetch<MODE, R>(a, first, lane);
-  }
+  StepBuf<R, U> A, B;
+  load_step<Q, MODE, R, U, G128>(a, A, unit_of(0), kb_of(0), NC, lane);
+  EpiPre pa = epi_prefetch<MODE, R>(a, unit_of(0), lane);
+  load_step<Q, MODE, R, U, G128>(a, B, unit_of(1), kb_of(1), NC, lane);
+  EpiPre pb = epi_prefetch<MODE, R>(a, unit_of(1), lane);
   if constexpr (MODE == GM_QKV) {
     if (threadIdx.x < a.head_dim / 2)
       inv_freq[threadIdx.x] = 1.0 / pow((double)a.rope_theta, (2.0 * threadIdx.x) / (double)a.head_dim);
@@ -378,14 +423,22 @@ __global__ __launch_bounds__(BLK) void gemv_kernel(const GemvArgs a) {
   float acc[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) acc[r] = 0.f;
-  for (int s = 0; s < S; ++s) {
-    const int unit = first + (s / NB) * stride, kb = s % NB;
-    if (s > 0) {
-      load_step<Q, MODE, R, U, G128>(a, A, unit, kb, NC, lane);
-      if (kb == 0) pre = epi_prefetch<MODE, R>(a, unit, lane);
+  for (int s = 0; s < S; s += 2) {
+    {
+      const int unit = unit_of(s), kb = kb_of(s);
+      compute_step<Q, R, U>(A, acc, xs, sx, kb, NC, lane, uk);
+      if (kb == NB - 1) finish_unit<MODE, R>(a, acc, unit, lane, scale, pa, inv_freq);
+      load_step<Q, MODE, R, U, G128>(a, A, unit_of(s + 2), kb_of(s + 2), NC, lane);
+      pa = epi_prefetch<MODE, R>(a, unit_of(s + 2), lane);
     }
-    compute_step<Q, R, U>(A, acc, xs, sx, kb, NC, lane, uk);
-    if (kb == NB - 1) finish_unit<MODE, R>(a, acc, unit, lane, scale, pre, inv_freq);
+    if (s + 1 >= S) break;
+    {
+      const int unit = unit_of(s + 1), kb = kb_of(s + 1);
+      compute_step<Q, R, U>(B, acc, xs, sx, kb, NC, lane, uk);
+      if (kb == NB - 1) finish_unit<MODE, R>(a, acc, unit, lane, scale, pb, inv_freq);
+      load_step<Q, MODE, R, U, G128>(a, B, unit_of(s + 3), kb_of(s + 3), NC, lane);
+      pb = epi_prefetch<MODE, R>(a, unit_of(s + 3), lane);
+    }
   }
 }
 
@@ -413,7 +466,7 @@ int gemv_check(const GemvArgs& a) {
   const int epc = a.quant == CQ_QUANT_INT4 ? 32 : a.quant == CQ_QUANT_INT8 ? 16 : 8;
   const size_t lds = (size_t)planes * (a.K / epc) * 16 + (a.quant ? (size_t)(a.K / epc) * 4 : 0);
   if (lds > 60 * 1024) return fail(CQ_EINVAL, "gemv: input vector too long for LDS staging");
-  if (a.norm_w && a.K > 16384) return fail(CQ_EINVAL, "gemv: fused RMSNorm supports K <= 16384");
+  if (a.norm_w && a.K > kNormMaxK) return fail(CQ_EINVAL, "gemv: fused RMSNorm supports K <= 16384");
   return CQ_OK;
 }
 
@@ -423,10 +476,10 @@ int gemv_check(const GemvArgs& a) {
 // Fat 1024-thread blocks stage x once per CU for the long GEMVs; the short
 // QKV projection prefers more, smaller blocks.
 template <int MODE> struct GemvTune;
-template <> struct GemvTune<GM_STORE> { static constexpr int R = 4, U = 1, BLK = 1024, PER_CU = 1; };
+template <> struct GemvTune<GM_STORE> { static constexpr int R = 2, U = 2, BLK = 1024, PER_CU = 1; };
 template <> struct GemvTune<GM_RESID> { static constexpr int R = 1, U = 2, BLK = 1024, PER_CU = 1; };
-template <> struct GemvTune<GM_SWIGLU> { static constexpr int R = 2, U = 2, BLK = 1024, PER_CU = 1; };
-template <> struct GemvTune<GM_QKV> { static constexpr int R = 2, U = 2, BLK = 256, PER_CU = 4; };
+template <> struct GemvTune<GM_SWIGLU> { static constexpr int R = 2, U = 1, BLK = 1024, PER_CU = 1; };
+template <> struct GemvTune<GM_QKV> { static constexpr int R = 2, U = 1, BLK = 256, PER_CU = 4; };
 
 template <int Q, int MODE, int R, int U, bool NORM, bool G128, int BLK = 256>
 int launch_variant(const GemvArgs& a, hipStream_t stream, int max_blocks) {
