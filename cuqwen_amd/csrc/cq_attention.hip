@@ -17,8 +17,8 @@
 //     tile feeds the P^T operand without any cross-lane movement;
 //   * the 8 waves merge in LDS and the block writes one (m, l, O) partial
 //     (or, with a single partition, the output itself);
-//   * stage 2: one block per query head merges the partials with the
-//     log-sum-exp rule (kernels.cu:222-288).  A separate launch is cheaper on
+//   * stage 2: one wave per (query head, 16-dim slice) merges the partials
+//     with the log-sum-exp rule (kernels.cu:222-288).  A separate launch is cheaper on
 //     this part than an in-kernel completion ticket plus device-scope fences.
 // Rounding follows the reference: scores are rounded to fp16 after the
 // 1/sqrt(hd) scale (kernels.cu:171), probabilities are rounded to fp16 for
@@ -221,74 +221,56 @@ __global__ __launch_bounds__(kAttnThreads) void attention_stage1(const AttnArgs 
   }
 }
 
-// One block per query head: log-sum-exp merge of the partitions
-// (kernels.cu:222-288) with 1/(L + 1e-9).  Every partial this block needs
-// (m, l and its share of O) is requested up front, so the merge costs one
-// memory round trip.
-constexpr int kMergeThreads = 256;
+// Stage 2: log-sum-exp merge of the partitions (kernels.cu:222-288) with
+// 1/(L + 1e-9).  One wave per (query head, 16-dim slice), so the few MB of
+// partials are spread over n_heads * hd/16 CUs instead of n_heads; lane p
+// holds partition p (64 partitions per round, merged into a running
+// (M, L, O) when there are more), and every load of a round is issued
+// before any is used.  The sums are DPP wave reductions.
+constexpr int kMergeDims = 16;
 template <int HD>
-__global__ __launch_bounds__(kMergeThreads) void attention_stage2(const AttnArgs a, int Pmax) {
-  constexpr int PG = kMergeThreads / HD;            // partition groups (2 for hd 128, 4 for hd 64)
-  constexpr int MAXQ = 32;                          // partitions per thread per round
+__global__ __launch_bounds__(kWave) void attention_stage2(const AttnArgs a, int Pmax) {
   const int T = *a.d_pos + 1;
   int tpp;
   const int nparts = attn_nparts(T, Pmax, &tpp);
   if (nparts == 1) return;   // stage 1 wrote the output
-  const int hq = blockIdx.x;
+  constexpr int NS = HD / kMergeDims;
+  const int hq = blockIdx.x / NS, d0 = (blockIdx.x % NS) * kMergeDims;
   const int g = a.n_heads / a.n_kv;
   const int kvh = hq / g, hh = hq % g;
+  const int lane = threadIdx.x;
   const float* ws_m = reinterpret_cast<const float*>(a.workspace);
   const float* ws_l = ws_m + (size_t)a.n_kv * Pmax * 16;
   const float* ws_o = ws_l + (size_t)a.n_kv * Pmax * 16;
   const size_t base = (size_t)kvh * Pmax;
-  const int p = threadIdx.x;
-  const int d = threadIdx.x % HD, pg = threadIdx.x / HD;
-  // issue every load first
-  const float mp = p < nparts ? ws_m[(base + p) * 16 + hh] : -INFINITY;
-  const float lp = p < nparts ? ws_l[(base + p) * 16 + hh] : 0.f;
-  float ov[MAXQ];
+  float M = -INFINITY, L = 0.f, O[kMergeDims];
 #pragma unroll
-  for (int i = 0; i < MAXQ; ++i) {
-    const int q = pg + i * PG;
-    ov[i] = q < nparts ? ws_o[((base + q) * 16 + hh) * HD + d] : 0.f;
+  for (int i = 0; i < kMergeDims; ++i) O[i] = 0.f;
+  for (int p0 = 0; p0 < nparts; p0 += kWave) {
+    const int p = p0 + lane;
+    const int pc = min(p, nparts - 1);   // clamped: every lane loads, invalid lanes get weight 0
+    const size_t slot = (base + pc) * 16 + hh;
+    const float mp = ws_m[slot], lp = ws_l[slot];
+    f4_t ov[kMergeDims / 4];
+    const f4_t* op = reinterpret_cast<const f4_t*>(ws_o + slot * HD + d0);
+#pragma unroll
+    for (int i = 0; i < kMergeDims / 4; ++i) ov[i] = op[i];
+    const float mv = p < nparts ? mp : -INFINITY;
+    const float Mn = fmaxf(M, wave_max(mv));
+    const float f = M == -INFINITY ? 0.f : __expf(M - Mn);
+    const float w = (p < nparts && mp != -INFINITY) ? __expf(mp - Mn) : 0.f;
+    L = L * f + wave_sum(lp * w);
+#pragma unroll
+    for (int i = 0; i < kMergeDims / 4; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) O[4 * i + e] = O[4 * i + e] * f + wave_sum(ov[i][e] * w);
+    M = Mn;
   }
-  // (one round covers nparts <= 32 * PG; larger counts take more rounds below)
-  __shared__ float pw[kAttnBlocksTarget];
-  __shared__ float red[16];
-  __shared__ float part_o[PG][HD];
-  float M = wave_max(mp);
-  if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = M;
-  __syncthreads();
-  M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  const float wgt = p < nparts ? __expf(mp - M) : 0.f;
-  pw[p] = wgt;
-  const float L = block_sum(lp * wgt, red);   // its first barrier also publishes pw
-  float acc = 0.f;
+  const float inv = 1.0f / (L + 1e-9f);
+  _Float16* out = reinterpret_cast<_Float16*>(a.out) + (int64_t)hq * HD + d0;
 #pragma unroll
-  for (int i = 0; i < MAXQ; ++i) {
-    const int q = pg + i * PG;
-    if (q < nparts) acc += ov[i] * pw[q];
-  }
-  for (int r0 = MAXQ * PG; r0 < nparts; r0 += MAXQ * PG) {
-#pragma unroll
-    for (int i = 0; i < MAXQ; ++i) {
-      const int q = r0 + pg + i * PG;
-      ov[i] = q < nparts ? ws_o[((base + q) * 16 + hh) * HD + d] : 0.f;
-    }
-#pragma unroll
-    for (int i = 0; i < MAXQ; ++i) {
-      const int q = r0 + pg + i * PG;
-      if (q < nparts) acc += ov[i] * pw[q];
-    }
-  }
-  part_o[pg][d] = acc;
-  __syncthreads();
-  if (pg == 0) {
-    float O = 0.f;
-#pragma unroll
-    for (int i = 0; i < PG; ++i) O += part_o[i][d];
-    reinterpret_cast<_Float16*>(a.out)[(int64_t)hq * HD + d] = (_Float16)(O * (1.0f / (L + 1e-9f)));
-  }
+  for (int i = 0; i < kMergeDims; ++i)
+    if (lane == i) out[i] = (_Float16)(O[i] * inv);
 }
 
 int launch_attention(const AttnArgs& a, hipStream_t stream) {
@@ -302,10 +284,10 @@ int launch_attention(const AttnArgs& a, hipStream_t stream) {
   const dim3 grid(P, a.n_kv);
   if (a.head_dim == 128) {
     hipLaunchKernelGGL(attention_stage1<128>, grid, dim3(kAttnThreads), 0, stream, a);
-    hipLaunchKernelGGL(attention_stage2<128>, dim3(a.n_heads), dim3(kMergeThreads), 0, stream, a, P);
+    hipLaunchKernelGGL(attention_stage2<128>, dim3(a.n_heads * (128 / kMergeDims)), dim3(kWave), 0, stream, a, P);
   } else {
     hipLaunchKernelGGL(attention_stage1<64>, grid, dim3(kAttnThreads), 0, stream, a);
-    hipLaunchKernelGGL(attention_stage2<64>, dim3(a.n_heads), dim3(kMergeThreads), 0, stream, a, P);
+    hipLaunchKernelGGL(attention_stage2<64>, dim3(a.n_heads * (64 / kMergeDims)), dim3(kWave), 0, stream, a, P);
   }
   CQ_HIP(hipGetLastError());
   return CQ_OK;

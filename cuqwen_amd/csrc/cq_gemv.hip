@@ -370,21 +370,33 @@ __device__ __forceinline__ void finish_unit(const GemvArgs& a, float (&acc)[R], 
   for (int r = 0; r < R; ++r) acc[r] = 0.f;
 }
 
-// Persistent GEMV: wave w owns units w, w + W, w + 2W, ... (W = waves in
-// the grid) and streams its (unit, k-step) sequence; a step is U 16-byte
-// chunks per lane of each of the unit's R rows.  Two step buffers rotate:
-// while one step is reduced the next one's loads are in flight, so a wave
-// always has a step outstanding instead of paying one HBM round trip per
-// step.  The first two steps (and their epilogue operands) are requested
-// before the LDS staging so the input-vector prologue overlaps them.  Every
-// load is unconditional (step indices are clamped to the wave's last step),
-// keeping the code straight-line and the compiler's load counters exact.
+// Step cursor of one wave: which (unit, k-step) a step buffer holds and
+// whether it is real work (a cursor past the block's range still names a
+// valid unit, so its loads stay unconditional, but is never computed).
+struct Cursor {
+  int unit, kb;
+  bool real;
+};
+
+// Persistent GEMV.  Block b owns the contiguous unit range
+// [b*n/G, (b+1)*n/G); inside the block, wave w starts on units begin + w and
+// begin + WPB + w and then claims further units from an LDS counter.  The
+// claiming matters: a SIMD issues its oldest wave first, so with a static
+// split the youngest waves of every SIMD finish far behind the oldest and
+// the SIMD spends its last microseconds with few loads in flight; claimed
+// units let early waves take over their share.  A step is U 16-byte chunks
+// per lane of each of the unit's R rows.  Two step buffers rotate: while one
+// step is reduced the next one's loads are in flight.  The first two steps
+// (and their epilogue operands) are requested before the LDS staging so the
+// input-vector prologue overlaps them.  Every load is unconditional, keeping
+// the code straight-line and the compiler's load counters exact.
 template <int Q, int MODE, int R, int U, bool NORM, bool G128, int BLK>
 __global__ __launch_bounds__(BLK) void gemv_kernel(const GemvArgs a) {
   using T = QTraits<Q>;
   extern __shared__ u4_t smem[];
   __shared__ float red[BLK / kWave];
   __shared__ double inv_freq[MODE == GM_QKV ? kMaxHeadDim / 2 : 1];
+  __shared__ int next_unit;
   const int NC = a.K / T::EPC;
   u4_t* xs = smem;
   float* sx = reinterpret_cast<float*>(smem + T::PLANES * NC);
@@ -394,25 +406,46 @@ __global__ __launch_bounds__(BLK) void gemv_kernel(const GemvArgs a) {
   // wave index through readfirstlane: the compiler then knows every
   // per-unit quantity is wave-uniform and keeps the unit / k-step / row
   // address arithmetic in scalar registers (and the loop a scalar loop)
-  const int first = blockIdx.x * WPB + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  const int stride = gridDim.x * WPB;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int u_begin = (int)(((int64_t)blockIdx.x * n_units) / gridDim.x);
+  const int u_end = (int)(((int64_t)(blockIdx.x + 1) * n_units) / gridDim.x);
+  const int u_last = max(u_end - 1, min(u_begin, n_units - 1));   // always a valid unit
   const int NB = (NC + kWave * U - 1) / (kWave * U);
-  const int my_units = first < n_units ? (n_units - first + stride - 1) / stride : 0;
-  const int S = my_units * NB;
-  // (unit, k-step) of step s, clamped to the wave's last step (a wave with
-  // no work reads the last unit's first step)
-  const int s_max = max(S - 1, 0);
-  const int base = S > 0 ? first : n_units - 1;
-  auto unit_of = [&](int s) { return base + (min(s, s_max) / NB) * stride; };
-  auto kb_of = [&](int s) { return min(s, s_max) % NB; };
+  if (threadIdx.x == 0) next_unit = u_begin + 2 * WPB;   // published by the staging barrier
+
+  auto make = [&](int unit, int kb) {
+    Cursor c;
+    c.real = unit < u_end;
+    c.unit = c.real ? unit : u_last;
+    c.kb = c.real ? kb : 0;
+    return c;
+  };
+  // the step after c; `second` is the wave's second static unit (-1 once used)
+  int second = u_begin + WPB + wave;
+  auto advance = [&](const Cursor& c) {
+    if (!c.real) return c;
+    if (c.kb + 1 < NB) return make(c.unit, c.kb + 1);
+    int u;
+    if (second >= 0) {
+      u = second;
+      second = -1;
+    } else {
+      int v = 0;
+      if (lane == 0) v = atomicAdd(&next_unit, 1);
+      u = __builtin_amdgcn_readfirstlane(v);
+    }
+    return make(u, 0);
+  };
 
   XStage<Q, NORM, BLK> st;
   stage_issue<Q, NORM, BLK>(a, st, 0, NC);
   StepBuf<R, U> A, B;
-  load_step<Q, MODE, R, U, G128>(a, A, unit_of(0), kb_of(0), NC, lane);
-  EpiPre pa = epi_prefetch<MODE, R>(a, unit_of(0), lane);
-  load_step<Q, MODE, R, U, G128>(a, B, unit_of(1), kb_of(1), NC, lane);
-  EpiPre pb = epi_prefetch<MODE, R>(a, unit_of(1), lane);
+  Cursor ca = make(u_begin + wave, 0);
+  Cursor cb = advance(ca);   // never claims: the first unit's next step or the second static unit
+  load_step<Q, MODE, R, U, G128>(a, A, ca.unit, ca.kb, NC, lane);
+  EpiPre pa = epi_prefetch<MODE, R>(a, ca.unit, lane);
+  load_step<Q, MODE, R, U, G128>(a, B, cb.unit, cb.kb, NC, lane);
+  EpiPre pb = epi_prefetch<MODE, R>(a, cb.unit, lane);
   if constexpr (MODE == GM_QKV) {
     if (threadIdx.x < a.head_dim / 2)
       inv_freq[threadIdx.x] = 1.0 / pow((double)a.rope_theta, (2.0 * threadIdx.x) / (double)a.head_dim);
@@ -423,22 +456,18 @@ __global__ __launch_bounds__(BLK) void gemv_kernel(const GemvArgs a) {
   float acc[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) acc[r] = 0.f;
-  for (int s = 0; s < S; s += 2) {
-    {
-      const int unit = unit_of(s), kb = kb_of(s);
-      compute_step<Q, R, U>(A, acc, xs, sx, kb, NC, lane, uk);
-      if (kb == NB - 1) finish_unit<MODE, R>(a, acc, unit, lane, scale, pa, inv_freq);
-      load_step<Q, MODE, R, U, G128>(a, A, unit_of(s + 2), kb_of(s + 2), NC, lane);
-      pa = epi_prefetch<MODE, R>(a, unit_of(s + 2), lane);
-    }
-    if (s + 1 >= S) break;
-    {
-      const int unit = unit_of(s + 1), kb = kb_of(s + 1);
-      compute_step<Q, R, U>(B, acc, xs, sx, kb, NC, lane, uk);
-      if (kb == NB - 1) finish_unit<MODE, R>(a, acc, unit, lane, scale, pb, inv_freq);
-      load_step<Q, MODE, R, U, G128>(a, B, unit_of(s + 3), kb_of(s + 3), NC, lane);
-      pb = epi_prefetch<MODE, R>(a, unit_of(s + 3), lane);
-    }
+  while (ca.real) {
+    compute_step<Q, R, U>(A, acc, xs, sx, ca.kb, NC, lane, uk);
+    if (ca.kb == NB - 1) finish_unit<MODE, R>(a, acc, ca.unit, lane, scale, pa, inv_freq);
+    ca = advance(cb);
+    load_step<Q, MODE, R, U, G128>(a, A, ca.unit, ca.kb, NC, lane);
+    pa = epi_prefetch<MODE, R>(a, ca.unit, lane);
+    if (!cb.real) break;
+    compute_step<Q, R, U>(B, acc, xs, sx, cb.kb, NC, lane, uk);
+    if (cb.kb == NB - 1) finish_unit<MODE, R>(a, acc, cb.unit, lane, scale, pb, inv_freq);
+    cb = advance(ca);
+    load_step<Q, MODE, R, U, G128>(a, B, cb.unit, cb.kb, NC, lane);
+    pb = epi_prefetch<MODE, R>(a, cb.unit, lane);
   }
 }
 
@@ -491,11 +520,9 @@ int launch_variant(const GemvArgs& a, hipStream_t stream, int max_blocks) {
   if (MODE == GM_SWIGLU) units = (a.N + R / 2 - 1) / (R / 2);
   else if (MODE == GM_QKV) units = (a.n_heads + 2 * a.n_kv) * (a.head_dim / 2) / (R / 2);
   else units = (a.N + R - 1) / R;
-  // balanced persistent grid: every wave gets ceil(units / max_waves) units
-  const int max_waves = max_blocks * kWavesPerBlock;
-  const int per_wave = (units + max_waves - 1) / max_waves;
-  const int waves = (units + per_wave - 1) / per_wave;
-  const int blocks = (waves + kWavesPerBlock - 1) / kWavesPerBlock;
+  // persistent grid: up to max_blocks blocks, each owning a contiguous range
+  // of at least one unit per wave
+  const int blocks = std::max(1, std::min(max_blocks, (units + kWavesPerBlock - 1) / kWavesPerBlock));
   hipLaunchKernelGGL((gemv_kernel<Q, MODE, R, U, NORM, G128, BLK>), dim3(blocks), dim3(BLK), lds, stream, a);
   CQ_HIP(hipGetLastError());
   return CQ_OK;

@@ -232,6 +232,25 @@ def test_attention_parity(g, H, KV, hd, T):
         assert rel_err(got, want0) <= TOL
 
 
+@pytest.mark.parametrize("H,KV,hd,T", [(8, 1, 128, 20000), (28, 4, 128, 32768), (14, 2, 64, 40000)])
+def test_attention_parity_many_partitions(g, H, KV, hd, T):
+    """Long contexts: 64 partitions per kv head (the 7B bench shape) and more
+    than 64 (the merge takes several rounds)."""
+    ms = ((T + 31) // 32) * 32
+    rng = np.random.default_rng(T + H)
+    q = rng.standard_normal(H * hd).astype(np.float16)
+    K = rng.standard_normal((KV, T, hd)).astype(np.float16)
+    Vv = rng.standard_normal((KV, T, hd)).astype(np.float16)
+    kc, vc = tile_kv(K, Vv, ms)
+    ws = g.empty(cq.lib.cq_attention_workspace_bytes(H, KV, hd), zero=True)
+    out = g.empty(H * hd * 2)
+    cq.check(cq.lib.cq_gqa_attention_decode(g.put(q), g.put(kc), g.put(vc), out.ptr, g.i32(T - 1), H, KV, hd, ms,
+                                            ws.ptr, None))
+    got = out.to_array(np.float16)
+    assert rel_err(got, orc.attention(q, K, Vv, H, KV, hd, T, mode=1)) <= TOL
+    assert rel_err(got, orc.attention(q, K, Vv, H, KV, hd, T, mode=0)) <= TOL
+
+
 def test_attention_ignores_stale_cache_tail(g):
     H, KV, hd, T, ms = 14, 2, 64, 45, 128
     rng = np.random.default_rng(5)
