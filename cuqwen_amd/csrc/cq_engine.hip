@@ -161,6 +161,7 @@ struct cq_state {
   int* history = nullptr;
   int* tokens_dev = nullptr;
   uint32_t* stamp = nullptr;
+  double* rope_inv_freq = nullptr;   // [head_dim/2]
   int* host_pinned = nullptr;     // staging for the per-step control words
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
@@ -184,7 +185,8 @@ int layer_gemvs(const cq_state* s, int l, GemvArgs* qkv, GemvArgs* o, GemvArgs* 
     a.bias[0] = L.bq; a.bias[1] = L.bk; a.bias[2] = L.bv;
     a.out[0] = s->q;
     a.n_heads = c.n_heads; a.n_kv = c.n_kv_heads; a.head_dim = c.head_dim; a.d_pos = &s->ctl->pos;
-    a.rope_theta = c.rope_theta; a.kcache = kc; a.vcache = vc; a.max_seq = c.max_seq_len;
+    a.rope_theta = c.rope_theta; a.rope_inv_freq = s->rope_inv_freq;
+    a.kcache = kc; a.vcache = vc; a.max_seq = c.max_seq_len;
     *qkv = a;
   }
   if (o) {
@@ -440,7 +442,7 @@ extern "C" int cq_state_create(const cq_config* cfg, const cq_weights* w, cq_sta
                o_ctl = take(sizeof(StepCtl)), o_hist = take((size_t)c.max_seq_len * 4),
                o_tok = take((size_t)c.max_seq_len * 4), o_stamp = take((size_t)c.vocab_size * 4),
                o_attn = take(attention_workspace_bytes(c.n_heads, c.n_kv_heads, c.head_dim)),
-               o_arg = take(kArgmaxBlocks * 8 + 64);
+               o_arg = take(kArgmaxBlocks * 8 + 64), o_rope = take((size_t)c.head_dim / 2 * sizeof(double));
   const size_t small = off;
   const size_t o_kc = take(kv_bytes), o_vc = take(kv_bytes);
   if (hipMalloc(&s->arena, off) != hipSuccess) return fail(CQ_ENOMEM, "state_create: device allocation failed");
@@ -450,6 +452,7 @@ extern "C" int cq_state_create(const cq_config* cfg, const cq_weights* w, cq_sta
   s->ctl = (StepCtl*)(a + o_ctl); s->history = (int*)(a + o_hist); s->tokens_dev = (int*)(a + o_tok);
   s->stamp = (uint32_t*)(a + o_stamp); s->attn_ws = a + o_attn; s->argmax_ws = (unsigned long long*)(a + o_arg);
   s->kcache = (__half*)(a + o_kc); s->vcache = (__half*)(a + o_vc);
+  s->rope_inv_freq = (double*)(a + o_rope);
   int rc = CQ_OK;
   auto chk = [&](hipError_t e, const char* what) {
     if (e != hipSuccess && rc == CQ_OK) rc = fail(CQ_EHIP, std::string("state_create: ") + what + ": " + hipGetErrorString(e));
@@ -461,6 +464,10 @@ extern "C" int cq_state_create(const cq_config* cfg, const cq_weights* w, cq_sta
   init.epoch = 1u;
   init.max_history = c.max_seq_len;
   chk(hipMemcpy(s->ctl, &init, sizeof init, hipMemcpyHostToDevice), "hipMemcpy ctl");
+  std::vector<double> inv_freq(c.head_dim / 2);
+  rope_inv_freq_host(c.rope_theta, c.head_dim, inv_freq.data());
+  chk(hipMemcpy(s->rope_inv_freq, inv_freq.data(), inv_freq.size() * sizeof(double), hipMemcpyHostToDevice),
+      "hipMemcpy rope");
   chk(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking), "hipStreamCreate");
   chk(hipHostMalloc((void**)&s->host_pinned, 64 * sizeof(int), hipHostMallocDefault), "hipHostMalloc");
   chk(hipEventCreate(&s->ev0), "hipEventCreate");

@@ -3,6 +3,12 @@
 #include "cq_internal.h"
 
 #include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <tuple>
 
 namespace cq {
 
@@ -124,9 +130,11 @@ __device__ __forceinline__ float stage_finish(const GemvArgs& a, XStage<Q, NORM,
     if (lane == 0) red[threadIdx.x / kWave] = ss;
   }
   stage_write<Q, NORM, BLK>(st, 0, NC, xs, sx);
-  for (int b = 1; b * XS::XB * BLK < NC; ++b) {
-    stage_issue<Q, NORM, BLK>(a, st, b, NC);
-    stage_write<Q, NORM, BLK>(st, b, NC, xs, sx);
+  if constexpr (!NORM) {   // with the norm fused, XB is sized so one batch holds all of x
+    for (int b = 1; b * XS::XB * BLK < NC; ++b) {
+      stage_issue<Q, NORM, BLK>(a, st, b, NC);
+      stage_write<Q, NORM, BLK>(st, b, NC, xs, sx);
+    }
   }
   __syncthreads();
   if constexpr (NORM) {
@@ -295,8 +303,8 @@ __device__ __forceinline__ void store_row(const GemvArgs& a, float v, float pre,
 
 // QKV epilogue of one rotation pair (rows i and i + hd/2 of a head): bias,
 // fp16, NeoX RoPE on q/k, k/v into the cache.  inv_freq[i] = theta^(-2i/hd)
-// in double; the angle pos * inv_freq is reduced modulo 2 pi in double and
-// its sine and cosine taken in fp32.
+// in double (a host-computed table staged in LDS); the angle pos * inv_freq
+// is reduced modulo 2 pi in double and its sine and cosine taken in fp32.
 template <int MODE, int R>
 __device__ __forceinline__ void qkv_pair(const GemvArgs& a, float y0, float y1, const EpiPre& pre, int unit,
                                          int i_pair, const double* inv_freq) {
@@ -437,8 +445,19 @@ __global__ __launch_bounds__(BLK) void gemv_kernel(const GemvArgs a) {
     return make(u, 0);
   };
 
+  // The x loads go out at raised wave priority so that every resident
+  // wave's staging loads are issued before any wave's weight prefetch:
+  // the CU's memory pipeline serves loads in issue order, and x behind the
+  // weights would hold the staging barrier for a full weight round trip.
+  __builtin_amdgcn_s_setprio(3);
   XStage<Q, NORM, BLK> st;
   stage_issue<Q, NORM, BLK>(a, st, 0, NC);
+  // the RoPE table rides with the x loads (every thread, clamped index):
+  // waiting for a load issued after the weight prefetch would wait for the
+  // whole prefetch
+  double rope_f = 0.0;
+  if constexpr (MODE == GM_QKV) rope_f = a.rope_inv_freq[min((int)threadIdx.x, a.head_dim / 2 - 1)];
+  __builtin_amdgcn_s_setprio(0);
   StepBuf<R, U> A, B;
   Cursor ca = make(u_begin + wave, 0);
   Cursor cb = advance(ca);   // never claims: the first unit's next step or the second static unit
@@ -446,10 +465,7 @@ __global__ __launch_bounds__(BLK) void gemv_kernel(const GemvArgs a) {
   EpiPre pa = epi_prefetch<MODE, R>(a, ca.unit, lane);
   load_step<Q, MODE, R, U, G128>(a, B, cb.unit, cb.kb, NC, lane);
   EpiPre pb = epi_prefetch<MODE, R>(a, cb.unit, lane);
-  if constexpr (MODE == GM_QKV) {
-    if (threadIdx.x < a.head_dim / 2)
-      inv_freq[threadIdx.x] = 1.0 / pow((double)a.rope_theta, (2.0 * threadIdx.x) / (double)a.head_dim);
-  }
+  if constexpr (MODE == GM_QKV) inv_freq[min((int)threadIdx.x, a.head_dim / 2 - 1)] = rope_f;   // duplicates write equal values
   const float scale = stage_finish<Q, NORM, BLK>(a, st, NC, xs, sx, red);
 
   const UnpackRegs uk = unpack_regs();
@@ -472,6 +488,39 @@ __global__ __launch_bounds__(BLK) void gemv_kernel(const GemvArgs a) {
 }
 
 // ------------------------------------------------------------------ host
+void rope_inv_freq_host(float theta, int head_dim, double* out) {
+  for (int i = 0; i < head_dim / 2; ++i) out[i] = 1.0 / std::pow((double)theta, (2.0 * i) / (double)head_dim);
+}
+
+int rope_table(float theta, int head_dim, const double** out) {
+  static std::mutex mu;
+  static std::map<std::tuple<int, uint32_t, int>, double*> tables;
+  if (head_dim <= 0 || head_dim > kMaxHeadDim || head_dim % 2) return fail(CQ_EINVAL, "rope: bad head_dim");
+  int dev = 0;
+  CQ_HIP(hipGetDevice(&dev));
+  uint32_t tbits;
+  std::memcpy(&tbits, &theta, 4);
+  std::lock_guard<std::mutex> lock(mu);
+  const auto key = std::make_tuple(dev, tbits, head_dim);
+  auto it = tables.find(key);
+  if (it != tables.end()) {
+    *out = it->second;
+    return CQ_OK;
+  }
+  double host[kMaxHeadDim / 2];
+  rope_inv_freq_host(theta, head_dim, host);
+  double* d = nullptr;
+  CQ_HIP(hipMalloc(&d, sizeof host));
+  const hipError_t e = hipMemcpy(d, host, sizeof(double) * (head_dim / 2), hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    (void)hipFree(d);
+    return fail(CQ_EHIP, std::string("rope: table upload failed: ") + hipGetErrorString(e));
+  }
+  tables.emplace(key, d);
+  *out = d;
+  return CQ_OK;
+}
+
 int gemv_check(const GemvArgs& a) {
   if (a.quant < 0 || a.quant > 2) return fail(CQ_EINVAL, "gemv: bad quant type");
   if (a.K <= 0 || a.N <= 0) return fail(CQ_EINVAL, "gemv: empty shape");
@@ -485,7 +534,8 @@ int gemv_check(const GemvArgs& a) {
   if (a.mode == GM_QKV) {
     if (a.head_dim % 4 || a.head_dim > kMaxHeadDim || a.n_heads <= 0 || a.n_kv <= 0 || a.n_heads % a.n_kv)
       return fail(CQ_EINVAL, "gemv: bad head configuration");
-    if (!a.W[1] || !a.W[2] || !a.d_pos) return fail(CQ_EINVAL, "gemv: qkv needs q, k, v weights and d_pos");
+    if (!a.W[1] || !a.W[2] || !a.d_pos || !a.rope_inv_freq)
+      return fail(CQ_EINVAL, "gemv: qkv needs q, k, v weights, d_pos and the RoPE table");
     if (a.quant != CQ_QUANT_FP16 && (!a.S[1] || !a.S[2])) return fail(CQ_EINVAL, "gemv: qkv needs q, k, v scales");
     if (a.kcache && a.max_seq % 32) return fail(CQ_EINVAL, "gemv: max_seq must be a multiple of 32");
   } else if (!a.out[0]) {
