@@ -252,8 +252,8 @@ __device__ __forceinline__ void compute_step(const StepBuf<R, U>& b, float (&acc
 
 // Epilogue operands fetched together with a unit's first weights, so the
 // epilogue does not start a dependent memory round trip: lane r < R holds
-// the residual x[row] (RESID) or the bias (STORE); in QKV mode lane i < R/2
-// holds the biases of its rotation pair.
+// the residual x[row] (RESID) or the bias and penalty stamp (STORE); in QKV
+// mode lane i < R/2 holds the biases of its rotation pair.
 struct EpiPre {
   uint32_t a = 0, b = 0;   // raw fp16 bits, zero-extended; converted where used
 };
@@ -268,9 +268,14 @@ __device__ __forceinline__ EpiPre epi_prefetch(const GemvArgs& a, int unit, int 
   EpiPre e;
   if constexpr (MODE == GM_STORE || MODE == GM_RESID) {
     const RowRef me = row_of<MODE, R>(a, unit, min(lane, R - 1));
-    if constexpr (MODE == GM_RESID) e.a = ld_u16(reinterpret_cast<const _Float16*>(a.out[0]) + me.row);
-    else e.a = ld_u16(a.bias[0] ? reinterpret_cast<const _Float16*>(a.bias[0]) + me.row
-                                : reinterpret_cast<const _Float16*>(a.x));
+    if constexpr (MODE == GM_RESID) {
+      e.a = ld_u16(reinterpret_cast<const _Float16*>(a.out[0]) + me.row);
+    } else {
+      e.a = ld_u16(a.bias[0] ? reinterpret_cast<const _Float16*>(a.bias[0]) + me.row
+                             : reinterpret_cast<const _Float16*>(a.x));
+      // the row's penalty stamp (a missing stamp array reads x[0..1], ignored at use)
+      e.b = *(a.stamp ? a.stamp + me.row : reinterpret_cast<const uint32_t*>(a.x));
+    }
   } else if constexpr (MODE == GM_QKV) {
     constexpr int PP = R / 2;
     const int i = min(lane, PP - 1);
@@ -286,13 +291,14 @@ __device__ __forceinline__ EpiPre epi_prefetch(const GemvArgs& a, int unit, int 
 
 // Epilogue of one output row (STORE / RESID modes).
 template <int MODE, int R>
-__device__ __forceinline__ void store_row(const GemvArgs& a, float v, float pre, int unit, int r) {
+__device__ __forceinline__ void store_row(const GemvArgs& a, float v, float pre, uint32_t stamp, uint32_t epoch,
+                                          int unit, int r) {
   const RowRef me = row_of<MODE, R>(a, unit, r);
   if (!me.valid) return;
   _Float16* out = reinterpret_cast<_Float16*>(a.out[0]);
   v += pre;   // residual (kernels.cu:621, :671: it stays fp16) or bias
   _Float16 h = (_Float16)v;
-  if (MODE == GM_STORE && a.stamp && a.stamp[me.row] == *a.d_epoch) {
+  if (MODE == GM_STORE && a.stamp && stamp == epoch) {
     // repetition penalty on the fp16 logit (kernels.cu:885-888)
     const float pen = (float)(_Float16)a.penalty;
     const float l = (float)h;
@@ -307,14 +313,13 @@ __device__ __forceinline__ void store_row(const GemvArgs& a, float v, float pre,
 // is reduced modulo 2 pi in double and its sine and cosine taken in fp32.
 template <int MODE, int R>
 __device__ __forceinline__ void qkv_pair(const GemvArgs& a, float y0, float y1, const EpiPre& pre, int unit,
-                                         int i_pair, const double* inv_freq) {
+                                         int i_pair, const double* inv_freq, int pos) {
   constexpr int PP = R / 2;
   const RowRef r0 = row_of<MODE, R>(a, unit, i_pair);
   const RowRef r1 = row_of<MODE, R>(a, unit, i_pair + PP);
   const bool has_bias = sel3(a.bias, r0.mat) != nullptr;
   y0 = (float)(_Float16)(y0 + (has_bias ? epi_f(pre.a) : 0.f));   // q/k/v are fp16 before RoPE (kernels.cu:470)
   y1 = (float)(_Float16)(y1 + (has_bias ? epi_f(pre.b) : 0.f));
-  const int pos = *a.d_pos;
   const int hd = a.head_dim;
   if (r0.mat < 2) {
     // NeoX rotation of (i, i + hd/2) (kernels.cu:370-398)
@@ -349,14 +354,15 @@ __device__ __forceinline__ void qkv_pair(const GemvArgs& a, float y0, float y1, 
 // through scratch).
 template <int MODE, int R>
 __device__ __forceinline__ void finish_unit(const GemvArgs& a, float (&acc)[R], int unit, int lane, float scale,
-                                            const EpiPre& pre, const double* inv_freq) {
+                                            const EpiPre& pre, const double* inv_freq, uint32_t step_word) {
 #pragma unroll
   for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]) * scale;
   if constexpr (MODE == GM_STORE || MODE == GM_RESID) {
 #pragma unroll
     for (int r = 0; r < R; ++r)
       if (lane == r)
-        store_row<MODE, R>(a, acc[r], (MODE == GM_RESID || a.bias[0]) ? epi_f(pre.a) : 0.f, unit, r);
+        store_row<MODE, R>(a, acc[r], (MODE == GM_RESID || a.bias[0]) ? epi_f(pre.a) : 0.f, pre.b, step_word, unit,
+                           r);
   } else if constexpr (MODE == GM_SWIGLU) {
 #pragma unroll
     for (int r = 0; r < R / 2; ++r) {
@@ -372,7 +378,7 @@ __device__ __forceinline__ void finish_unit(const GemvArgs& a, float (&acc)[R], 
   } else {
 #pragma unroll
     for (int r = 0; r < R / 2; ++r)
-      if (lane == r) qkv_pair<MODE, R>(a, acc[r], acc[r + R / 2], pre, unit, r, inv_freq);
+      if (lane == r) qkv_pair<MODE, R>(a, acc[r], acc[r + R / 2], pre, unit, r, inv_freq, (int)step_word);
   }
 #pragma unroll
   for (int r = 0; r < R; ++r) acc[r] = 0.f;
@@ -396,8 +402,9 @@ struct Cursor {
 // per lane of each of the unit's R rows.  Two step buffers rotate: while one
 // step is reduced the next one's loads are in flight.  The first two steps
 // (and their epilogue operands) are requested before the LDS staging so the
-// input-vector prologue overlaps them.  Every load is unconditional, keeping
-// the code straight-line and the compiler's load counters exact.
+// input-vector prologue overlaps them.  The main loop issues loads only for
+// real work, and unconditionally inside its body (clamped chunk indices),
+// keeping the compiler's load counters exact.
 template <int Q, int MODE, int R, int U, bool NORM, bool G128, int BLK>
 __global__ __launch_bounds__(BLK) void gemv_kernel(const GemvArgs a) {
   using T = QTraits<Q>;
@@ -457,10 +464,17 @@ __global__ __launch_bounds__(BLK) void gemv_kernel(const GemvArgs a) {
   // whole prefetch
   double rope_f = 0.0;
   if constexpr (MODE == GM_QKV) rope_f = a.rope_inv_freq[min((int)threadIdx.x, a.head_dim / 2 - 1)];
+  // the step's control word the epilogue needs (QKV: position; STORE: the
+  // penalty epoch), also read up front rather than in the epilogue
+  uint32_t step_word = 0;
+  if constexpr (MODE == GM_QKV) step_word = (uint32_t)*a.d_pos;
+  if constexpr (MODE == GM_STORE) step_word = a.stamp ? *a.d_epoch : 0u;
   __builtin_amdgcn_s_setprio(0);
   StepBuf<R, U> A, B;
   Cursor ca = make(u_begin + wave, 0);
   Cursor cb = advance(ca);   // never claims: the first unit's next step or the second static unit
+  // the first two steps are requested unconditionally (a cursor past the
+  // range reads a valid unit that is never used)
   load_step<Q, MODE, R, U, G128>(a, A, ca.unit, ca.kb, NC, lane);
   EpiPre pa = epi_prefetch<MODE, R>(a, ca.unit, lane);
   load_step<Q, MODE, R, U, G128>(a, B, cb.unit, cb.kb, NC, lane);
@@ -472,18 +486,45 @@ __global__ __launch_bounds__(BLK) void gemv_kernel(const GemvArgs a) {
   float acc[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) acc[r] = 0.f;
-  while (ca.real) {
+  auto run_a = [&]() {
     compute_step<Q, R, U>(A, acc, xs, sx, ca.kb, NC, lane, uk);
-    if (ca.kb == NB - 1) finish_unit<MODE, R>(a, acc, ca.unit, lane, scale, pa, inv_freq);
-    ca = advance(cb);
-    load_step<Q, MODE, R, U, G128>(a, A, ca.unit, ca.kb, NC, lane);
-    pa = epi_prefetch<MODE, R>(a, ca.unit, lane);
-    if (!cb.real) break;
+    if (ca.kb == NB - 1) finish_unit<MODE, R>(a, acc, ca.unit, lane, scale, pa, inv_freq, step_word);
+  };
+  auto run_b = [&]() {
     compute_step<Q, R, U>(B, acc, xs, sx, cb.kb, NC, lane, uk);
-    if (cb.kb == NB - 1) finish_unit<MODE, R>(a, acc, cb.unit, lane, scale, pb, inv_freq);
-    cb = advance(ca);
-    load_step<Q, MODE, R, U, G128>(a, B, cb.unit, cb.kb, NC, lane);
-    pb = epi_prefetch<MODE, R>(a, cb.unit, lane);
+    if (cb.kb == NB - 1) finish_unit<MODE, R>(a, acc, cb.unit, lane, scale, pb, inv_freq, step_word);
+  };
+  // Steady state: A and B both hold real steps and each round refills both,
+  // so every load in the loop is unconditional and the compiler's load
+  // counters stay exact.  When the next step is past the wave's range the
+  // wave leaves the loop before issuing its loads (a load whose data is
+  // never used would still hold the wave until it returned) and finishes the
+  // buffer it still holds.
+  if (ca.real) {
+    if (!cb.real) {
+      run_a();
+    } else {
+      while (true) {
+        run_a();
+        const Cursor na = advance(cb);
+        if (!na.real) {
+          run_b();
+          break;
+        }
+        ca = na;
+        load_step<Q, MODE, R, U, G128>(a, A, ca.unit, ca.kb, NC, lane);
+        pa = epi_prefetch<MODE, R>(a, ca.unit, lane);
+        run_b();
+        const Cursor nb = advance(ca);
+        if (!nb.real) {
+          run_a();
+          break;
+        }
+        cb = nb;
+        load_step<Q, MODE, R, U, G128>(a, B, cb.unit, cb.kb, NC, lane);
+        pb = epi_prefetch<MODE, R>(a, cb.unit, lane);
+      }
+    }
   }
 }
 
