@@ -95,6 +95,23 @@ __device__ __forceinline__ float wave_max(float v) {
   return fmaxf(fmaxf(lane_of(v, 0), lane_of(v, 16)), fmaxf(lane_of(v, 32), lane_of(v, 48)));
 }
 
+// Order-preserving argmax key (kernels.cu:907-911): a larger float gives a
+// larger key, equal floats let the lower index win (~idx), NaN sorts above
+// +inf.
+__device__ __forceinline__ unsigned long long argmax_key(float v, int idx) {
+  const uint32_t fu = __float_as_uint(v);
+  const uint32_t key = (fu & 0x80000000u) ? ~fu : (fu | 0x80000000u);
+  return ((unsigned long long)key << 32) | (uint32_t)(~idx);
+}
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const unsigned long long o = __shfl_xor(v, off, kWave);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
 // Block-wide sum for blockDim.x a multiple of 64 (<= 1024); `red` holds 16
 // floats of LDS.  All threads get the result.
 __device__ __forceinline__ float block_sum(float v, float* red) {

@@ -254,8 +254,10 @@ int step_body(cq_state* s) {
     CQ_TRY(launch_gemv(m1, st));
     CQ_TRY(launch_gemv(m2, st));
   }
-  CQ_TRY(launch_gemv(lm_head_gemv(s), st));
-  CQ_TRY(launch_argmax(s->logits, c.vocab_size, s->argmax_ws, s->ctl, nullptr, s->history, s->tokens_dev, st));
+  GemvArgs lm = lm_head_gemv(s);
+  lm.argmax_out = s->argmax_ws;   // one key per wave, reduced below
+  CQ_TRY(launch_gemv(lm, st));
+  CQ_TRY(launch_argmax_reduce(s->argmax_ws, kArgmaxPartials, s->ctl, nullptr, s->history, s->tokens_dev, st));
   return CQ_OK;
 }
 
@@ -442,7 +444,7 @@ extern "C" int cq_state_create(const cq_config* cfg, const cq_weights* w, cq_sta
                o_ctl = take(sizeof(StepCtl)), o_hist = take((size_t)c.max_seq_len * 4),
                o_tok = take((size_t)c.max_seq_len * 4), o_stamp = take((size_t)c.vocab_size * 4),
                o_attn = take(attention_workspace_bytes(c.n_heads, c.n_kv_heads, c.head_dim)),
-               o_arg = take(kArgmaxBlocks * 8 + 64), o_rope = take((size_t)c.head_dim / 2 * sizeof(double));
+               o_arg = take(kArgmaxPartials * 8 + 64), o_rope = take((size_t)c.head_dim / 2 * sizeof(double));
   const size_t small = off;
   const size_t o_kc = take(kv_bytes), o_vc = take(kv_bytes);
   if (hipMalloc(&s->arena, off) != hipSuccess) return fail(CQ_ENOMEM, "state_create: device allocation failed");
@@ -625,7 +627,7 @@ extern "C" int cq_state_profile(cq_state* s, int32_t pos, int32_t iters, int32_t
       {"gate_up_swiglu", wbytes(qt, 2 * I, d) + 2 * d * 2 + 2 * I, 3},
       {"down_residual", wbytes(qt, d, I) + 2 * I + 2 * d * 2, 4},
       {"lm_head", wbytes(lmq, V, d) + 2 * d * 2 + 2 * V, 5},
-      {"argmax", 2 * V, 6},
+      {"argmax", 8.0 * kArgmaxPartials, 6},   // the lm_head GEMV already reduced the logits to one key per wave
   };
   const int nk = (int)(sizeof ks / sizeof ks[0]);
   int n = 0;
@@ -643,8 +645,13 @@ extern "C" int cq_state_profile(cq_state* s, int32_t pos, int32_t iters, int32_t
           case 2: CQ_TRY(launch_gemv(o, s->stream)); break;
           case 3: CQ_TRY(launch_gemv(m1, s->stream)); break;
           case 4: CQ_TRY(launch_gemv(m2, s->stream)); break;
-          case 5: CQ_TRY(launch_gemv(lm_head_gemv(s), s->stream)); break;
-          case 6: CQ_TRY(launch_argmax(s->logits, c.vocab_size, s->argmax_ws, nullptr, nullptr, nullptr, nullptr, s->stream)); break;
+          case 5: {
+            GemvArgs lm = lm_head_gemv(s);
+            lm.argmax_out = s->argmax_ws;
+            CQ_TRY(launch_gemv(lm, s->stream));
+            break;
+          }
+          case 6: CQ_TRY(launch_argmax_reduce(s->argmax_ws, kArgmaxPartials, nullptr, nullptr, nullptr, nullptr, s->stream)); break;
         }
       }
       return CQ_OK;

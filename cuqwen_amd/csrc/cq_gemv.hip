@@ -289,12 +289,13 @@ __device__ __forceinline__ EpiPre epi_prefetch(const GemvArgs& a, int unit, int 
   return e;
 }
 
-// Epilogue of one output row (STORE / RESID modes).
+// Epilogue of one output row (STORE / RESID modes); returns the stored
+// value's argmax key.
 template <int MODE, int R>
-__device__ __forceinline__ void store_row(const GemvArgs& a, float v, float pre, uint32_t stamp, uint32_t epoch,
-                                          int unit, int r) {
+__device__ __forceinline__ unsigned long long store_row(const GemvArgs& a, float v, float pre, uint32_t stamp,
+                                                        uint32_t epoch, int unit, int r) {
   const RowRef me = row_of<MODE, R>(a, unit, r);
-  if (!me.valid) return;
+  if (!me.valid) return 0ull;
   _Float16* out = reinterpret_cast<_Float16*>(a.out[0]);
   v += pre;   // residual (kernels.cu:621, :671: it stays fp16) or bias
   _Float16 h = (_Float16)v;
@@ -305,6 +306,7 @@ __device__ __forceinline__ void store_row(const GemvArgs& a, float v, float pre,
     h = (_Float16)(l < 0.f ? l * pen : l / pen);
   }
   out[me.row] = h;
+  return argmax_key((float)h, me.row);   // the stored value, as the argmax reads it back
 }
 
 // QKV epilogue of one rotation pair (rows i and i + hd/2 of a head): bias,
@@ -354,15 +356,18 @@ __device__ __forceinline__ void qkv_pair(const GemvArgs& a, float y0, float y1, 
 // through scratch).
 template <int MODE, int R>
 __device__ __forceinline__ void finish_unit(const GemvArgs& a, float (&acc)[R], int unit, int lane, float scale,
-                                            const EpiPre& pre, const double* inv_freq, uint32_t step_word) {
+                                            const EpiPre& pre, const double* inv_freq, uint32_t step_word,
+                                            unsigned long long& best) {
 #pragma unroll
   for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]) * scale;
   if constexpr (MODE == GM_STORE || MODE == GM_RESID) {
 #pragma unroll
     for (int r = 0; r < R; ++r)
-      if (lane == r)
-        store_row<MODE, R>(a, acc[r], (MODE == GM_RESID || a.bias[0]) ? epi_f(pre.a) : 0.f, pre.b, step_word, unit,
-                           r);
+      if (lane == r) {
+        const unsigned long long k = store_row<MODE, R>(a, acc[r], (MODE == GM_RESID || a.bias[0]) ? epi_f(pre.a) : 0.f,
+                                                        pre.b, step_word, unit, r);
+        if constexpr (MODE == GM_STORE) best = k > best ? k : best;
+      }
   } else if constexpr (MODE == GM_SWIGLU) {
 #pragma unroll
     for (int r = 0; r < R / 2; ++r) {
@@ -486,13 +491,14 @@ __global__ __launch_bounds__(BLK) void gemv_kernel(const GemvArgs a) {
   float acc[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) acc[r] = 0.f;
+  unsigned long long best = 0ull;   // STORE: argmax key of the rows this lane stored
   auto run_a = [&]() {
     compute_step<Q, R, U>(A, acc, xs, sx, ca.kb, NC, lane, uk);
-    if (ca.kb == NB - 1) finish_unit<MODE, R>(a, acc, ca.unit, lane, scale, pa, inv_freq, step_word);
+    if (ca.kb == NB - 1) finish_unit<MODE, R>(a, acc, ca.unit, lane, scale, pa, inv_freq, step_word, best);
   };
   auto run_b = [&]() {
     compute_step<Q, R, U>(B, acc, xs, sx, cb.kb, NC, lane, uk);
-    if (cb.kb == NB - 1) finish_unit<MODE, R>(a, acc, cb.unit, lane, scale, pb, inv_freq, step_word);
+    if (cb.kb == NB - 1) finish_unit<MODE, R>(a, acc, cb.unit, lane, scale, pb, inv_freq, step_word, best);
   };
   // Steady state: A and B both hold real steps and each round refills both,
   // so every load in the loop is unconditional and the compiler's load
@@ -524,6 +530,13 @@ __global__ __launch_bounds__(BLK) void gemv_kernel(const GemvArgs a) {
         load_step<Q, MODE, R, U, G128>(a, B, cb.unit, cb.kb, NC, lane);
         pb = epi_prefetch<MODE, R>(a, cb.unit, lane);
       }
+    }
+  }
+  if constexpr (MODE == GM_STORE) {
+    // every launched wave writes its slot (0 when it stored nothing)
+    if (a.argmax_out) {
+      best = wave_max_u64(best);
+      if (lane == 0) a.argmax_out[blockIdx.x * WPB + wave] = best;
     }
   }
 }
@@ -587,6 +600,7 @@ int gemv_check(const GemvArgs& a) {
   const size_t lds = (size_t)planes * (a.K / epc) * 16 + (a.quant ? (size_t)(a.K / epc) * 4 : 0);
   if (lds > 60 * 1024) return fail(CQ_EINVAL, "gemv: input vector too long for LDS staging");
   if (a.norm_w && a.K > kNormMaxK) return fail(CQ_EINVAL, "gemv: fused RMSNorm supports K <= 16384");
+  if (a.argmax_out && a.mode != GM_STORE) return fail(CQ_EINVAL, "gemv: argmax keys need the store mode");
   return CQ_OK;
 }
 
@@ -614,6 +628,7 @@ int launch_variant(const GemvArgs& a, hipStream_t stream, int max_blocks) {
   // persistent grid: up to max_blocks blocks, each owning a contiguous range
   // of at least one unit per wave
   const int blocks = std::max(1, std::min(max_blocks, (units + kWavesPerBlock - 1) / kWavesPerBlock));
+  if (a.argmax_out && blocks * kWavesPerBlock > kArgmaxPartials) return fail(CQ_EINVAL, "gemv: too many waves for the argmax slots");
   hipLaunchKernelGGL((gemv_kernel<Q, MODE, R, U, NORM, G128, BLK>), dim3(blocks), dim3(BLK), lds, stream, a);
   CQ_HIP(hipGetLastError());
   return CQ_OK;

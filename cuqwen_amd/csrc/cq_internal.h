@@ -32,6 +32,9 @@ struct GemvArgs {
   const uint32_t* stamp = nullptr;
   const uint32_t* d_epoch = nullptr;
   float penalty = 1.f;
+  // STORE mode: each wave writes the argmax key of the rows it stored to
+  // argmax_out[wave] (at most kArgmaxPartials waves)
+  unsigned long long* argmax_out = nullptr;
 };
 
 // Validates shapes and launches; returns CQ_OK or an error code.
@@ -94,6 +97,10 @@ struct StepCtl {
 // ctl->chain, advances the step; `tokens_out` (optional) records the token at
 // ctl->step.
 constexpr int kArgmaxBlocks = 256;
+constexpr int kArgmaxPartials = 4096;   // keys written by the lm_head GEMV (one per wave)
+// Reduces n argmax keys and does the step bookkeeping of launch_argmax.
+int launch_argmax_reduce(const unsigned long long* partials, int n, StepCtl* ctl, int* d_token_out, int* history,
+                         int* tokens_out, hipStream_t stream);
 int launch_argmax(const __half* logits, int vocab, unsigned long long* partials, StepCtl* ctl,
                   int* d_token_out, int* history, int* tokens_out, hipStream_t stream);
 

@@ -101,21 +101,6 @@ int launch_epoch_bump(uint32_t* d_epoch, hipStream_t stream) {
 }
 
 // ----------------------------------------------------------------- argmax
-// Order-preserving key (kernels.cu:907-911): larger float -> larger key,
-// equal floats -> the lower index wins (~idx), NaN above +inf.
-__device__ __forceinline__ unsigned long long argmax_key(float v, int idx) {
-  const uint32_t fu = __float_as_uint(v);
-  const uint32_t key = (fu & 0x80000000u) ? ~fu : (fu | 0x80000000u);
-  return ((unsigned long long)key << 32) | (uint32_t)(~idx);
-}
-__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    const unsigned long long o = __shfl_xor(v, off, kWave);
-    v = o > v ? o : v;
-  }
-  return v;
-}
 __device__ __forceinline__ unsigned long long block_max_u64(unsigned long long v, unsigned long long* red) {
   v = wave_max_u64(v);
   __syncthreads();
@@ -129,6 +114,8 @@ __device__ __forceinline__ unsigned long long block_max_u64(unsigned long long v
 // Stage 1: each block writes its best key; stage 2 (one block) reduces them
 // and does the step bookkeeping (kernels.cu:915-950).  Two launches cost
 // less here than one launch with a completion ticket and device-scope fences.
+// The decode step skips stage 1: the lm_head GEMV writes one key per wave
+// (GemvArgs::argmax_out) and stage 2 reduces those.
 __global__ __launch_bounds__(256) void argmax_stage1(const _Float16* logits, int vocab,
                                                      unsigned long long* partials) {
   __shared__ unsigned long long red[16];
@@ -141,10 +128,14 @@ __global__ __launch_bounds__(256) void argmax_stage1(const _Float16* logits, int
   if (threadIdx.x == 0) partials[blockIdx.x] = best;
 }
 
-__global__ __launch_bounds__(kArgmaxBlocks) void argmax_stage2(const unsigned long long* partials, StepCtl* ctl,
-                                                               int* d_token_out, int* history, int* tokens_out) {
+constexpr int kArgmaxReduceThreads = 1024;
+__global__ __launch_bounds__(kArgmaxReduceThreads) void argmax_stage2(const unsigned long long* partials, int n,
+                                                                     StepCtl* ctl, int* d_token_out, int* history,
+                                                                     int* tokens_out) {
   __shared__ unsigned long long red[16];
-  const unsigned long long b = block_max_u64(partials[threadIdx.x], red);
+  unsigned long long v = 0ull;
+  for (int i = threadIdx.x; i < n; i += kArgmaxReduceThreads) v = partials[i] > v ? partials[i] : v;
+  const unsigned long long b = block_max_u64(v, red);
   if (threadIdx.x == 0) {
     const int token = (int)(~(uint32_t)(b & 0xffffffffu));
     if (d_token_out) *d_token_out = token;
@@ -165,15 +156,21 @@ __global__ __launch_bounds__(kArgmaxBlocks) void argmax_stage2(const unsigned lo
   }
 }
 
+int launch_argmax_reduce(const unsigned long long* partials, int n, StepCtl* ctl, int* d_token_out, int* history,
+                         int* tokens_out, hipStream_t stream) {
+  if (!partials || n <= 0) return fail(CQ_EINVAL, "argmax: bad arguments");
+  hipLaunchKernelGGL(argmax_stage2, dim3(1), dim3(kArgmaxReduceThreads), 0, stream, partials, n, ctl, d_token_out,
+                     history, tokens_out);
+  CQ_HIP(hipGetLastError());
+  return CQ_OK;
+}
+
 int launch_argmax(const __half* logits, int vocab, unsigned long long* partials, StepCtl* ctl, int* d_token_out,
                   int* history, int* tokens_out, hipStream_t stream) {
   if (!logits || vocab <= 0 || !partials) return fail(CQ_EINVAL, "argmax: bad arguments");
   hipLaunchKernelGGL(argmax_stage1, dim3(kArgmaxBlocks), dim3(256), 0, stream, (const _Float16*)logits, vocab,
                      partials);
-  hipLaunchKernelGGL(argmax_stage2, dim3(1), dim3(kArgmaxBlocks), 0, stream, partials, ctl, d_token_out, history,
-                     tokens_out);
-  CQ_HIP(hipGetLastError());
-  return CQ_OK;
+  return launch_argmax_reduce(partials, kArgmaxBlocks, ctl, d_token_out, history, tokens_out, stream);
 }
 
 // ------------------------------------------------------------ step begin
