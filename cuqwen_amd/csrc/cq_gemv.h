@@ -82,25 +82,38 @@ template <> __device__ __forceinline__ float chunk_dot<CQ_QUANT_INT4>(u4_t w, co
   return acc[0] + acc[1];
 }
 
-// Order of the 8 fp16 x values of one plane as the unpack pairs them, and
-// the plane's unpack-bias term: int4 pairs (0,4) (1/16,5/16) (2,6)
-// (3/16,7/16) and owes 1032 * (x0+x4+x2+x6) + 72 * (x1+x5+x3+x7); int8 keeps
-// natural order and owes 1152 * sum(x); fp16 owes nothing.
-template <int Q> __device__ __forceinline__ float plane_order(const float* v, _Float16* out) {
+// Staging transform of one 16-byte plane of the input (8 fp16 values m0..m7,
+// already x or half(x * w)) into the order the unpack pairs it, plus the
+// plane's unpack-bias term: int4 pairs (m0,m4) (m1/16,m5/16) (m2,m6)
+// (m3/16,m7/16) and owes 1032 * (m0+m4+m2+m6) + 72 * (m1+m5+m3+m7); int8
+// keeps natural order and owes 1152 * sum(m); fp16 owes nothing.  Packed
+// fp16 arithmetic throughout (m/16 is the correctly rounded quotient); the
+// bias term is summed in fp32 with dot2 instructions.
+template <int Q> __device__ __forceinline__ float plane_order_packed(const u4_t& m, u4_t& out) {
   if constexpr (Q == CQ_QUANT_INT4) {
-    out[0] = (_Float16)v[0]; out[1] = (_Float16)v[4];
-    out[2] = (_Float16)(v[1] * 0.0625f); out[3] = (_Float16)(v[5] * 0.0625f);
-    out[4] = (_Float16)v[2]; out[5] = (_Float16)v[6];
-    out[6] = (_Float16)(v[3] * 0.0625f); out[7] = (_Float16)(v[7] * 0.0625f);
-    return kInt4BiasLo * (v[0] + v[4] + v[2] + v[6]) + kInt4BiasHi * (v[1] + v[5] + v[3] + v[7]);
+    const h2_t sixteenth = {(_Float16)0.0625f, (_Float16)0.0625f};
+    const h2_t blo = {(_Float16)kInt4BiasLo, (_Float16)kInt4BiasLo};
+    const h2_t bhi = {(_Float16)kInt4BiasHi, (_Float16)kInt4BiasHi};
+    const uint32_t p04 = __builtin_amdgcn_perm(m.z, m.x, 0x05040100u);   // (m0, m4)
+    const uint32_t p15 = __builtin_amdgcn_perm(m.z, m.x, 0x07060302u);   // (m1, m5)
+    const uint32_t p26 = __builtin_amdgcn_perm(m.w, m.y, 0x05040100u);   // (m2, m6)
+    const uint32_t p37 = __builtin_amdgcn_perm(m.w, m.y, 0x07060302u);   // (m3, m7)
+    out.x = p04;
+    out.y = as_u32(as_h2(p15) * sixteenth);
+    out.z = p26;
+    out.w = as_u32(as_h2(p37) * sixteenth);
+    float c = __builtin_amdgcn_fdot2(as_h2(p04), blo, 0.f, false);
+    c = __builtin_amdgcn_fdot2(as_h2(p26), blo, c, false);
+    c = __builtin_amdgcn_fdot2(as_h2(p15), bhi, c, false);
+    return __builtin_amdgcn_fdot2(as_h2(p37), bhi, c, false);
   } else {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) out[i] = (_Float16)v[i];
+    out = m;
     if constexpr (Q == CQ_QUANT_INT8) {
-      float s = 0.f;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) s += v[i];
-      return kInt8Bias * s;
+      const h2_t b8 = {(_Float16)kInt8Bias, (_Float16)kInt8Bias};
+      float c = __builtin_amdgcn_fdot2(as_h2(m.x), b8, 0.f, false);
+      c = __builtin_amdgcn_fdot2(as_h2(m.y), b8, c, false);
+      c = __builtin_amdgcn_fdot2(as_h2(m.z), b8, c, false);
+      return __builtin_amdgcn_fdot2(as_h2(m.w), b8, c, false);
     }
     return 0.f;
   }

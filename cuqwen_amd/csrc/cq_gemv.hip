@@ -80,22 +80,18 @@ __device__ __forceinline__ void stage_write(const XStage<Q, NORM, BLK>& st, int 
     u4_t planes[T::PLANES];
 #pragma unroll
     for (int p = 0; p < T::PLANES; ++p) {
-      const h8_t xv = __builtin_bit_cast(h8_t, st.x[i][p]);
-      float v[8];
+      u4_t m = st.x[i][p];
       if constexpr (NORM) {
-        const h8_t wv = __builtin_bit_cast(h8_t, st.w[i][p]);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = (float)(_Float16)((float)xv[e] * (float)wv[e]);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = (float)xv[e];
+        // half(x * w) as one packed multiply per pair: the product of two
+        // fp16 values is exact in fp32, so this rounds exactly like the
+        // fp32 multiply and conversion
+        const u4_t w = st.w[i][p];
+        m.x = as_u32(as_h2(m.x) * as_h2(w.x));
+        m.y = as_u32(as_h2(m.y) * as_h2(w.y));
+        m.z = as_u32(as_h2(m.z) * as_h2(w.z));
+        m.w = as_u32(as_h2(m.w) * as_h2(w.w));
       }
-      _Float16 o[8];
-      corr += plane_order<Q>(v, o);
-      h8_t ov;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) ov[e] = o[e];
-      planes[p] = __builtin_bit_cast(u4_t, ov);
+      corr += plane_order_packed<Q>(m, planes[p]);
     }
 #pragma unroll
     for (int p = 0; p < T::PLANES; ++p) xs[p * NC + c] = planes[p];
@@ -120,9 +116,11 @@ __device__ __forceinline__ float stage_finish(const GemvArgs& a, XStage<Q, NORM,
       if (c0 < NC && c0 + lane < NC) {
 #pragma unroll
         for (int p = 0; p < T::PLANES; ++p) {
-          const h8_t xv = __builtin_bit_cast(h8_t, st.x[i][p]);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) ss += (float)xv[e] * (float)xv[e];
+          const u4_t xv = st.x[i][p];
+          ss = __builtin_amdgcn_fdot2(as_h2(xv.x), as_h2(xv.x), ss, false);
+          ss = __builtin_amdgcn_fdot2(as_h2(xv.y), as_h2(xv.y), ss, false);
+          ss = __builtin_amdgcn_fdot2(as_h2(xv.z), as_h2(xv.z), ss, false);
+          ss = __builtin_amdgcn_fdot2(as_h2(xv.w), as_h2(xv.w), ss, false);
         }
       }
     }
