@@ -652,6 +652,12 @@ static int launch_q(const GemvArgs& a, hipStream_t stream) {
     return norm ? launch_t<Q, MODE, true, true>(a, stream) : launch_t<Q, MODE, false, true>(a, stream);
   } else if constexpr (MODE == GM_RESID) {
     if (norm) return fail(CQ_EINVAL, "gemv: residual mode takes no norm");
+    // short rows (at most two 64-chunk steps, e.g. the 7B o_proj) stream
+    // faster one chunk per lane per step; long rows (down) two
+    if (a.K / QTraits<Q>::EPC <= 2 * kWave) {
+      using TN = GemvTune<MODE>;
+      return launch_variant<Q, MODE, TN::R, 1, false, true, TN::BLK>(a, stream, TN::PER_CU * kNumCUs);
+    }
     return launch_t<Q, MODE, false, true>(a, stream);
   } else {
     return norm ? launch_t<Q, MODE, true, true>(a, stream) : launch_t<Q, MODE, false, true>(a, stream);
