@@ -187,10 +187,12 @@ __global__ __launch_bounds__(kAttnThreads) void attention_stage1(const AttnArgs 
   __shared__ float wm[kAttnWaves][16], wl[kAttnWaves][16];
   __shared__ float wo[kAttnWaves][16][HD + 1];
   if (j == 0) { wm[wave][h] = m; wl[wave][h] = l; }
+  if (h < g) {   // the padding columns of the group are never read
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt)
+    for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) wo[wave][h][dt * 16 + 4 * j + i] = o[dt][i];
+      for (int i = 0; i < 4; ++i) wo[wave][h][dt * 16 + 4 * j + i] = o[dt][i];
+  }
   __syncthreads();
 
   float* ws_m = reinterpret_cast<float*>(a.workspace);

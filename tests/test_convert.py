@@ -1,0 +1,211 @@
+"""The offline checkpoint converter (cuqwen_amd/convert.py, in place of the
+reference exporter export_weights.py:208-325 without its download step).
+
+A tiny Qwen2.5-shaped HuggingFace directory is written here (two safetensors
+shards, BF16 / F16 / F32 tensors), converted, and the output file is parsed
+independently from the documented layout: fp16 tensors must equal the
+exporter's conversion (BF16 bits << 16 -> fp32 -> fp16 round to nearest
+even), projections must equal the oracle's quantizer (pinned against the
+exporter's formulas in test_oracle.py) applied to those fp16 values, and the
+header / lm_head rules must follow export_weights.py:243-322."""
+import json
+import os
+import struct
+
+import numpy as np
+import pytest
+
+import cuqwen_amd as cq
+from cuqwen_amd import convert as cv
+from oracle import oracle as orc
+
+CFG = dict(vocab_size=1000, hidden_size=256, intermediate_size=384, num_hidden_layers=2,
+           num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=512)
+
+
+def _bf16_bits(a, rng):
+    # arbitrary bf16 bit patterns around the values (the converter must take any)
+    u = np.asarray(a, dtype=np.float32).view(np.uint32)
+    return ((u >> 16) ^ rng.integers(0, 2, u.shape, dtype=np.uint32)).astype(np.uint16)
+
+
+def _write_safetensors(path, tensors):
+    """tensors: name -> (dtype string, shape, raw bytes)."""
+    header, blobs, off = {}, [], 0
+    for name, (dt, shape, raw) in tensors.items():
+        header[name] = {"dtype": dt, "shape": list(shape), "data_offsets": [off, off + len(raw)]}
+        blobs.append(raw)
+        off += len(raw)
+    header["__metadata__"] = {"format": "pt"}
+    h = json.dumps(header).encode()
+    h += b" " * (-len(h) % 8)
+    with open(path, "wb") as f:
+        f.write(struct.pack("<Q", len(h)))
+        f.write(h)
+        for b in blobs:
+            f.write(b)
+
+
+def _make_checkpoint(d, tied=False, with_lm_head=True, seed=3):
+    rng = np.random.default_rng(seed)
+    cfg = dict(CFG, tie_word_embeddings=tied)
+    V, D, I, L = cfg["vocab_size"], cfg["hidden_size"], cfg["intermediate_size"], cfg["num_hidden_layers"]
+    hd = D // cfg["num_attention_heads"]
+    qd, kvd = cfg["num_attention_heads"] * hd, cfg["num_key_value_heads"] * hd
+    src = {}   # name -> fp16 array the converter must produce from it
+
+    def add(name, shape, dtype, scale=0.05):
+        v = (rng.standard_normal(shape) * scale).astype(np.float32)
+        if dtype == "BF16":
+            bits = _bf16_bits(v, rng)
+            raw = bits.tobytes()
+            f16 = (bits.astype(np.uint32) << 16).view(np.float32).astype(np.float16)
+        elif dtype == "F16":
+            f16 = v.astype(np.float16)
+            raw = f16.tobytes()
+        else:
+            raw = v.tobytes()
+            f16 = v.astype(np.float16)
+        src[name] = f16.reshape(shape)
+        return name, (dtype, shape, raw)
+
+    shard1, shard2 = {}, {}
+    shard1.update([add("model.embed_tokens.weight", (V, D), "BF16")])
+    for l in range(L):
+        p = f"model.layers.{l}"
+        tgt = shard1 if l == 0 else shard2
+        tgt.update([
+            add(f"{p}.input_layernorm.weight", (D,), "F32", 1.0),
+            add(f"{p}.self_attn.q_proj.weight", (qd, D), "BF16"),
+            add(f"{p}.self_attn.q_proj.bias", (qd,), "F16"),
+            add(f"{p}.self_attn.k_proj.weight", (kvd, D), "BF16"),
+            add(f"{p}.self_attn.k_proj.bias", (kvd,), "BF16"),
+            add(f"{p}.self_attn.v_proj.weight", (kvd, D), "F32"),
+            add(f"{p}.self_attn.v_proj.bias", (kvd,), "BF16"),
+            add(f"{p}.self_attn.o_proj.weight", (D, qd), "BF16"),
+            add(f"{p}.post_attention_layernorm.weight", (D,), "BF16", 1.0),
+            add(f"{p}.mlp.gate_proj.weight", (I, D), "BF16"),
+            add(f"{p}.mlp.up_proj.weight", (I, D), "F16"),
+            add(f"{p}.mlp.down_proj.weight", (D, I), "BF16"),
+        ])
+    shard2.update([add("model.norm.weight", (D,), "BF16", 1.0)])
+    if with_lm_head:
+        shard2.update([add("lm_head.weight", (V, D), "BF16")])
+    os.makedirs(d, exist_ok=True)
+    with open(os.path.join(d, "config.json"), "w") as f:
+        json.dump(cfg, f)
+    _write_safetensors(os.path.join(d, "model-00001-of-00002.safetensors"), shard1)
+    _write_safetensors(os.path.join(d, "model-00002-of-00002.safetensors"), shard2)
+    return cfg, src
+
+
+def _expected_file(cfg, src, quant, lm):
+    """The bytes the exporter would write, built from the layout description."""
+    V, D, I, L = cfg["vocab_size"], cfg["hidden_size"], cfg["intermediate_size"], cfg["num_hidden_layers"]
+    H, KV = cfg["num_attention_heads"], cfg["num_key_value_heads"]
+    hd = D // H
+    qt = {"fp16": 0, "int8": 1, "int4": 2}[quant]
+    lm_fmt = 1 if lm == "int8" else 0
+    out = [struct.pack("<11i", 0x5157454E, V, D, I, L, H, KV, hd, cfg["max_position_embeddings"], qt, lm_fmt)]
+    out.append(b"\0" * (256 - len(out[0])))
+
+    def vec(n):
+        out.append(src[n].tobytes())
+
+    def proj(n, q):
+        if q == 0:
+            out.append(src[n].tobytes())
+        else:
+            w, s = orc.quantize(q, src[n])
+            out.append(w.tobytes())
+            out.append(s.tobytes())
+
+    vec("model.embed_tokens.weight")
+    for l in range(L):
+        p = f"model.layers.{l}"
+        vec(f"{p}.input_layernorm.weight")
+        proj(f"{p}.self_attn.q_proj.weight", qt)
+        vec(f"{p}.self_attn.q_proj.bias")
+        proj(f"{p}.self_attn.k_proj.weight", qt)
+        vec(f"{p}.self_attn.k_proj.bias")
+        proj(f"{p}.self_attn.v_proj.weight", qt)
+        vec(f"{p}.self_attn.v_proj.bias")
+        proj(f"{p}.self_attn.o_proj.weight", qt)
+        vec(f"{p}.post_attention_layernorm.weight")
+        proj(f"{p}.mlp.gate_proj.weight", qt)
+        proj(f"{p}.mlp.up_proj.weight", qt)
+        proj(f"{p}.mlp.down_proj.weight", qt)
+    vec("model.norm.weight")
+    if lm == "int8":
+        proj("lm_head.weight", 1)
+    elif lm == "fp16":
+        vec("lm_head.weight")
+    return b"".join(out)
+
+
+@pytest.mark.parametrize("quant,tied,with_lm,lm", [
+    ("int4", False, True, "int8"),     # quantized untied: int8 lm_head (export_weights.py:243)
+    ("int8", False, True, "int8"),
+    ("fp16", False, True, "fp16"),     # fp16 untied: fp16 lm_head (:318-320)
+    ("int4", True, False, None),       # tied: nothing after the final norm (:321-322)
+    ("int8", True, True, None),        # tied even though an lm_head tensor exists
+])
+def test_convert_matches_exporter_layout(tmp_path, quant, tied, with_lm, lm):
+    d = str(tmp_path / "hf")
+    cfg, src = _make_checkpoint(d, tied=tied, with_lm_head=with_lm)
+    out = str(tmp_path / "model.bin")
+    hdr = cv.convert(d, out, quant)
+    assert hdr["lm_head_fmt"] == (1 if lm == "int8" else 0)
+    got = open(out, "rb").read()
+    want = _expected_file(cfg, src, quant, lm)
+    assert len(got) == len(want)
+    assert got == want
+    # the library accepts it, and decides the lm_head the same way
+    c = cq.read_header(out)
+    assert (c.dim, c.n_layers, c.quant_type, c.lm_head_fmt) == (256, 2, hdr["quant_type"], hdr["lm_head_fmt"])
+    assert bool(c.tied) == (lm is None)
+
+
+def test_bf16_to_fp16_known_answers(tmp_path):
+    """BF16 -> fp32 is exact (bits << 16); fp32 -> fp16 rounds to nearest even."""
+    cases = {0x3F80: 0x3C00,        # 1.0
+             0xBF80: 0xBC00,        # -1.0
+             0x4780: 0x7C00,        # 65536 overflows to +inf
+             0x3380: 0x0001,        # 2^-24: smallest fp16 subnormal
+             0x3300: 0x0000,        # 2^-25: halfway to 0 -> even (0)
+             0x3340: 0x0001,        # 1.5 * 2^-25 -> rounds up
+             0x477F: 0x7BF8}        # 65280 = fp16 max - 224, exactly representable
+    bits = np.array(list(cases), dtype=np.uint16)
+    d = tmp_path / "one"
+    d.mkdir()
+    _write_safetensors(str(d / "a.safetensors"), {"t": ("BF16", (len(bits),), bits.tobytes())})
+    st = cv.SafetensorsDir(str(d))
+    got = st.fp16_rows("t", 0, len(bits)).view(np.uint16)
+    assert list(got) == list(cases.values())
+
+
+def test_convert_errors(tmp_path):
+    d = str(tmp_path / "hf")
+    _make_checkpoint(d)
+    with pytest.raises(cv.ConvertError):
+        cv.convert(d, str(tmp_path / "x.bin"), "int3")
+    # a missing tensor names itself and leaves no output behind
+    os.remove(os.path.join(d, "model-00002-of-00002.safetensors"))
+    with pytest.raises(cv.ConvertError, match="model.layers.1"):
+        cv.convert(d, str(tmp_path / "y.bin"), "int4")
+    assert not os.path.exists(str(tmp_path / "y.bin"))
+    assert not os.path.exists(str(tmp_path / "y.bin.partial"))
+    # unsupported dtype
+    e = tmp_path / "bad"
+    e.mkdir()
+    _write_safetensors(str(e / "a.safetensors"), {"t": ("I8", (4,), b"\0" * 4)})
+    with pytest.raises(cv.ConvertError, match="dtype"):
+        cv.SafetensorsDir(str(e)).fp16_rows("t", 0, 4)
+
+
+def test_convert_cli(tmp_path):
+    d = str(tmp_path / "hf")
+    _make_checkpoint(d)
+    out = str(tmp_path / "cli.bin")
+    assert cv.main([d, "--quant", "int4", "--out", out]) == 0
+    assert cq.read_header(out).quant_type == 2

@@ -109,6 +109,26 @@ def test_decode_tiny_matches_oracle(tmp_path, quant):
     w.free()
 
 
+@pytest.mark.parametrize("quant", ["int4", "fp16"])
+def test_converted_checkpoint_decodes_like_oracle(tmp_path, quant):
+    """A HuggingFace-layout checkpoint through the offline converter (random
+    norm weights and biases, untied lm_head: int8 in the quantized build),
+    loaded on the device, decodes like the oracle reading the same file."""
+    from cuqwen_amd import convert as cv
+    from tests.test_convert import _make_checkpoint
+    d = str(tmp_path / "hf")
+    _make_checkpoint(d, seed=11)
+    path = str(tmp_path / "converted.bin")
+    cv.convert(d, path, quant)
+    cfg, w = cq.load_weights(path)
+    assert cfg.lm_head_fmt == (1 if quant == "int4" else 0) and not cfg.tied
+    om = orc.Model.load(path, cfg, cfg.max_seq_len)
+    prompt = [int(cq.lib.cq_synth_uniform(43, 0, i, cfg.vocab_size)) for i in range(4)]
+    _, _, checked = _teacher_forced(cfg, w, om, prompt, 16, check_kv=False)
+    assert checked >= 8
+    w.free()
+
+
 def test_forward_range_errors():
     cfg = tiny_config(1)
     w = cq.synth_weights(cfg, 3)
