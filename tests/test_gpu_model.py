@@ -169,3 +169,62 @@ def test_config2_qwen05b_int8_decode_parity():
     assert checked >= steps * 0.8
     st.free()
     w.free()
+
+
+def _prefilled_parity(cfg, n_ctx, steps, seed_tok):
+    """KV prefilled with the seeded N(0,1) generator to n_ctx positions on
+    both sides, then `steps` greedy steps; logits within 1e-2 and top-1 equal
+    where the oracle's top-2 gap exceeds 1e-2.  Returns how many were checked."""
+    w = cq.synth_weights(cfg, 0x5157454E)
+    om = orc.Model.synth(cfg, 0x5157454E, n_ctx + steps)
+    om.fill_kv(n_ctx, 77)
+    st = cq.State(cfg, w)
+    st.fill_kv(n_ctx, 77)
+    tok = int(cq.lib.cq_synth_uniform(seed_tok, 0, 0, cfg.vocab_size))
+    hist, checked = [], 0
+    for i in range(steps):
+        ot = om.forward(tok, n_ctx + i, hist)
+        gt = st.forward(tok, n_ctx + i, hist)
+        ol = om.logits()
+        assert np.max(np.abs(st.logits().astype(np.float64) - ol)) <= TOL * np.max(np.abs(ol.astype(np.float64))), i
+        if _gap(ol) > 1e-2:
+            assert gt == ot, (i, gt, ot)
+            checked += 1
+        hist.append(ot)
+        tok = ot
+    st.free()
+    w.free()
+    return checked
+
+
+def test_config3_qwen15b_int4_decode_parity():
+    """BASELINE config 3 (Qwen2.5-1.5B INT4, tied fp16 lm_head): KV prefilled
+    to 4096 positions, then greedy steps at 4096.. against the oracle."""
+    cfg = cq.preset("1.5B", "int4")
+    assert cfg.tied and cfg.lm_head_fmt == 0
+    assert _prefilled_parity(cfg, 4096, 16, 42) >= 12
+
+
+def test_config5_shapes_qwen14b_int4_32k():
+    """BASELINE config 5 shapes (Qwen2.5-14B INT4: d 5120, I 13824, 40 q / 8
+    kv heads, int8 lm_head) at the full 32K context, with 4 of the 48 layers
+    so the host oracle stays within seconds."""
+    cfg = cq.preset("14B", "int4").replace(n_layers=4)
+    assert cfg.lm_head_fmt == 1 and cfg.max_seq_len == 32768
+    assert _prefilled_parity(cfg, 32768 - 4, 4, 43) >= 3
+
+
+def test_config4_qwen7b_int4_32k_bench_workload_parity():
+    """The bench workload itself (Qwen2.5-7B INT4, all 28
+    layers, int8 lm_head) at positions just below 32768."""
+    cfg = cq.preset("7B", "int4")
+    assert _prefilled_parity(cfg, 32768 - 4, 4, 44) >= 3
+
+
+@pytest.mark.parametrize("quant,n_ctx", [("int8", 8192), ("fp16", 1024)])
+def test_config4_qwen7b_other_precisions(quant, n_ctx):
+    """BASELINE config 4 in INT8 at 8K and FP16 at 1K (7B shapes, 8 of the 28
+    layers)."""
+    cfg = cq.preset("7B", quant).replace(n_layers=8)
+    assert _prefilled_parity(cfg, n_ctx, 6, 45) >= 4
+
