@@ -142,6 +142,11 @@ extern "C" int cq_argmax(const void* logits, int32_t* d_token_out, int32_t vocab
                        nullptr, as_stream(stream));
 }
 
+extern "C" int cq_rope(void* q, void* k, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, const int32_t* d_pos,
+                       float rope_theta, void* stream) {
+  return launch_rope((__half*)q, (__half*)k, n_heads, n_kv_heads, head_dim, d_pos, rope_theta, as_stream(stream));
+}
+
 extern "C" int cq_kv_cache_store(const void* k, const void* v, void* kc, void* vc, const int32_t* d_pos,
                                  int32_t n_kv_heads, int32_t max_seq_len, int32_t head_dim, void* stream) {
   return launch_kv_store((const __half*)k, (const __half*)v, (__half*)kc, (__half*)vc, d_pos, n_kv_heads, max_seq_len,

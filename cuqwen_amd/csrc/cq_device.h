@@ -95,6 +95,23 @@ __device__ __forceinline__ float wave_max(float v) {
   return fmaxf(fmaxf(lane_of(v, 0), lane_of(v, 16)), fmaxf(lane_of(v, 32), lane_of(v, 48)));
 }
 
+// NeoX RoPE rotation of one pair (y0, y1) = (v[i], v[i + hd/2])
+// (kernels.cu:370-398): the angle pos * inv_freq (inv_freq = theta^(-2i/hd)
+// in double) is reduced modulo 2 pi in double (2 pi split in a high and a
+// low part) and its sine and cosine taken in fp32; the rotation is rounded
+// at the same points as the reference's fp32 expression.
+__device__ __forceinline__ void rope_rotate(float& y0, float& y1, int pos, double inv_freq) {
+  const double ang = (double)pos * inv_freq;
+  const double k = rint(ang * 0.15915494309189535);                                        // 1 / (2 pi)
+  const double rd = fma(-k, 6.283185307179586232e+00, ang) - k * 2.4492935982947064e-16;   // 2 pi hi + lo
+  float s, c;
+  sincosf((float)rd, &s, &c);
+  const float o0 = add_rn(mul_rn(y0, c), -mul_rn(y1, s));
+  const float o1 = add_rn(mul_rn(y1, c), mul_rn(y0, s));
+  y0 = o0;
+  y1 = o1;
+}
+
 // Order-preserving argmax key (kernels.cu:907-911): a larger float gives a
 // larger key, equal floats let the lower index win (~idx), NaN sorts above
 // +inf.

@@ -321,18 +321,7 @@ __device__ __forceinline__ void qkv_pair(const GemvArgs& a, float y0, float y1, 
   y0 = (float)(_Float16)(y0 + (has_bias ? epi_f(pre.a) : 0.f));   // q/k/v are fp16 before RoPE (kernels.cu:470)
   y1 = (float)(_Float16)(y1 + (has_bias ? epi_f(pre.b) : 0.f));
   const int hd = a.head_dim;
-  if (r0.mat < 2) {
-    // NeoX rotation of (i, i + hd/2) (kernels.cu:370-398)
-    const double ang = (double)pos * inv_freq[r0.row % hd];
-    const double k = rint(ang * 0.15915494309189535);                        // 1 / (2 pi)
-    const double rd = fma(-k, 6.283185307179586232e+00, ang) - k * 2.4492935982947064e-16;   // 2 pi hi + lo
-    float s, c;
-    sincosf((float)rd, &s, &c);
-    const float o0 = add_rn(mul_rn(y0, c), -mul_rn(y1, s));
-    const float o1 = add_rn(mul_rn(y1, c), mul_rn(y0, s));
-    y0 = o0;
-    y1 = o1;
-  }
+  if (r0.mat < 2) rope_rotate(y0, y1, pos, inv_freq[r0.row % hd]);   // q and k only
   const _Float16 h0 = (_Float16)y0, h1 = (_Float16)y1;
   _Float16* out = reinterpret_cast<_Float16*>(sel3(a.out, r0.mat));
   if (out) { out[r0.row] = h0; out[r1.row] = h1; }

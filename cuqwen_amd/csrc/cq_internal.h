@@ -69,6 +69,8 @@ int attention_max_parts(int n_kv);
 // --------------------------------------------------------------- misc ops
 int launch_embedding(const __half* embed, const int* d_token, __half* out, int dim, hipStream_t stream);
 int launch_rmsnorm(const __half* x, const __half* w, __half* out, int dim, float eps, hipStream_t stream);
+int launch_rope(__half* q, __half* k, int n_heads, int n_kv, int head_dim, const int* d_pos, float theta,
+                hipStream_t stream);
 int launch_kv_store(const __half* k, const __half* v, __half* kc, __half* vc, const int* d_pos, int n_kv,
                     int max_seq, int hd, hipStream_t stream);
 // Marks ids d_history[0..*d_history_len) in `stamp` with the value *d_epoch.

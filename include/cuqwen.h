@@ -253,6 +253,14 @@ size_t cq_argmax_workspace_bytes(int32_t vocab);
 int64_t cq_kv_k_offset(int32_t kv_head, int32_t t, int32_t d, int32_t max_seq_len, int32_t head_dim);
 int64_t cq_kv_v_offset(int32_t kv_head, int32_t t, int32_t d, int32_t max_seq_len, int32_t head_dim);
 
+/* apply_rope_kernel (src/kernels.cu:370-398, launched inside
+ * launch_fused_attn_block, kernels.cu:513-517): NeoX rotation of the pairs
+ * (i, i + head_dim/2) of every q head (n_heads x head_dim fp16) and k head
+ * (n_kv_heads x head_dim) in place at position *d_pos, freq = theta^(-2i/hd).
+ * The angle is reduced in double (the reference uses fp32 fast-math). */
+int cq_rope(void* q, void* k, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, const int32_t* d_pos,
+            float rope_theta, void* stream);
+
 /* launch_kv_cache_store (include/kernels.cuh:37, src/kernels.cu:326-367). */
 int cq_kv_cache_store(const void* k, const void* v, void* layer_k_cache, void* layer_v_cache,
                       const int32_t* d_pos, int32_t n_kv_heads, int32_t max_seq_len, int32_t head_dim,

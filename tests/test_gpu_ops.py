@@ -210,6 +210,27 @@ def test_kv_cache_store_layout(g):
     assert not K.any() and not Vv.any()
 
 
+@pytest.mark.parametrize("H,KV,hd", [(14, 2, 64), (28, 4, 128), (40, 8, 128)])
+@pytest.mark.parametrize("pos", [0, 1, 1000, 32767])
+def test_rope_standalone(g, H, KV, hd, pos):
+    """cq_rope (apply_rope_kernel, kernels.cu:370-398) vs the oracle's RoPE;
+    at position 0 the rotation is the identity, bit for bit."""
+    rng = np.random.default_rng(pos + H)
+    q = rng.standard_normal(H * hd).astype(np.float16)
+    k = rng.standard_normal(KV * hd).astype(np.float16)
+    bq, bk = g.empty(q.nbytes), g.empty(k.nbytes)
+    cq.check(cq.lib.cq_memcpy_h2d(bq.ptr, q.ctypes.data, q.nbytes))
+    cq.check(cq.lib.cq_memcpy_h2d(bk.ptr, k.ctypes.data, k.nbytes))
+    cq.check(cq.lib.cq_rope(bq.ptr, bk.ptr, H, KV, hd, g.i32(pos), 1e6, None))
+    gq = bq.to_array(np.float16)
+    gk = bk.to_array(np.float16)
+    if pos == 0:
+        assert np.array_equal(gq.view(np.uint16), q.view(np.uint16))
+        assert np.array_equal(gk.view(np.uint16), k.view(np.uint16))
+    assert rel_err(gq, orc.rope(q, H, hd, pos)) <= TOL
+    assert rel_err(gk, orc.rope(k, KV, hd, pos)) <= TOL
+
+
 @pytest.mark.parametrize("H,KV,hd", [(14, 2, 64), (28, 4, 128), (12, 2, 128), (40, 8, 128), (16, 2, 128)])
 @pytest.mark.parametrize("T", [1, 2, 31, 32, 33, 257, 1000, 4096, 9000])
 def test_attention_parity(g, H, KV, hd, T):
