@@ -1,0 +1,172 @@
+// Device building blocks of the FlashDecoding GQA attention (gfx950): the
+// 32-key K/V tile of one wave, its loads, the online-softmax step with
+// v_mfma_f32_16x16x32_f16, and the run-time partitioning of the context.
+// Shared by the attention kernels and the fused QKV + attention kernel.
+#pragma once
+
+#include "cq_device.h"
+#include "cq_internal.h"
+
+namespace cq {
+
+constexpr int kAttnWaves = 8;
+constexpr int kAttnThreads = kAttnWaves * kWave;
+constexpr int kAttnBlocksTarget = 256;   // one block per CU of MI355X
+constexpr int kMinTilesPerPart = 8;      // 256 keys: one tile per wave at least
+constexpr int kTileKeys = 32;
+
+template <int HD>
+struct KVTile {
+  h8_t ka[2][HD / 32];
+  h8_t va[HD / 16];
+};
+
+template <int HD>
+__device__ __forceinline__ void load_tile(KVTile<HD>& t, const _Float16* kbase, const _Float16* vbase, int ti,
+                                          int lane) {
+  const _Float16* kt = kbase + (int64_t)ti * kTileKeys * HD;
+  const _Float16* vt = vbase + (int64_t)ti * kTileKeys * HD;
+#pragma unroll
+  for (int st = 0; st < 2; ++st)
+#pragma unroll
+    for (int kk = 0; kk < HD / 32; ++kk)
+      t.ka[st][kk] = __builtin_bit_cast(h8_t, load_u4_stream(kt + st * 16 * HD + (kk * 64 + lane) * 8));
+#pragma unroll
+  for (int dt = 0; dt < HD / 16; ++dt) t.va[dt] = __builtin_bit_cast(h8_t, load_u4_stream(vt + (dt * 64 + lane) * 8));
+}
+
+// One 32-key tile of the online softmax for this wave.
+template <int HD>
+__device__ __forceinline__ void attend_tile(KVTile<HD>& t, const h8_t* qb, int ti, int T, float scale, int j,
+                                            float& m, float& l, f4_t* o) {
+  constexpr int KK = HD / 32, DT = HD / 16;
+  f4_t s[2];
+#pragma unroll
+  for (int st = 0; st < 2; ++st) {
+    s[st] = f4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) s[st] = __builtin_amdgcn_mfma_f32_16x16x32_f16(t.ka[st][kk], qb[kk], s[st], 0, 0, 0);
+  }
+  // lane holds S^T[key = ti*32 + st*16 + 4j + i][head]
+  const int key0 = ti * kTileKeys + 4 * j;
+  const bool tail = (ti + 1) * kTileKeys > T;
+  float sv[8];
+  float mt = -INFINITY;
+#pragma unroll
+  for (int st = 0; st < 2; ++st)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float v = (float)(_Float16)(s[st][i] * scale);
+      if (tail && key0 + st * 16 + i >= T) v = -INFINITY;
+      sv[st * 4 + i] = v;
+      mt = fmaxf(mt, v);
+    }
+  mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
+  mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
+  const float mn = fmaxf(m, mt);
+  const float alpha = __expf(m - mn);
+  m = mn;
+  l *= alpha;
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
+  h8_t pb;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float p = __expf(sv[e] - mn);
+    l += p;
+    pb[e] = (_Float16)p;
+  }
+  if (tail) {
+    // keys past the end may hold anything; keep them out of P*V
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int key = ti * kTileKeys + (e < 4 ? 4 * j + e : 16 + 4 * j + e - 4);
+        if (key >= T) t.va[dt][e] = (_Float16)0.f;
+      }
+  }
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(t.va[dt], pb, o[dt], 0, 0, 0);
+}
+
+__device__ __forceinline__ int attn_nparts(int T, int P, int* tpp_out) {
+  const int n_tiles = (T + kTileKeys - 1) / kTileKeys;
+  int tpp = (n_tiles + P - 1) / P;
+  if (tpp < kMinTilesPerPart) tpp = kMinTilesPerPart;
+  *tpp_out = tpp;
+  return (n_tiles + tpp - 1) / tpp;
+}
+
+
+// The wave's tiles ti, ti + 8, ... < tile1 of a partition, double-buffered:
+// `A` already holds (or has in flight) tile ti; the next tile goes into the
+// other buffer before the current one is computed.  On return m / l / o hold
+// the wave's online-softmax state (l summed over the lane's 4 key slots).
+template <int HD>
+__device__ __forceinline__ void attend_partition(KVTile<HD>& A, KVTile<HD>& B, const h8_t* qb, int ti, int tile1,
+                                                 int T, const _Float16* kbase, const _Float16* vbase, int lane,
+                                                 float& m, float& l, f4_t* o) {
+  const int j = lane >> 4;
+  const float scale = 1.0f / sqrtf((float)HD);
+  for (; ti < tile1; ti += 2 * kAttnWaves) {
+    const int t1 = ti + kAttnWaves;
+    if (t1 < tile1) load_tile<HD>(B, kbase, vbase, t1, lane);
+    attend_tile<HD>(A, qb, ti, T, scale, j, m, l, o);
+    if (t1 >= tile1) break;
+    if (t1 + kAttnWaves < tile1) load_tile<HD>(A, kbase, vbase, t1 + kAttnWaves, lane);
+    attend_tile<HD>(B, qb, t1, T, scale, j, m, l, o);
+  }
+  l += __shfl_xor(l, 16, kWave);
+  l += __shfl_xor(l, 32, kWave);
+}
+
+// Merge of the block's 8 waves in LDS (per wave m[16], l[16], O[16][HD]);
+// the block writes one (m, l, O) partial into the workspace, or the
+// normalised output itself when a single partition covers the context.
+template <int HD>
+__device__ __forceinline__ void block_merge_write(const AttnArgs& a, int kvh, int part, int nparts, int g, float m,
+                                                  float l, const f4_t* o) {
+  constexpr int DT = HD / 16;
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int h = lane & 15, j = lane >> 4;
+  __shared__ float wm[kAttnWaves][16], wl[kAttnWaves][16];
+  __shared__ float wo[kAttnWaves][16][HD + 1];
+  if (j == 0) { wm[wave][h] = m; wl[wave][h] = l; }
+  if (h < g) {   // the padding columns of the group are never read
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) wo[wave][h][dt * 16 + 4 * j + i] = o[dt][i];
+  }
+  __syncthreads();
+
+  float* ws_m = reinterpret_cast<float*>(a.workspace);
+  const int Pmax = gridDim.x;
+  float* ws_l = ws_m + (size_t)a.n_kv * Pmax * 16;
+  float* ws_o = ws_l + (size_t)a.n_kv * Pmax * 16;
+  const size_t pslot = (size_t)kvh * Pmax + part;
+  _Float16* out = reinterpret_cast<_Float16*>(a.out);
+
+  for (int idx = threadIdx.x; idx < g * HD; idx += kAttnThreads) {
+    const int hh = idx / HD, d = idx % HD;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, wm[w][hh]);
+    float L = 0.f, O = 0.f;
+#pragma unroll
+    for (int w = 0; w < kAttnWaves; ++w) {
+      const float f = wm[w][hh] == -INFINITY ? 0.f : __expf(wm[w][hh] - M);
+      L += wl[w][hh] * f;
+      O += wo[w][hh][d] * f;
+    }
+    if (nparts == 1) {
+      out[(int64_t)(kvh * g + hh) * HD + d] = (_Float16)(O * (1.0f / (L + 1e-9f)));
+    } else {
+      ws_o[(pslot * 16 + hh) * HD + d] = O;
+      if (d == 0) { ws_m[pslot * 16 + hh] = M; ws_l[pslot * 16 + hh] = L; }
+    }
+  }
+}
+
+}  // namespace cq

@@ -23,18 +23,11 @@
 // Rounding follows the reference: scores are rounded to fp16 after the
 // 1/sqrt(hd) scale (kernels.cu:171), probabilities are rounded to fp16 for
 // the PV product while the row sum uses the unrounded values (:185-186).
-#include "cq_device.h"
-#include "cq_internal.h"
+#include "cq_attention.h"
 
 #include <cmath>
 
 namespace cq {
-
-constexpr int kAttnWaves = 8;
-constexpr int kAttnThreads = kAttnWaves * kWave;
-constexpr int kAttnBlocksTarget = 256;   // one block per CU of MI355X
-constexpr int kMinTilesPerPart = 8;      // 256 keys: one tile per wave at least
-constexpr int kTileKeys = 32;
 
 int attention_max_parts(int n_kv) { return (kAttnBlocksTarget + n_kv - 1) / n_kv; }
 
@@ -43,89 +36,6 @@ size_t attention_workspace_bytes(int n_heads, int n_kv, int head_dim) {
   (void)n_heads;
   const size_t P = (size_t)attention_max_parts(n_kv);
   return (size_t)n_kv * P * 16 * (2 + (size_t)head_dim) * sizeof(float);
-}
-
-template <int HD>
-struct KVTile {
-  h8_t ka[2][HD / 32];
-  h8_t va[HD / 16];
-};
-
-template <int HD>
-__device__ __forceinline__ void load_tile(KVTile<HD>& t, const _Float16* kbase, const _Float16* vbase, int ti,
-                                          int lane) {
-  const _Float16* kt = kbase + (int64_t)ti * kTileKeys * HD;
-  const _Float16* vt = vbase + (int64_t)ti * kTileKeys * HD;
-#pragma unroll
-  for (int st = 0; st < 2; ++st)
-#pragma unroll
-    for (int kk = 0; kk < HD / 32; ++kk)
-      t.ka[st][kk] = __builtin_bit_cast(h8_t, load_u4_stream(kt + st * 16 * HD + (kk * 64 + lane) * 8));
-#pragma unroll
-  for (int dt = 0; dt < HD / 16; ++dt) t.va[dt] = __builtin_bit_cast(h8_t, load_u4_stream(vt + (dt * 64 + lane) * 8));
-}
-
-// One 32-key tile of the online softmax for this wave.
-template <int HD>
-__device__ __forceinline__ void attend_tile(KVTile<HD>& t, const h8_t* qb, int ti, int T, float scale, int j,
-                                            float& m, float& l, f4_t* o) {
-  constexpr int KK = HD / 32, DT = HD / 16;
-  f4_t s[2];
-#pragma unroll
-  for (int st = 0; st < 2; ++st) {
-    s[st] = f4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk) s[st] = __builtin_amdgcn_mfma_f32_16x16x32_f16(t.ka[st][kk], qb[kk], s[st], 0, 0, 0);
-  }
-  // lane holds S^T[key = ti*32 + st*16 + 4j + i][head]
-  const int key0 = ti * kTileKeys + 4 * j;
-  const bool tail = (ti + 1) * kTileKeys > T;
-  float sv[8];
-  float mt = -INFINITY;
-#pragma unroll
-  for (int st = 0; st < 2; ++st)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float v = (float)(_Float16)(s[st][i] * scale);
-      if (tail && key0 + st * 16 + i >= T) v = -INFINITY;
-      sv[st * 4 + i] = v;
-      mt = fmaxf(mt, v);
-    }
-  mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
-  mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
-  const float mn = fmaxf(m, mt);
-  const float alpha = __expf(m - mn);
-  m = mn;
-  l *= alpha;
-#pragma unroll
-  for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
-  h8_t pb;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const float p = __expf(sv[e] - mn);
-    l += p;
-    pb[e] = (_Float16)p;
-  }
-  if (tail) {
-    // keys past the end may hold anything; keep them out of P*V
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int key = ti * kTileKeys + (e < 4 ? 4 * j + e : 16 + 4 * j + e - 4);
-        if (key >= T) t.va[dt][e] = (_Float16)0.f;
-      }
-  }
-#pragma unroll
-  for (int dt = 0; dt < DT; ++dt) o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(t.va[dt], pb, o[dt], 0, 0, 0);
-}
-
-__device__ __forceinline__ int attn_nparts(int T, int P, int* tpp_out) {
-  const int n_tiles = (T + kTileKeys - 1) / kTileKeys;
-  int tpp = (n_tiles + P - 1) / P;
-  if (tpp < kMinTilesPerPart) tpp = kMinTilesPerPart;
-  *tpp_out = tpp;
-  return (n_tiles + tpp - 1) / tpp;
 }
 
 template <int HD>
@@ -147,7 +57,6 @@ __global__ __launch_bounds__(kAttnThreads) void attention_stage1(const AttnArgs 
 
   const int h = lane & 15;        // query head column of this lane
   const int j = lane >> 4;        // k-slot group of this lane
-  const float scale = 1.0f / sqrtf((float)HD);
 
   const _Float16* kbase = reinterpret_cast<const _Float16*>(a.kcache) + (int64_t)kvh * a.max_seq * HD;
   const _Float16* vbase = reinterpret_cast<const _Float16*>(a.vcache) + (int64_t)kvh * a.max_seq * HD;
@@ -171,56 +80,8 @@ __global__ __launch_bounds__(kAttnThreads) void attention_stage1(const AttnArgs 
   f4_t o[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) o[dt] = f4_t{0.f, 0.f, 0.f, 0.f};
-
-  for (; ti < tile1; ti += 2 * kAttnWaves) {
-    const int t1 = ti + kAttnWaves;
-    if (t1 < tile1) load_tile<HD>(B, kbase, vbase, t1, lane);
-    attend_tile<HD>(A, qb, ti, T, scale, j, m, l, o);
-    if (t1 >= tile1) break;
-    if (t1 + kAttnWaves < tile1) load_tile<HD>(A, kbase, vbase, t1 + kAttnWaves, lane);
-    attend_tile<HD>(B, qb, t1, T, scale, j, m, l, o);
-  }
-  l += __shfl_xor(l, 16, kWave);
-  l += __shfl_xor(l, 32, kWave);
-
-  // ---- merge the 8 waves in LDS: per wave m[16], l[16], O[16][HD]
-  __shared__ float wm[kAttnWaves][16], wl[kAttnWaves][16];
-  __shared__ float wo[kAttnWaves][16][HD + 1];
-  if (j == 0) { wm[wave][h] = m; wl[wave][h] = l; }
-  if (h < g) {   // the padding columns of the group are never read
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) wo[wave][h][dt * 16 + 4 * j + i] = o[dt][i];
-  }
-  __syncthreads();
-
-  float* ws_m = reinterpret_cast<float*>(a.workspace);
-  const int Pmax = gridDim.x;
-  float* ws_l = ws_m + (size_t)a.n_kv * Pmax * 16;
-  float* ws_o = ws_l + (size_t)a.n_kv * Pmax * 16;
-  const size_t pslot = (size_t)kvh * Pmax + part;
-  _Float16* out = reinterpret_cast<_Float16*>(a.out);
-
-  for (int idx = threadIdx.x; idx < g * HD; idx += kAttnThreads) {
-    const int hh = idx / HD, d = idx % HD;
-    float M = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, wm[w][hh]);
-    float L = 0.f, O = 0.f;
-#pragma unroll
-    for (int w = 0; w < kAttnWaves; ++w) {
-      const float f = wm[w][hh] == -INFINITY ? 0.f : __expf(wm[w][hh] - M);
-      L += wl[w][hh] * f;
-      O += wo[w][hh][d] * f;
-    }
-    if (nparts == 1) {
-      out[(int64_t)(kvh * g + hh) * HD + d] = (_Float16)(O * (1.0f / (L + 1e-9f)));
-    } else {
-      ws_o[(pslot * 16 + hh) * HD + d] = O;
-      if (d == 0) { ws_m[pslot * 16 + hh] = M; ws_l[pslot * 16 + hh] = L; }
-    }
-  }
+  attend_partition<HD>(A, B, qb, ti, tile1, T, kbase, vbase, lane, m, l, o);
+  block_merge_write<HD>(a, kvh, part, nparts, g, m, l, o);
 }
 
 // Stage 2: log-sum-exp merge of the partitions (kernels.cu:222-288) with
@@ -284,13 +145,12 @@ int launch_attention(const AttnArgs& a, hipStream_t stream) {
     return fail(CQ_EINVAL, "attention: null pointer");
   const int P = attention_max_parts(a.n_kv);
   const dim3 grid(P, a.n_kv);
-  if (a.head_dim == 128) {
-    hipLaunchKernelGGL(attention_stage1<128>, grid, dim3(kAttnThreads), 0, stream, a);
+  if (a.head_dim == 128) hipLaunchKernelGGL(attention_stage1<128>, grid, dim3(kAttnThreads), 0, stream, a);
+  else hipLaunchKernelGGL(attention_stage1<64>, grid, dim3(kAttnThreads), 0, stream, a);
+  if (a.head_dim == 128)
     hipLaunchKernelGGL(attention_stage2<128>, dim3(a.n_heads * (128 / kMergeDims)), dim3(kWave), 0, stream, a, P);
-  } else {
-    hipLaunchKernelGGL(attention_stage1<64>, grid, dim3(kAttnThreads), 0, stream, a);
+  else
     hipLaunchKernelGGL(attention_stage2<64>, dim3(a.n_heads * (64 / kMergeDims)), dim3(kWave), 0, stream, a, P);
-  }
   CQ_HIP(hipGetLastError());
   return CQ_OK;
 }
