@@ -95,6 +95,8 @@ def _load():
         "cq_state_kv_read": (I32, [P, I32, I32, I32, I32, P]),
         "cq_state_kv_write": (I32, [P, I32, I32, I32, I32, P]),
         "cq_state_last_decode_us": (I32, [P, ctypes.POINTER(ctypes.c_double)]),
+        "cq_prefill": (I32, [P, IP, I32, I32, IP]),
+        "cq_state_last_prefill_us": (I32, [P, ctypes.POINTER(ctypes.c_double)]),
         "cq_synth_normal": (ctypes.c_uint16, [U64, U64, U64, F]),
         "cq_synth_uniform": (ctypes.c_uint32, [U64, U64, U64, ctypes.c_uint32]),
         "cq_tensor_stream_id": (U64, [I32, I32]),
@@ -144,6 +146,7 @@ EXPORTED = [
     "cq_last_error", "cq_config_preset", "cq_read_header", "cq_write_synthetic_file", "cq_load_weights",
     "cq_synth_weights", "cq_free_weights", "cq_weights_tensor", "cq_state_create", "cq_state_destroy",
     "cq_forward", "cq_decode", "cq_state_logits", "cq_state_fill_kv", "cq_state_kv_read", "cq_state_kv_write",
+    "cq_prefill", "cq_state_last_prefill_us",
     "cq_state_last_decode_us", "cq_synth_normal", "cq_synth_uniform", "cq_tensor_stream_id", "cq_kv_stream_id",
     "cq_quantize", "cq_device_count", "cq_malloc", "cq_free", "cq_memcpy_h2d", "cq_memcpy_d2h", "cq_memset", "cq_memcpy_d2d",
     "cq_synchronize", "cq_embedding_lookup", "cq_rmsnorm", "cq_gemv", "cq_gemv_add", "cq_fused_attn_block",
@@ -323,6 +326,20 @@ class State:
                             hist.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)) if hist.size else None,
                             int(hist.size), out.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))))
         return out
+
+    def prefill(self, tokens, pos0=0):
+        """Prompt tokens at positions pos0..: KV cache filled, returns the
+        greedy id after the last one (src/main.cu:87-92 semantics)."""
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        out = ctypes.c_int32(-1)
+        check(lib.cq_prefill(self.handle, t.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), int(t.size), int(pos0),
+                             ctypes.byref(out)))
+        return out.value
+
+    def last_prefill_us(self):
+        us = ctypes.c_double()
+        check(lib.cq_state_last_prefill_us(self.handle, ctypes.byref(us)))
+        return us.value
 
     def last_decode_us(self):
         us = ctypes.c_double()

@@ -7,6 +7,7 @@
 #include "cq_format.h"
 #include "cq_internal.h"
 
+#include <algorithm>
 #include <cstdio>
 #include <cstring>
 #include <memory>
@@ -167,6 +168,12 @@ struct cq_state {
   hipGraphExec_t exec = nullptr;
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
   double last_us = 0.0;
+  double last_prefill_us = 0.0;
+  // batched-prefill workspace, allocated on the first cq_prefill
+  char* pf_arena = nullptr;
+  __half *pf_x = nullptr, *pf_a = nullptr, *pf_q = nullptr, *pf_ao = nullptr, *pf_inter = nullptr;
+  float* pf_inv = nullptr;
+  int* pf_tokens = nullptr;
 };
 
 namespace {
@@ -490,6 +497,7 @@ extern "C" int cq_state_destroy(cq_state* s) {
   if (s->ev0) hipEventDestroy(s->ev0);
   if (s->ev1) hipEventDestroy(s->ev1);
   if (s->host_pinned) hipHostFree(s->host_pinned);
+  if (s->pf_arena) hipFree(s->pf_arena);
   if (s->stream) hipStreamDestroy(s->stream);
   if (s->arena) hipFree(s->arena);
   delete s;
@@ -597,6 +605,110 @@ extern "C" int cq_state_kv_write(cq_state* s, int32_t layer, int32_t kv_head, in
     for (int d = 0; d < hd; ++d)
       tmp[(size_t)(kind == 0 ? kv_k_offset(0, t, d, ms, hd) : kv_v_offset(0, t, d, ms, hd))] = host_in[(size_t)t * hd + d];
   CQ_HIP(hipMemcpy(base, tmp.data(), halves * 2, hipMemcpyHostToDevice));
+  return CQ_OK;
+}
+
+// ------------------------------------------------------------ prefill
+namespace {
+
+constexpr int kPrefillChunk = 512;   // tokens per pass through the layers
+
+int prefill_workspace(cq_state* s) {
+  if (s->pf_arena) return CQ_OK;
+  const cq_config& c = s->cfg;
+  const size_t C = kPrefillChunk, d = c.dim, qd = (size_t)c.n_heads * c.head_dim, I = c.intermediate_size;
+  size_t off = 0;
+  auto take = [&](size_t bytes) { size_t o = off; off = align_up(off + bytes); return o; };
+  const size_t o_x = take(C * d * 2), o_a = take(C * d * 2), o_q = take(C * qd * 2), o_ao = take(C * qd * 2),
+               o_i = take(C * I * 2), o_inv = take(C * 4), o_t = take(C * 4);
+  if (hipMalloc(&s->pf_arena, off) != hipSuccess) return fail(CQ_ENOMEM, "prefill: workspace allocation failed");
+  char* a = s->pf_arena;
+  s->pf_x = (__half*)(a + o_x); s->pf_a = (__half*)(a + o_a); s->pf_q = (__half*)(a + o_q);
+  s->pf_ao = (__half*)(a + o_ao); s->pf_inter = (__half*)(a + o_i); s->pf_inv = (float*)(a + o_inv);
+  s->pf_tokens = (int*)(a + o_t);
+  return CQ_OK;
+}
+
+// tokens[0..n) at positions pos0.. through every layer, M tokens at a time;
+// fills the KV cache (the residual stream of the last layer is not needed).
+int prefill_batched(cq_state* s, const int32_t* tokens, int n, int pos0) {
+  CQ_TRY(prefill_workspace(s));
+  const cq_config& c = s->cfg;
+  hipStream_t st = s->stream;
+  const int d = c.dim, qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim, I = c.intermediate_size;
+  for (int c0 = 0; c0 < n; c0 += kPrefillChunk) {
+    const int M = std::min(kPrefillChunk, n - c0);
+    CQ_HIP(hipMemcpyAsync(s->pf_tokens, tokens + c0, (size_t)M * 4, hipMemcpyHostToDevice, st));
+    CQ_TRY(launch_pf_embed(s->w->embed, s->pf_tokens, M, d, s->pf_x, st));
+    for (int l = 0; l < c.n_layers; ++l) {
+      const LayerW& L = s->w->layers[l];
+      _Float16* kc = (_Float16*)(s->kcache + (size_t)l * s->layer_kv_halves);
+      _Float16* vc = (_Float16*)(s->vcache + (size_t)l * s->layer_kv_halves);
+      CQ_TRY(launch_pf_norm(s->pf_x, L.in_norm, c.norm_eps, M, d, s->pf_a, s->pf_inv, st));
+      PfGemmArgs g;
+      g.mode = GM_QKV; g.quant = c.quant_type; g.A = (const _Float16*)s->pf_a; g.inv = s->pf_inv;
+      g.M = M; g.N = qd + 2 * kvd; g.K = d;
+      g.W[0] = L.wq; g.W[1] = L.wk; g.W[2] = L.wv;
+      g.S[0] = (const _Float16*)L.sq; g.S[1] = (const _Float16*)L.sk; g.S[2] = (const _Float16*)L.sv;
+      g.bias[0] = (const _Float16*)L.bq; g.bias[1] = (const _Float16*)L.bk; g.bias[2] = (const _Float16*)L.bv;
+      g.rows[0] = qd; g.rows[1] = kvd; g.rows[2] = kvd;
+      g.out = (_Float16*)s->pf_q; g.head_dim = c.head_dim; g.pos0 = pos0 + c0; g.max_seq = c.max_seq_len;
+      g.inv_freq = s->rope_inv_freq; g.kcache = kc; g.vcache = vc;
+      CQ_TRY(launch_pf_gemm(g, st));
+      PfAttnArgs at;
+      at.q = (const _Float16*)s->pf_q; at.kcache = kc; at.vcache = vc; at.out = (_Float16*)s->pf_ao;
+      at.M = M; at.pos0 = pos0 + c0; at.n_heads = c.n_heads; at.n_kv = c.n_kv_heads; at.head_dim = c.head_dim;
+      at.max_seq = c.max_seq_len;
+      CQ_TRY(launch_pf_attention(at, st));
+      if (l == c.n_layers - 1) break;   // the last layer's residual stream feeds nothing here
+      PfGemmArgs o;
+      o.mode = GM_RESID; o.quant = c.quant_type; o.A = (const _Float16*)s->pf_ao; o.M = M; o.N = d; o.K = qd;
+      o.W[0] = L.wo; o.S[0] = (const _Float16*)L.so; o.rows[0] = d; o.out = (_Float16*)s->pf_x;
+      CQ_TRY(launch_pf_gemm(o, st));
+      CQ_TRY(launch_pf_norm(s->pf_x, L.post_norm, c.norm_eps, M, d, s->pf_a, s->pf_inv, st));
+      PfGemmArgs m1;
+      m1.mode = GM_SWIGLU; m1.quant = c.quant_type; m1.A = (const _Float16*)s->pf_a; m1.inv = s->pf_inv;
+      m1.M = M; m1.N = I; m1.K = d; m1.W[0] = L.wg; m1.W[1] = L.wu;
+      m1.S[0] = (const _Float16*)L.sg; m1.S[1] = (const _Float16*)L.su; m1.rows[0] = I; m1.rows[1] = I;
+      m1.out = (_Float16*)s->pf_inter;
+      CQ_TRY(launch_pf_gemm(m1, st));
+      PfGemmArgs m2;
+      m2.mode = GM_RESID; m2.quant = c.quant_type; m2.A = (const _Float16*)s->pf_inter; m2.M = M; m2.N = d; m2.K = I;
+      m2.W[0] = L.wd; m2.S[0] = (const _Float16*)L.sd; m2.rows[0] = d; m2.out = (_Float16*)s->pf_x;
+      CQ_TRY(launch_pf_gemm(m2, st));
+    }
+  }
+  return CQ_OK;
+}
+
+}  // namespace
+
+extern "C" int cq_prefill(cq_state* s, const int32_t* tokens, int32_t n_tokens, int32_t pos0, int32_t* token_out) {
+  if (!s || !tokens) return fail(CQ_EINVAL, "prefill: null argument");
+  if (n_tokens <= 0) return fail(CQ_EINVAL, "prefill: no tokens");
+  if (pos0 < 0 || (int64_t)pos0 + n_tokens > s->cfg.max_seq_len) return fail(CQ_ERANGE, "prefill: positions exceed max_seq_len");
+  for (int i = 0; i < n_tokens; ++i)
+    if (tokens[i] < 0 || tokens[i] >= s->cfg.vocab_size) return fail(CQ_ERANGE, "prefill: token outside the vocabulary");
+  CQ_TRY(ensure_graph(s));   // recorded before any prefill work is queued on the stream
+  CQ_HIP(hipEventRecord(s->ev0, s->stream));
+  if (n_tokens > 1) CQ_TRY(prefill_batched(s, tokens, n_tokens - 1, pos0));
+  // the last prompt token is a normal decode step: logits, argmax (no
+  // penalty history, like the reference's prefill loop)
+  CQ_TRY(set_ctl(s, tokens[n_tokens - 1], pos0 + n_tokens - 1, nullptr, 0, 0));
+  CQ_HIP(hipGraphLaunch(s->exec, s->stream));
+  CQ_HIP(hipEventRecord(s->ev1, s->stream));
+  CQ_HIP(hipMemcpyAsync(s->host_pinned + 8, &s->ctl->sampled, sizeof(int), hipMemcpyDeviceToHost, s->stream));
+  CQ_HIP(hipStreamSynchronize(s->stream));
+  float ms = 0.f;
+  CQ_HIP(hipEventElapsedTime(&ms, s->ev0, s->ev1));
+  s->last_prefill_us = (double)ms * 1000.0;
+  if (token_out) *token_out = s->host_pinned[8];
+  return CQ_OK;
+}
+
+extern "C" int cq_state_last_prefill_us(cq_state* s, double* us) {
+  if (!s || !us) return fail(CQ_EINVAL, "null argument");
+  *us = s->last_prefill_us;
   return CQ_OK;
 }
 

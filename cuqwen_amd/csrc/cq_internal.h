@@ -66,6 +66,40 @@ size_t attention_workspace_bytes(int n_heads, int n_kv, int head_dim);
 int launch_attention(const AttnArgs& a, hipStream_t stream);
 int attention_max_parts(int n_kv);
 
+// ---------------------------------------------------------------- prefill
+// M-token GEMM on the matrix cores (cq_prefill.hip).  A: [M][K] activations
+// in the permuted 8-group layout; rows[]: rows of W[0..2] (QKV: q, k, v;
+// otherwise rows[0] = N); out: RESID -> [M][N] residual (natural, in place),
+// SWIGLU -> [M][N] (permuted), QKV -> q [M][rows[0]] (natural) + KV cache.
+struct PfGemmArgs {
+  int mode = GM_RESID;
+  int quant = CQ_QUANT_FP16;
+  const _Float16* A = nullptr;
+  const float* inv = nullptr;   // [M] RMSNorm scale (QKV, SWIGLU)
+  int M = 0, N = 0, K = 0;
+  const void* W[3] = {nullptr, nullptr, nullptr};
+  const _Float16* S[3] = {nullptr, nullptr, nullptr};
+  const _Float16* bias[3] = {nullptr, nullptr, nullptr};
+  int rows[3] = {0, 0, 0};
+  _Float16* out = nullptr;
+  int head_dim = 0, pos0 = 0, max_seq = 0;
+  const double* inv_freq = nullptr;
+  _Float16* kcache = nullptr;
+  _Float16* vcache = nullptr;
+};
+struct PfAttnArgs {
+  const _Float16* q = nullptr;   // [M][n_heads * hd] natural
+  const _Float16* kcache = nullptr;
+  const _Float16* vcache = nullptr;
+  _Float16* out = nullptr;       // [M][n_heads * hd] permuted
+  int M = 0, pos0 = 0, n_heads = 0, n_kv = 0, head_dim = 0, max_seq = 0;
+};
+int launch_pf_norm(const __half* x, const __half* w, float eps, int M, int dim, __half* A, float* inv,
+                   hipStream_t stream);
+int launch_pf_embed(const __half* embed, const int* tokens, int M, int dim, __half* x, hipStream_t stream);
+int launch_pf_gemm(const PfGemmArgs& a, hipStream_t stream);
+int launch_pf_attention(const PfAttnArgs& a, hipStream_t stream);
+
 // --------------------------------------------------------------- misc ops
 int launch_embedding(const __half* embed, const int* d_token, __half* out, int dim, hipStream_t stream);
 int launch_rmsnorm(const __half* x, const __half* w, __half* out, int dim, float eps, hipStream_t stream);

@@ -1,0 +1,515 @@
+// Batched prefill for gfx950: the prompt goes through the layers M tokens at
+// a time instead of one decode step per token (the reference's prefill loop,
+// src/main.cu:87-92, calls qwen_forward once per prompt token; batched
+// prefill is its roadmap item, README.md:145).
+//
+// Per layer and chunk of M tokens:
+//   pf_norm_rows    x -> half(x * w) and rsqrt(mean(x^2) + eps) per token
+//                   (the decode GEMVs' fused RMSNorm, kernels.cu:689-751)
+//   pf_gemm<QKV>    Q / K / V rows, bias, RoPE at each token's position, K / V
+//                   into the cache (kernels.cu:402-474, :370-398, :326-347)
+//   pf_attention    causal FlashDecoding over the cache (kernels.cu:105-288
+//                   with a per-token key limit)
+//   pf_gemm<RESID>  O-proj + residual (kernels.cu:640-687)
+//   pf_norm_rows, pf_gemm<SWIGLU> (kernels.cu:523-585), pf_gemm<RESID> (down)
+// The GEMMs are M > 1, so they run on the matrix cores: each wave dequantizes
+// its weight rows in registers (int4 / int8 to exact small-integer fp16) as
+// the A operand of v_mfma_f32_16x16x32_f16 and takes 16-token slices of the
+// activation tile, staged in LDS, as the B operand.  Quantized rows are
+// summed per 128-wide group in fp32 and scaled by the group's fp16 scale, as
+// the decode path does per chunk.
+//
+// Activation layout: the inputs of the GEMMs (normed x, attention output,
+// SwiGLU output) are stored with each group of 8 consecutive elements in the
+// order [0,4,1,5,2,6,3,7] -- the order in which the int4 / int8 unpack yields
+// weight pairs -- so neither operand needs a shuffle in the main loop.
+#include "cq_attention.h"
+#include "cq_gemv.h"
+
+namespace cq {
+
+constexpr int kPfThreads = 256;   // 4 waves
+constexpr int kPfBM = 64;         // tokens per GEMM block (4 slices of 16)
+constexpr int kPfRowsPerWave = 32;
+constexpr int kPfBN = 4 * kPfRowsPerWave;   // weight rows per GEMM block
+constexpr int kPfK = 128;         // K per main-loop step (one quantization group)
+constexpr int kPfLdsStride = kPfK + 8;     // halves per token row in LDS (16-byte skew)
+
+// position of element k in the permuted activation layout
+__device__ __forceinline__ int pf_pos(int k) {
+  const int e = k & 7;
+  return (k & ~7) | (e < 4 ? 2 * e : 2 * e - 7);
+}
+
+// ------------------------------------------------------------- row norm
+// One block per token row: A[m] = half(x * w) (permuted), inv[m] =
+// rsqrt(mean(x^2) + half(eps)).  Without w, A = x (permuted) and no inv.
+__global__ __launch_bounds__(256) void pf_norm_rows(const _Float16* x, const _Float16* w, float eps, int dim,
+                                                    _Float16* A, float* inv) {
+  __shared__ float red[16];
+  const int m = blockIdx.x;
+  const _Float16* xr = x + (int64_t)m * dim;
+  _Float16* ar = A + (int64_t)m * dim;
+  float ss = 0.f;
+  for (int k = threadIdx.x; k < dim; k += blockDim.x) {
+    const float v = (float)xr[k];
+    ss = fmaf(v, v, ss);
+    ar[pf_pos(k)] = w ? (_Float16)(v * (float)w[k]) : xr[k];
+  }
+  if (w) {
+    ss = block_sum(ss, red);
+    if (threadIdx.x == 0) inv[m] = rsqrtf(ss / (float)dim + (float)(_Float16)eps);
+  }
+}
+
+// Embedding rows of the chunk's tokens (kernels.cu:85-103).
+__global__ __launch_bounds__(256) void pf_embed(const u4_t* embed, const int* tokens, u4_t* x, int vec_dim) {
+  const int m = blockIdx.x;
+  const int64_t t = tokens[m];
+  for (int i = threadIdx.x; i < vec_dim; i += blockDim.x) x[(int64_t)m * vec_dim + i] = embed[t * vec_dim + i];
+}
+
+// ------------------------------------------------------------------ GEMM
+template <int Q> struct PfW;   // 16-byte weight loads per lane per 128-wide step
+template <> struct PfW<CQ_QUANT_INT4> { static constexpr int LOADS = 1; };
+template <> struct PfW<CQ_QUANT_INT8> { static constexpr int LOADS = 2; };
+template <> struct PfW<CQ_QUANT_FP16> { static constexpr int LOADS = 4; };
+
+// The A operand (8 fp16 weights in the order [0,4,1,5,2,6,3,7] of true k
+// j*32 + s*8 + e) for sub-step s from the lane's loaded bytes.
+template <int Q>
+__device__ __forceinline__ h8_t pf_unpack(const u4_t* w, int s) {
+  u4_t o;
+  if constexpr (Q == CQ_QUANT_INT4) {
+    const uint32_t f = w[0][s] ^ kInt4Flip;   // nibble = q + 8
+    const h2_t bias = {(_Float16)-1032.f, (_Float16)-1032.f};
+    o.x = as_u32(as_h2((f & 0x000F000Fu) | 0x64006400u) + bias);
+    o.y = as_u32(as_h2(((f >> 4) & 0x000F000Fu) | 0x64006400u) + bias);
+    o.z = as_u32(as_h2(((f >> 8) & 0x000F000Fu) | 0x64006400u) + bias);
+    o.w = as_u32(as_h2(((f >> 12) & 0x000F000Fu) | 0x64006400u) + bias);
+  } else if constexpr (Q == CQ_QUANT_INT8) {
+    // bytes 8s..8s+7 of the lane's 32: words w0 (b0..b3), w1 (b4..b7)
+    const uint32_t w0 = w[s >> 1][(s & 1) * 2] ^ kInt8Flip, w1 = w[s >> 1][(s & 1) * 2 + 1] ^ kInt8Flip;
+    const h2_t bias = {(_Float16)-1152.f, (_Float16)-1152.f};
+    // (byte i of w0, 0, byte i of w1, 0) | 0x6400 6400 = (1024 + u0, 1024 + u4)
+    o.x = as_u32(as_h2(__builtin_amdgcn_perm(w1, w0, 0x0c040c00u) | 0x64006400u) + bias);
+    o.y = as_u32(as_h2(__builtin_amdgcn_perm(w1, w0, 0x0c050c01u) | 0x64006400u) + bias);
+    o.z = as_u32(as_h2(__builtin_amdgcn_perm(w1, w0, 0x0c060c02u) | 0x64006400u) + bias);
+    o.w = as_u32(as_h2(__builtin_amdgcn_perm(w1, w0, 0x0c070c03u) | 0x64006400u) + bias);
+  } else {
+    const u4_t h = w[s];   // halves e0..e7 in words (e0,e1) (e2,e3) (e4,e5) (e6,e7)
+    o.x = __builtin_amdgcn_perm(h.z, h.x, 0x05040100u);   // (e0, e4)
+    o.y = __builtin_amdgcn_perm(h.z, h.x, 0x07060302u);   // (e1, e5)
+    o.z = __builtin_amdgcn_perm(h.w, h.y, 0x05040100u);   // (e2, e6)
+    o.w = __builtin_amdgcn_perm(h.w, h.y, 0x07060302u);   // (e3, e7)
+  }
+  return __builtin_bit_cast(h8_t, o);
+}
+
+// Row r of the concatenated output (QKV: q rows, then k, then v) -> matrix.
+__device__ __forceinline__ int pf_mat(const PfGemmArgs& a, int row, int* local) {
+  if (row < a.rows[0]) { *local = row; return 0; }
+  if (row < a.rows[0] + a.rows[1]) { *local = row - a.rows[0]; return 1; }
+  *local = row - a.rows[0] - a.rows[1];
+  return 2;
+}
+
+template <int Q>
+__device__ __forceinline__ void pf_load_w(const PfGemmArgs& a, const char* rowp, int ks, int j, u4_t* w) {
+  constexpr int L = PfW<Q>::LOADS;
+  const char* p = rowp + (int64_t)ks * (64 * L) + j * (L * 16);   // 64*L bytes of the row per step, L*16 per lane
+#pragma unroll
+  for (int i = 0; i < L; ++i) w[i] = load_u4(p + i * 16);
+}
+
+// C^T tile of a wave: NMAT matrices (SwiGLU: gate and up) x RT row slices of
+// 16 x 4 token slices of 16; lane holds rows 4*(lane/16)+v, token lane%16.
+template <int Q, int MODE>
+__global__ __launch_bounds__(kPfThreads) void pf_gemm_kernel(const PfGemmArgs a) {
+  constexpr int NMAT = MODE == GM_SWIGLU ? 2 : 1;
+  constexpr int RT = MODE == GM_SWIGLU ? 1 : 2;   // SwiGLU: 16 gate + 16 up rows per wave
+  constexpr int WROWS = RT * 16;
+  constexpr int BN = 4 * WROWS;
+  constexpr int L = PfW<Q>::LOADS;
+  __shared__ _Float16 xs[2][kPfBM * kPfLdsStride];   // double-buffered activation tile
+  __shared__ _Float16 ot[MODE == GM_QKV ? kPfBN * kPfBM : 1];   // QKV epilogue tile (rows x tokens)
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int r = lane & 15, j = lane >> 4;
+  const int m0 = blockIdx.y * kPfBM;
+  const int nb0 = blockIdx.x * BN;             // first output row of the block
+  const int nw0 = nb0 + wave * WROWS;          // first output row of the wave
+  const int K = a.K, nks = K / kPfK;
+
+  // weight row pointers of the lane (A operand row r of each slice)
+  const char* rowp[NMAT][RT];
+  const _Float16* srow[NMAT][RT][4];   // scale rows of the lane's 4 output rows
+#pragma unroll
+  for (int mt = 0; mt < NMAT; ++mt)
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      int local, row = min(nw0 + rt * 16 + r, a.N - 1);
+      const int mat = MODE == GM_SWIGLU ? mt : pf_mat(a, row, &local);
+      if (MODE == GM_SWIGLU) local = row;
+      const int64_t rbytes = Q == CQ_QUANT_INT4 ? K / 2 : Q == CQ_QUANT_INT8 ? K : 2 * K;
+      rowp[mt][rt] = reinterpret_cast<const char*>(a.W[mat]) + (int64_t)local * rbytes;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        int l2, row2 = min(nw0 + rt * 16 + 4 * j + v, a.N - 1);
+        const int mat2 = MODE == GM_SWIGLU ? mt : pf_mat(a, row2, &l2);
+        if (MODE == GM_SWIGLU) l2 = row2;
+        srow[mt][rt][v] = Q == CQ_QUANT_FP16 ? nullptr : a.S[mat2] + (int64_t)l2 * (K / kGroup);
+      }
+    }
+
+  // activation tile loader: thread t moves 4 x 16 bytes of the 64 x 128 tile
+  auto x_load = [&](int ks, u4_t* v) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = threadIdx.x + i * kPfThreads;   // 16-byte chunk of the tile, 16 per token row
+      const int m = min(m0 + c / 16, a.M - 1);
+      v[i] = load_u4(a.A + (int64_t)m * K + ks * kPfK + (c % 16) * 8);
+    }
+  };
+  auto x_store = [&](int buf, const u4_t* v) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = threadIdx.x + i * kPfThreads;
+      *reinterpret_cast<u4_t*>(&xs[buf][(c / 16) * kPfLdsStride + (c % 16) * 8]) = v[i];
+    }
+  };
+
+  f4_t acc[NMAT][RT][4];
+#pragma unroll
+  for (int mt = 0; mt < NMAT; ++mt)
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) acc[mt][rt][tt] = f4_t{0.f, 0.f, 0.f, 0.f};
+
+  u4_t xv[4], wv[NMAT][RT][L];
+  x_load(0, xv);
+#pragma unroll
+  for (int mt = 0; mt < NMAT; ++mt)
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) pf_load_w<Q>(a, rowp[mt][rt], 0, j, wv[mt][rt]);
+  x_store(0, xv);
+  __syncthreads();
+
+  for (int ks = 0; ks < nks; ++ks) {
+    const int buf = ks & 1;
+    // next step's activations and weights in flight during this step's MMAs
+    u4_t wn[NMAT][RT][L];
+    const int kn = min(ks + 1, nks - 1);
+    x_load(kn, xv);
+#pragma unroll
+    for (int mt = 0; mt < NMAT; ++mt)
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) pf_load_w<Q>(a, rowp[mt][rt], kn, j, wn[mt][rt]);
+    _Float16 sc[NMAT][RT][4];
+    if constexpr (Q != CQ_QUANT_FP16) {
+#pragma unroll
+      for (int mt = 0; mt < NMAT; ++mt)
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) sc[mt][rt][v] = srow[mt][rt][v][ks];
+    }
+
+    f4_t part[NMAT][RT][4];
+#pragma unroll
+    for (int mt = 0; mt < NMAT; ++mt)
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt)
+          part[mt][rt][tt] = Q == CQ_QUANT_FP16 ? acc[mt][rt][tt] : f4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      h8_t xb[4];
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt)
+        xb[tt] = *reinterpret_cast<const h8_t*>(&xs[buf][(tt * 16 + r) * kPfLdsStride + j * 32 + s * 8]);
+#pragma unroll
+      for (int mt = 0; mt < NMAT; ++mt)
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+          const h8_t wa = pf_unpack<Q>(wv[mt][rt], s);
+#pragma unroll
+          for (int tt = 0; tt < 4; ++tt)
+            part[mt][rt][tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, xb[tt], part[mt][rt][tt], 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int mt = 0; mt < NMAT; ++mt)
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
+          if constexpr (Q == CQ_QUANT_FP16) {
+            acc[mt][rt][tt] = part[mt][rt][tt];
+          } else {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) acc[mt][rt][tt][v] = fmaf((float)sc[mt][rt][v], part[mt][rt][tt][v], acc[mt][rt][tt][v]);
+          }
+        }
+#pragma unroll
+    for (int mt = 0; mt < NMAT; ++mt)
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int i = 0; i < L; ++i) wv[mt][rt][i] = wn[mt][rt][i];
+    if (ks + 1 < nks) x_store(buf ^ 1, xv);
+    __syncthreads();
+  }
+
+  // ---- epilogues: lane holds rows nw0 + rt*16 + 4j + v, token m0 + tt*16 + r
+  if constexpr (MODE == GM_RESID) {
+    _Float16* y = a.out;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int n = nw0 + rt * 16 + 4 * j + v, m = m0 + tt * 16 + r;
+          if (n < a.N && m < a.M) {
+            _Float16* p = y + (int64_t)m * a.N + n;
+            *p = (_Float16)((float)*p + acc[0][rt][tt][v]);   // residual stays fp16 (kernels.cu:621)
+          }
+        }
+  } else if constexpr (MODE == GM_SWIGLU) {
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int n = nw0 + 4 * j + v, m = m0 + tt * 16 + r;
+        if (n < a.N && m < a.M) {
+          const float s = a.inv[m];
+          const float g = acc[0][0][tt][v] * s, u = acc[1][0][tt][v] * s;
+          const float sig = 1.f / (1.f + expf(-g));   // kernels.cu:566
+          a.out[(int64_t)m * a.N + pf_pos(n)] = (_Float16)((g * sig) * u);
+        }
+      }
+  } else {
+    // QKV: scale, bias, fp16 into LDS; then pairs (i, i + hd/2) of each head
+    // rotate (q, k) and go to Q or the KV cache
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int nl = wave * WROWS + rt * 16 + 4 * j + v, ml = tt * 16 + r;
+          const int n = nb0 + nl, m = min(m0 + ml, a.M - 1);
+          int local;
+          const int mat = pf_mat(a, min(n, a.N - 1), &local);
+          const _Float16* b = a.bias[mat];
+          const float y = acc[0][rt][tt][v] * a.inv[m] + (b ? (float)b[local] : 0.f);
+          ot[nl * kPfBM + ml] = (_Float16)y;   // q/k/v are fp16 before RoPE (kernels.cu:470)
+        }
+    __syncthreads();
+    const int hd = a.head_dim, half = hd / 2;
+    for (int idx = threadIdx.x; idx < (kPfBN / 2) * kPfBM; idx += kPfThreads) {
+      const int ml = idx % kPfBM, pi = idx / kPfBM;   // pair pi of the block's 64 pairs
+      const int nl0 = (pi / half) * hd + pi % half, nl1 = nl0 + half;
+      const int n0 = nb0 + nl0, m = m0 + ml;
+      if (n0 >= a.N || m >= a.M) continue;
+      int local;
+      const int mat = pf_mat(a, n0, &local);
+      float y0 = (float)ot[nl0 * kPfBM + ml], y1 = (float)ot[nl1 * kPfBM + ml];
+      const int pos = a.pos0 + m, i = local % hd;
+      if (mat < 2) rope_rotate(y0, y1, pos, a.inv_freq[i]);
+      const _Float16 h0 = (_Float16)y0, h1 = (_Float16)y1;
+      if (mat == 0) {
+        a.out[(int64_t)m * a.rows[0] + local] = h0;
+        a.out[(int64_t)m * a.rows[0] + local + half] = h1;
+      } else {
+        const int kvh = local / hd;
+        _Float16* c = mat == 1 ? a.kcache : a.vcache;
+        if (mat == 1) {
+          c[kv_k_offset(kvh, pos, i, a.max_seq, hd)] = h0;
+          c[kv_k_offset(kvh, pos, i + half, a.max_seq, hd)] = h1;
+        } else {
+          c[kv_v_offset(kvh, pos, i, a.max_seq, hd)] = h0;
+          c[kv_v_offset(kvh, pos, i + half, a.max_seq, hd)] = h1;
+        }
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------ causal attention
+// Block = (16 consecutive tokens, one query head): the 16 tokens are the
+// columns of S^T = K Q^T; 8 waves take every 8th 32-key tile up to the last
+// token's position (double-buffered like the decode kernel), keys past a
+// token's own position are masked per column, and the waves merge in LDS.
+// Output rows are written in the GEMM activation layout.
+template <int HD>
+__device__ __forceinline__ void pf_attend_tile(KVTile<HD>& t, const h8_t* qb, int ti, int t_lane, int t_max,
+                                               float scale, int j, float& m, float& l, f4_t* o) {
+  constexpr int KK = HD / 32, DT = HD / 16;
+  f4_t s[2];
+#pragma unroll
+  for (int st = 0; st < 2; ++st) {
+    s[st] = f4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) s[st] = __builtin_amdgcn_mfma_f32_16x16x32_f16(t.ka[st][kk], qb[kk], s[st], 0, 0, 0);
+  }
+  const int key0 = ti * kTileKeys + 4 * j;
+  float sv[8];
+  float mt = -INFINITY;
+#pragma unroll
+  for (int st = 0; st < 2; ++st)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float v = (float)(_Float16)(s[st][i] * scale);   // kernels.cu:171
+      if (key0 + st * 16 + i >= t_lane) v = -INFINITY;
+      sv[st * 4 + i] = v;
+      mt = fmaxf(mt, v);
+    }
+  mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
+  mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
+  const float mn = fmaxf(m, mt);
+  // a column can have no valid key yet (its token precedes this tile)
+  const float alpha = m == -INFINITY ? 0.f : __expf(m - mn);
+  m = mn;
+  l *= alpha;
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
+  h8_t pb;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float p = sv[e] == -INFINITY ? 0.f : __expf(sv[e] - mn);
+    l += p;
+    pb[e] = (_Float16)p;
+  }
+  if ((ti + 1) * kTileKeys > t_max) {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int key = ti * kTileKeys + (e < 4 ? 4 * j + e : 16 + 4 * j + e - 4);
+        if (key >= t_max) t.va[dt][e] = (_Float16)0.f;
+      }
+  }
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(t.va[dt], pb, o[dt], 0, 0, 0);
+}
+
+template <int HD>
+__global__ __launch_bounds__(kAttnThreads) void pf_attention_kernel(const PfAttnArgs a) {
+  constexpr int KK = HD / 32, DT = HD / 16;
+  const int t0 = blockIdx.x * 16, hq = blockIdx.y;
+  const int g = a.n_heads / a.n_kv, kvh = hq / g;
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int h = lane & 15, j = lane >> 4;   // h: token column
+  const int tcol = min(t0 + h, a.M - 1);
+  const int t_lane = a.pos0 + tcol + 1;                       // keys visible to this column
+  const int t_max = a.pos0 + min(t0 + 16, a.M);               // keys visible to the block
+  const int n_tiles = (t_max + kTileKeys - 1) / kTileKeys;
+  const float scale = 1.0f / sqrtf((float)HD);
+  const _Float16* kbase = a.kcache + (int64_t)kvh * a.max_seq * HD;
+  const _Float16* vbase = a.vcache + (int64_t)kvh * a.max_seq * HD;
+  KVTile<HD> A, B;
+  int ti = wave;
+  if (ti < n_tiles) load_tile<HD>(A, kbase, vbase, ti, lane);
+  h8_t qb[KK];
+  const _Float16* q = a.q + (int64_t)tcol * a.n_heads * HD + hq * HD;
+#pragma unroll
+  for (int kk = 0; kk < KK; ++kk) qb[kk] = __builtin_bit_cast(h8_t, load_u4(q + kk * 32 + j * 8));
+  float m = -INFINITY, l = 0.f;
+  f4_t o[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) o[dt] = f4_t{0.f, 0.f, 0.f, 0.f};
+  for (; ti < n_tiles; ti += 2 * kAttnWaves) {
+    const int t1 = ti + kAttnWaves;
+    if (t1 < n_tiles) load_tile<HD>(B, kbase, vbase, t1, lane);
+    pf_attend_tile<HD>(A, qb, ti, t_lane, t_max, scale, j, m, l, o);
+    if (t1 >= n_tiles) break;
+    if (t1 + kAttnWaves < n_tiles) load_tile<HD>(A, kbase, vbase, t1 + kAttnWaves, lane);
+    pf_attend_tile<HD>(B, qb, t1, t_lane, t_max, scale, j, m, l, o);
+  }
+  l += __shfl_xor(l, 16, kWave);
+  l += __shfl_xor(l, 32, kWave);
+
+  __shared__ float wm[kAttnWaves][16], wl[kAttnWaves][16];
+  __shared__ float wo[kAttnWaves][16][HD + 1];
+  if (j == 0) { wm[wave][h] = m; wl[wave][h] = l; }
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) wo[wave][h][dt * 16 + 4 * j + i] = o[dt][i];
+  __syncthreads();
+  const int qd = a.n_heads * HD;
+  for (int idx = threadIdx.x; idx < 16 * HD; idx += kAttnThreads) {
+    const int c = idx / HD, d = idx % HD;
+    if (t0 + c >= a.M) continue;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, wm[w][c]);
+    float L = 0.f, O = 0.f;
+#pragma unroll
+    for (int w = 0; w < kAttnWaves; ++w) {
+      const float f = wm[w][c] == -INFINITY ? 0.f : __expf(wm[w][c] - M);
+      L += wl[w][c] * f;
+      O += wo[w][c][d] * f;
+    }
+    a.out[(int64_t)(t0 + c) * qd + pf_pos(hq * HD + d)] = (_Float16)(O * (1.0f / (L + 1e-9f)));
+  }
+}
+
+// ------------------------------------------------------------------ host
+int launch_pf_norm(const __half* x, const __half* w, float eps, int M, int dim, __half* A, float* inv,
+                   hipStream_t stream) {
+  hipLaunchKernelGGL(pf_norm_rows, dim3(M), dim3(256), 0, stream, (const _Float16*)x, (const _Float16*)w, eps, dim,
+                     (_Float16*)A, inv);
+  CQ_HIP(hipGetLastError());
+  return CQ_OK;
+}
+
+int launch_pf_embed(const __half* embed, const int* tokens, int M, int dim, __half* x, hipStream_t stream) {
+  hipLaunchKernelGGL(pf_embed, dim3(M), dim3(256), 0, stream, reinterpret_cast<const u4_t*>(embed), tokens,
+                     reinterpret_cast<u4_t*>(x), dim / 8);
+  CQ_HIP(hipGetLastError());
+  return CQ_OK;
+}
+
+template <int Q>
+static void launch_pf_gemm_q(const PfGemmArgs& a, hipStream_t stream) {
+  const int bn = a.mode == GM_SWIGLU ? 64 : kPfBN;
+  const dim3 grid((a.N + bn - 1) / bn, (a.M + kPfBM - 1) / kPfBM);
+  if (a.mode == GM_QKV) hipLaunchKernelGGL((pf_gemm_kernel<Q, GM_QKV>), grid, dim3(kPfThreads), 0, stream, a);
+  else if (a.mode == GM_SWIGLU) hipLaunchKernelGGL((pf_gemm_kernel<Q, GM_SWIGLU>), grid, dim3(kPfThreads), 0, stream, a);
+  else hipLaunchKernelGGL((pf_gemm_kernel<Q, GM_RESID>), grid, dim3(kPfThreads), 0, stream, a);
+}
+
+int launch_pf_gemm(const PfGemmArgs& a, hipStream_t stream) {
+  if (a.M <= 0 || a.N <= 0 || a.K <= 0 || a.K % kPfK) return fail(CQ_EINVAL, "prefill gemm: K must be a multiple of 128");
+  if (!a.A || !a.W[0] || !a.out) return fail(CQ_EINVAL, "prefill gemm: null operand");
+  if (a.quant != CQ_QUANT_FP16 && !a.S[0]) return fail(CQ_EINVAL, "prefill gemm: quantized weights need scales");
+  if (a.mode == GM_SWIGLU && (!a.W[1] || !a.inv)) return fail(CQ_EINVAL, "prefill gemm: swiglu needs gate, up and the norm");
+  if (a.mode == GM_QKV) {
+    if (!a.inv || !a.W[1] || !a.W[2] || !a.kcache || !a.vcache || !a.inv_freq) return fail(CQ_EINVAL, "prefill gemm: qkv operands");
+    if (kPfBN % a.head_dim || a.rows[0] % a.head_dim || a.rows[1] % a.head_dim || a.rows[0] + a.rows[1] + a.rows[2] != a.N)
+      return fail(CQ_EINVAL, "prefill gemm: qkv rows must be whole heads");
+  }
+  switch (a.quant) {
+    case CQ_QUANT_FP16: launch_pf_gemm_q<CQ_QUANT_FP16>(a, stream); break;
+    case CQ_QUANT_INT8: launch_pf_gemm_q<CQ_QUANT_INT8>(a, stream); break;
+    default: launch_pf_gemm_q<CQ_QUANT_INT4>(a, stream); break;
+  }
+  CQ_HIP(hipGetLastError());
+  return CQ_OK;
+}
+
+int launch_pf_attention(const PfAttnArgs& a, hipStream_t stream) {
+  if (a.head_dim != 64 && a.head_dim != 128) return fail(CQ_EINVAL, "prefill attention: head_dim must be 64 or 128");
+  if (a.M <= 0 || a.pos0 < 0 || a.pos0 + a.M > a.max_seq) return fail(CQ_ERANGE, "prefill attention: positions");
+  const dim3 grid((a.M + 15) / 16, a.n_heads);
+  if (a.head_dim == 128) hipLaunchKernelGGL(pf_attention_kernel<128>, grid, dim3(kAttnThreads), 0, stream, a);
+  else hipLaunchKernelGGL(pf_attention_kernel<64>, grid, dim3(kAttnThreads), 0, stream, a);
+  CQ_HIP(hipGetLastError());
+  return CQ_OK;
+}
+
+}  // namespace cq

@@ -128,6 +128,20 @@ int cq_forward(cq_state* s, int32_t token, int32_t pos, const int32_t* history,
 int cq_decode(cq_state* s, int32_t token, int32_t pos0, int32_t n_steps,
               const int32_t* history, int32_t history_len, int32_t* tokens_out);
 
+/* Prompt processing.  The reference's prefill loop (src/main.cu:87-92) runs
+ * one qwen_forward per prompt token with no penalty history; this entry
+ * point gives the same result with tokens[0..n_tokens-1) pushed through the
+ * layers in batches (matrix-core GEMMs and a causal attention kernel, up to
+ * 512 tokens per pass) and the last token run as a decode step.  Fills the
+ * KV cache for positions [pos0, pos0 + n_tokens); *token_out receives the
+ * greedy id after the last prompt token and cq_state_logits its logits.
+ * Errors: CQ_ERANGE for positions past max_seq_len or ids outside the
+ * vocabulary. */
+int cq_prefill(cq_state* s, const int32_t* tokens, int32_t n_tokens, int32_t pos0, int32_t* token_out);
+
+/* Device time (microseconds) of the last cq_prefill call. */
+int cq_state_last_prefill_us(cq_state* s, double* us);
+
 /* Copy the fp16 logits of the last step (after the repetition penalty, as the
  * reference's state.logits holds them) to host memory (vocab_size halves). */
 int cq_state_logits(cq_state* s, uint16_t* host_out);
