@@ -34,6 +34,8 @@ def parse():
     ap.add_argument("--ctx", type=int, default=32768, help="context length at the end of the timed steps")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-profile", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--prompt", type=int, default=1024, help="prompt tokens of the batched-prefill measurement")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a 256 MiB device-to-device copy (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -84,6 +86,35 @@ def gemv_config1(cq, np):
         b[1].free()
     return {"shape": "M=1 K=4864 N=896 W8A16 g128", "us": round(us.value, 3), "bytes": alg,
             "GBps": round(alg / us.value / 1e3, 1), "frac": round(alg / us.value / 1e3 / PEAK_GBPS, 4)}
+
+
+def prefill_leg(cq, cfg, st, n):
+    """Batched prefill of an n-token synthetic prompt at position 0 (after the
+    decode measurement; it overwrites the first n cache slots), against the
+    reference's prefill-by-decode (one decode step per prompt token,
+    src/main.cu:87-92) timed on the same state at the same positions.
+    Matrix-core roofline: the GEMM flops of the batched tokens over the whole
+    prefill time (attention, norms and the last token's decode step included)."""
+    prompt = [int(cq.lib.cq_synth_uniform(42, 0, i, cfg.vocab_size)) for i in range(n)]
+    st.prefill(prompt, 0)   # workspace allocation, first-touch
+    best = None
+    for _ in range(3):
+        st.prefill(prompt, 0)
+        us = st.last_prefill_us()
+        best = us if best is None else min(best, us)
+    t0 = time.perf_counter()
+    steps = min(n, 32)
+    st.decode(prompt[0], 0, steps)
+    cq.synchronize()
+    by_decode_ms = (time.perf_counter() - t0) * 1e3 / steps * n
+    d, I, L = cfg.dim, cfg.intermediate_size, cfg.n_layers
+    qd, kvd = cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim
+    flops = 2.0 * (n - 1) * (L * (qd + 2 * kvd) * d + (L - 1) * (d * qd + 3 * I * d))
+    tflops = flops / (best * 1e-6) / 1e12
+    return {"prompt_tokens": n, "ms": round(best / 1e3, 3), "tok_per_s": round(n / (best * 1e-6), 1),
+            "prefill_by_decode_ms": round(by_decode_ms, 2), "speedup": round(by_decode_ms / (best / 1e3), 2),
+            "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": 2500.0, "unit": "TFLOP/s",
+                         "frac": round(tflops / 2500.0, 4)}}
 
 
 def cpu_baseline(cfg, ctx, threads):
@@ -164,6 +195,10 @@ def main():
     if not args.no_profile:
         g1 = gemv_config1(cq, np)
         log(f"[bench] config-1 GEMV: {g1}")
+    pf = None
+    if not args.no_prefill:
+        pf = prefill_leg(cq, cfg, st, args.prompt)
+        log(f"[bench] prefill: {pf}")
     st.free()
     w.free()
     if args.calib_copy:
@@ -192,7 +227,7 @@ def main():
                    "model": f"Qwen2.5-{args.model}", "global_batch": 1, "seq_len": args.ctx,
                    "parallelism": "single-gpu"},
         "device_ms_per_step": round(dev_us / 1e3, 5),
-        "roofline": roof, "cpu_baseline": cpu, "kernels": kernels, "gemv_config1": g1,
+        "roofline": roof, "cpu_baseline": cpu, "kernels": kernels, "gemv_config1": g1, "prefill": pf,
     }
     print(json.dumps(res), flush=True)
 

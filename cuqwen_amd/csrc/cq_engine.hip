@@ -173,7 +173,10 @@ struct cq_state {
   char* pf_arena = nullptr;
   __half *pf_x = nullptr, *pf_a = nullptr, *pf_q = nullptr, *pf_ao = nullptr, *pf_inter = nullptr;
   float* pf_inv = nullptr;
+  float* pf_part = nullptr;   // split-K partials of the prefill GEMMs
   int* pf_tokens = nullptr;
+  int* pf_tokens_host = nullptr;   // pinned staging of a chunk's ids
+  hipEvent_t pf_copied = nullptr;  // the staging buffer's last upload has completed
 };
 
 namespace {
@@ -498,6 +501,8 @@ extern "C" int cq_state_destroy(cq_state* s) {
   if (s->ev1) hipEventDestroy(s->ev1);
   if (s->host_pinned) hipHostFree(s->host_pinned);
   if (s->pf_arena) hipFree(s->pf_arena);
+  if (s->pf_tokens_host) hipHostFree(s->pf_tokens_host);
+  if (s->pf_copied) hipEventDestroy(s->pf_copied);
   if (s->stream) hipStreamDestroy(s->stream);
   if (s->arena) hipFree(s->arena);
   delete s;
@@ -611,7 +616,8 @@ extern "C" int cq_state_kv_write(cq_state* s, int32_t layer, int32_t kv_head, in
 // ------------------------------------------------------------ prefill
 namespace {
 
-constexpr int kPrefillChunk = 512;   // tokens per pass through the layers
+constexpr int kPrefillChunk = 2048;   // tokens per pass through the layers
+constexpr size_t kPrefillPartBytes = 64u << 20;   // split-K partials (small chunks)
 
 int prefill_workspace(cq_state* s) {
   if (s->pf_arena) return CQ_OK;
@@ -620,12 +626,16 @@ int prefill_workspace(cq_state* s) {
   size_t off = 0;
   auto take = [&](size_t bytes) { size_t o = off; off = align_up(off + bytes); return o; };
   const size_t o_x = take(C * d * 2), o_a = take(C * d * 2), o_q = take(C * qd * 2), o_ao = take(C * qd * 2),
-               o_i = take(C * I * 2), o_inv = take(C * 4), o_t = take(C * 4);
+               o_i = take(C * I * 2), o_inv = take(C * 4), o_t = take(C * 4), o_p = take(kPrefillPartBytes);
   if (hipMalloc(&s->pf_arena, off) != hipSuccess) return fail(CQ_ENOMEM, "prefill: workspace allocation failed");
   char* a = s->pf_arena;
   s->pf_x = (__half*)(a + o_x); s->pf_a = (__half*)(a + o_a); s->pf_q = (__half*)(a + o_q);
   s->pf_ao = (__half*)(a + o_ao); s->pf_inter = (__half*)(a + o_i); s->pf_inv = (float*)(a + o_inv);
   s->pf_tokens = (int*)(a + o_t);
+  s->pf_part = (float*)(a + o_p);
+  if (hipHostMalloc((void**)&s->pf_tokens_host, C * 4, hipHostMallocDefault) != hipSuccess)
+    return fail(CQ_ENOMEM, "prefill: pinned staging allocation failed");
+  CQ_HIP(hipEventCreateWithFlags(&s->pf_copied, hipEventDisableTiming));
   return CQ_OK;
 }
 
@@ -638,7 +648,11 @@ int prefill_batched(cq_state* s, const int32_t* tokens, int n, int pos0) {
   const int d = c.dim, qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim, I = c.intermediate_size;
   for (int c0 = 0; c0 < n; c0 += kPrefillChunk) {
     const int M = std::min(kPrefillChunk, n - c0);
-    CQ_HIP(hipMemcpyAsync(s->pf_tokens, tokens + c0, (size_t)M * 4, hipMemcpyHostToDevice, st));
+    // the pinned staging buffer is refilled only once its previous upload is done
+    CQ_HIP(hipEventSynchronize(s->pf_copied));
+    std::memcpy(s->pf_tokens_host, tokens + c0, (size_t)M * 4);
+    CQ_HIP(hipMemcpyAsync(s->pf_tokens, s->pf_tokens_host, (size_t)M * 4, hipMemcpyHostToDevice, st));
+    CQ_HIP(hipEventRecord(s->pf_copied, st));
     CQ_TRY(launch_pf_embed(s->w->embed, s->pf_tokens, M, d, s->pf_x, st));
     for (int l = 0; l < c.n_layers; ++l) {
       const LayerW& L = s->w->layers[l];
@@ -654,6 +668,7 @@ int prefill_batched(cq_state* s, const int32_t* tokens, int n, int pos0) {
       g.rows[0] = qd; g.rows[1] = kvd; g.rows[2] = kvd;
       g.out = (_Float16*)s->pf_q; g.head_dim = c.head_dim; g.pos0 = pos0 + c0; g.max_seq = c.max_seq_len;
       g.inv_freq = s->rope_inv_freq; g.kcache = kc; g.vcache = vc;
+      g.part = s->pf_part; g.part_bytes = kPrefillPartBytes;
       CQ_TRY(launch_pf_gemm(g, st));
       PfAttnArgs at;
       at.q = (const _Float16*)s->pf_q; at.kcache = kc; at.vcache = vc; at.out = (_Float16*)s->pf_ao;
@@ -664,6 +679,7 @@ int prefill_batched(cq_state* s, const int32_t* tokens, int n, int pos0) {
       PfGemmArgs o;
       o.mode = GM_RESID; o.quant = c.quant_type; o.A = (const _Float16*)s->pf_ao; o.M = M; o.N = d; o.K = qd;
       o.W[0] = L.wo; o.S[0] = (const _Float16*)L.so; o.rows[0] = d; o.out = (_Float16*)s->pf_x;
+      o.part = s->pf_part; o.part_bytes = kPrefillPartBytes;
       CQ_TRY(launch_pf_gemm(o, st));
       CQ_TRY(launch_pf_norm(s->pf_x, L.post_norm, c.norm_eps, M, d, s->pf_a, s->pf_inv, st));
       PfGemmArgs m1;
@@ -671,10 +687,12 @@ int prefill_batched(cq_state* s, const int32_t* tokens, int n, int pos0) {
       m1.M = M; m1.N = I; m1.K = d; m1.W[0] = L.wg; m1.W[1] = L.wu;
       m1.S[0] = (const _Float16*)L.sg; m1.S[1] = (const _Float16*)L.su; m1.rows[0] = I; m1.rows[1] = I;
       m1.out = (_Float16*)s->pf_inter;
+      m1.part = s->pf_part; m1.part_bytes = kPrefillPartBytes;
       CQ_TRY(launch_pf_gemm(m1, st));
       PfGemmArgs m2;
       m2.mode = GM_RESID; m2.quant = c.quant_type; m2.A = (const _Float16*)s->pf_inter; m2.M = M; m2.N = d; m2.K = I;
       m2.W[0] = L.wd; m2.S[0] = (const _Float16*)L.sd; m2.rows[0] = d; m2.out = (_Float16*)s->pf_x;
+      m2.part = s->pf_part; m2.part_bytes = kPrefillPartBytes;
       CQ_TRY(launch_pf_gemm(m2, st));
     }
   }

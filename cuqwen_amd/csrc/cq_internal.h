@@ -86,6 +86,9 @@ struct PfGemmArgs {
   const double* inv_freq = nullptr;
   _Float16* kcache = nullptr;
   _Float16* vcache = nullptr;
+  // split-K workspace (fp32 partials); nullptr: no split
+  float* part = nullptr;
+  size_t part_bytes = 0;
 };
 struct PfAttnArgs {
   const _Float16* q = nullptr;   // [M][n_heads * hd] natural

@@ -26,6 +26,8 @@
 #include "cq_attention.h"
 #include "cq_gemv.h"
 
+#include <algorithm>
+
 namespace cq {
 
 constexpr int kPfThreads = 256;   // 4 waves
@@ -34,6 +36,8 @@ constexpr int kPfRowsPerWave = 32;
 constexpr int kPfBN = 4 * kPfRowsPerWave;   // weight rows per GEMM block
 constexpr int kPfK = 128;         // K per main-loop step (one quantization group)
 constexpr int kPfLdsStride = kPfK + 8;     // halves per token row in LDS (16-byte skew)
+constexpr int kPfTargetBlocks = 512;       // split K below this many blocks (2 per CU)
+constexpr int kPfMaxSplit = 8;
 
 // position of element k in the permuted activation layout
 __device__ __forceinline__ int pf_pos(int k) {
@@ -114,6 +118,26 @@ __device__ __forceinline__ int pf_mat(const PfGemmArgs& a, int row, int* local) 
   return 2;
 }
 
+// One rotated pair (rows local, local + hd/2 of matrix mat) of token m:
+// q into the Q buffer, k / v into the cache at position pos0 + m.
+__device__ __forceinline__ void pf_qkv_store(const PfGemmArgs& a, int mat, int local, int m, _Float16 h0, _Float16 h1) {
+  const int hd = a.head_dim, half = hd / 2;
+  if (mat == 0) {
+    a.out[(int64_t)m * a.rows[0] + local] = h0;
+    a.out[(int64_t)m * a.rows[0] + local + half] = h1;
+  } else {
+    const int kvh = local / hd, i = local % hd, pos = a.pos0 + m;
+    _Float16* c = mat == 1 ? a.kcache : a.vcache;
+    if (mat == 1) {
+      c[kv_k_offset(kvh, pos, i, a.max_seq, hd)] = h0;
+      c[kv_k_offset(kvh, pos, i + half, a.max_seq, hd)] = h1;
+    } else {
+      c[kv_v_offset(kvh, pos, i, a.max_seq, hd)] = h0;
+      c[kv_v_offset(kvh, pos, i + half, a.max_seq, hd)] = h1;
+    }
+  }
+}
+
 template <int Q>
 __device__ __forceinline__ void pf_load_w(const PfGemmArgs& a, const char* rowp, int ks, int j, u4_t* w) {
   constexpr int L = PfW<Q>::LOADS;
@@ -124,7 +148,7 @@ __device__ __forceinline__ void pf_load_w(const PfGemmArgs& a, const char* rowp,
 
 // C^T tile of a wave: NMAT matrices (SwiGLU: gate and up) x RT row slices of
 // 16 x 4 token slices of 16; lane holds rows 4*(lane/16)+v, token lane%16.
-template <int Q, int MODE>
+template <int Q, int MODE, bool SPLIT>
 __global__ __launch_bounds__(kPfThreads) void pf_gemm_kernel(const PfGemmArgs a) {
   constexpr int NMAT = MODE == GM_SWIGLU ? 2 : 1;
   constexpr int RT = MODE == GM_SWIGLU ? 1 : 2;   // SwiGLU: 16 gate + 16 up rows per wave
@@ -139,6 +163,9 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm_kernel(const PfGemmArgs a)
   const int nb0 = blockIdx.x * BN;             // first output row of the block
   const int nw0 = nb0 + wave * WROWS;          // first output row of the wave
   const int K = a.K, nks = K / kPfK;
+  // split-K: block z of gridDim.z sums K steps [kb, ke) into an fp32 partial
+  const int kb = SPLIT ? (int)((int64_t)blockIdx.z * nks / gridDim.z) : 0;
+  const int ke = SPLIT ? (int)((int64_t)(blockIdx.z + 1) * nks / gridDim.z) : nks;
 
   // weight row pointers of the lane (A operand row r of each slice)
   const char* rowp[NMAT][RT];
@@ -187,19 +214,19 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm_kernel(const PfGemmArgs a)
       for (int tt = 0; tt < 4; ++tt) acc[mt][rt][tt] = f4_t{0.f, 0.f, 0.f, 0.f};
 
   u4_t xv[4], wv[NMAT][RT][L];
-  x_load(0, xv);
+  x_load(kb, xv);
 #pragma unroll
   for (int mt = 0; mt < NMAT; ++mt)
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt) pf_load_w<Q>(a, rowp[mt][rt], 0, j, wv[mt][rt]);
+    for (int rt = 0; rt < RT; ++rt) pf_load_w<Q>(a, rowp[mt][rt], kb, j, wv[mt][rt]);
   x_store(0, xv);
   __syncthreads();
 
-  for (int ks = 0; ks < nks; ++ks) {
-    const int buf = ks & 1;
+  for (int ks = kb; ks < ke; ++ks) {
+    const int buf = (ks - kb) & 1;
     // next step's activations and weights in flight during this step's MMAs
     u4_t wn[NMAT][RT][L];
-    const int kn = min(ks + 1, nks - 1);
+    const int kn = min(ks + 1, ke - 1);
     x_load(kn, xv);
 #pragma unroll
     for (int mt = 0; mt < NMAT; ++mt)
@@ -258,8 +285,25 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm_kernel(const PfGemmArgs a)
       for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
         for (int i = 0; i < L; ++i) wv[mt][rt][i] = wn[mt][rt][i];
-    if (ks + 1 < nks) x_store(buf ^ 1, xv);
+    if (ks + 1 < ke) x_store(buf ^ 1, xv);
     __syncthreads();
+  }
+
+  if constexpr (SPLIT) {
+    // fp32 partial [z][mat][M][N]; the split epilogue sums and finishes
+#pragma unroll
+    for (int mt = 0; mt < NMAT; ++mt)
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int n = nw0 + rt * 16 + 4 * j + v, m = m0 + tt * 16 + r;
+            if (n < a.N && m < a.M)
+              a.part[(((int64_t)blockIdx.z * NMAT + mt) * a.M + m) * a.N + n] = acc[mt][rt][tt][v];
+          }
+    return;
   }
 
   // ---- epilogues: lane holds rows nw0 + rt*16 + 4j + v, token m0 + tt*16 + r
@@ -319,20 +363,46 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm_kernel(const PfGemmArgs a)
       float y0 = (float)ot[nl0 * kPfBM + ml], y1 = (float)ot[nl1 * kPfBM + ml];
       const int pos = a.pos0 + m, i = local % hd;
       if (mat < 2) rope_rotate(y0, y1, pos, a.inv_freq[i]);
-      const _Float16 h0 = (_Float16)y0, h1 = (_Float16)y1;
-      if (mat == 0) {
-        a.out[(int64_t)m * a.rows[0] + local] = h0;
-        a.out[(int64_t)m * a.rows[0] + local + half] = h1;
+      pf_qkv_store(a, mat, local, m, (_Float16)y0, (_Float16)y1);
+    }
+  }
+}
+
+// Split-K epilogue: sums the S partials of each output and applies the
+// mode's epilogue (the same arithmetic as the fused epilogues above).
+template <int MODE>
+__global__ __launch_bounds__(256) void pf_split_epilogue(const PfGemmArgs a, int S) {
+  const int64_t MN = (int64_t)a.M * a.N;
+  const int NMAT = MODE == GM_SWIGLU ? 2 : 1;
+  auto sum = [&](int mt, int m, int n) {
+    float v = 0.f;
+    for (int z = 0; z < S; ++z) v += a.part[((int64_t)z * NMAT + mt) * MN + (int64_t)m * a.N + n];
+    return v;
+  };
+  if constexpr (MODE == GM_QKV) {
+    const int hd = a.head_dim, half = hd / 2, np = a.N / 2;
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < (int64_t)a.M * np;
+         idx += (int64_t)gridDim.x * blockDim.x) {
+      const int m = (int)(idx / np), p = (int)(idx % np);
+      const int n0 = (p / half) * hd + p % half, n1 = n0 + half;
+      int local;
+      const int mat = pf_mat(a, n0, &local);
+      const _Float16* b = a.bias[mat];
+      float y0 = (float)(_Float16)(sum(0, m, n0) * a.inv[m] + (b ? (float)b[local] : 0.f));
+      float y1 = (float)(_Float16)(sum(0, m, n1) * a.inv[m] + (b ? (float)b[local + half] : 0.f));
+      if (mat < 2) rope_rotate(y0, y1, a.pos0 + m, a.inv_freq[local % hd]);
+      pf_qkv_store(a, mat, local, m, (_Float16)y0, (_Float16)y1);
+    }
+  } else {
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < MN; idx += (int64_t)gridDim.x * blockDim.x) {
+      const int m = (int)(idx / a.N), n = (int)(idx % a.N);
+      if constexpr (MODE == GM_RESID) {
+        _Float16* p = a.out + idx;
+        *p = (_Float16)((float)*p + sum(0, m, n));
       } else {
-        const int kvh = local / hd;
-        _Float16* c = mat == 1 ? a.kcache : a.vcache;
-        if (mat == 1) {
-          c[kv_k_offset(kvh, pos, i, a.max_seq, hd)] = h0;
-          c[kv_k_offset(kvh, pos, i + half, a.max_seq, hd)] = h1;
-        } else {
-          c[kv_v_offset(kvh, pos, i, a.max_seq, hd)] = h0;
-          c[kv_v_offset(kvh, pos, i + half, a.max_seq, hd)] = h1;
-        }
+        const float g = sum(0, m, n) * a.inv[m], u = sum(1, m, n) * a.inv[m];
+        const float sig = 1.f / (1.f + expf(-g));
+        a.out[(int64_t)m * a.N + pf_pos(n)] = (_Float16)((g * sig) * u);
       }
     }
   }
@@ -474,13 +544,36 @@ int launch_pf_embed(const __half* embed, const int* tokens, int M, int dim, __ha
   return CQ_OK;
 }
 
+template <int Q, int MODE>
+static int launch_pf_gemm_m(const PfGemmArgs& a, hipStream_t stream) {
+  const int bn = MODE == GM_SWIGLU ? 64 : kPfBN;
+  const int gx = (a.N + bn - 1) / bn, gy = (a.M + kPfBM - 1) / kPfBM;
+  const int nks = a.K / kPfK, nmat = MODE == GM_SWIGLU ? 2 : 1;
+  // split K until the grid holds ~2 blocks per CU (small M), within the workspace
+  int S = 1;
+  const int blocks = gx * gy;
+  if (blocks < kPfTargetBlocks && a.part) {
+    S = std::min({kPfMaxSplit, (kPfTargetBlocks + blocks - 1) / blocks, nks});
+    while (S > 1 && (size_t)S * nmat * a.M * a.N * sizeof(float) > a.part_bytes) --S;
+  }
+  if (S > 1) {
+    hipLaunchKernelGGL((pf_gemm_kernel<Q, MODE, true>), dim3(gx, gy, S), dim3(kPfThreads), 0, stream, a);
+    CQ_HIP(hipGetLastError());
+    const int64_t work = MODE == GM_QKV ? (int64_t)a.M * a.N / 2 : (int64_t)a.M * a.N;
+    const int eb = (int)std::min<int64_t>((work + 255) / 256, 4096);
+    hipLaunchKernelGGL((pf_split_epilogue<MODE>), dim3(eb), dim3(256), 0, stream, a, S);
+  } else {
+    hipLaunchKernelGGL((pf_gemm_kernel<Q, MODE, false>), dim3(gx, gy), dim3(kPfThreads), 0, stream, a);
+  }
+  CQ_HIP(hipGetLastError());
+  return CQ_OK;
+}
+
 template <int Q>
-static void launch_pf_gemm_q(const PfGemmArgs& a, hipStream_t stream) {
-  const int bn = a.mode == GM_SWIGLU ? 64 : kPfBN;
-  const dim3 grid((a.N + bn - 1) / bn, (a.M + kPfBM - 1) / kPfBM);
-  if (a.mode == GM_QKV) hipLaunchKernelGGL((pf_gemm_kernel<Q, GM_QKV>), grid, dim3(kPfThreads), 0, stream, a);
-  else if (a.mode == GM_SWIGLU) hipLaunchKernelGGL((pf_gemm_kernel<Q, GM_SWIGLU>), grid, dim3(kPfThreads), 0, stream, a);
-  else hipLaunchKernelGGL((pf_gemm_kernel<Q, GM_RESID>), grid, dim3(kPfThreads), 0, stream, a);
+static int launch_pf_gemm_q(const PfGemmArgs& a, hipStream_t stream) {
+  if (a.mode == GM_QKV) return launch_pf_gemm_m<Q, GM_QKV>(a, stream);
+  if (a.mode == GM_SWIGLU) return launch_pf_gemm_m<Q, GM_SWIGLU>(a, stream);
+  return launch_pf_gemm_m<Q, GM_RESID>(a, stream);
 }
 
 int launch_pf_gemm(const PfGemmArgs& a, hipStream_t stream) {
@@ -494,12 +587,10 @@ int launch_pf_gemm(const PfGemmArgs& a, hipStream_t stream) {
       return fail(CQ_EINVAL, "prefill gemm: qkv rows must be whole heads");
   }
   switch (a.quant) {
-    case CQ_QUANT_FP16: launch_pf_gemm_q<CQ_QUANT_FP16>(a, stream); break;
-    case CQ_QUANT_INT8: launch_pf_gemm_q<CQ_QUANT_INT8>(a, stream); break;
-    default: launch_pf_gemm_q<CQ_QUANT_INT4>(a, stream); break;
+    case CQ_QUANT_FP16: return launch_pf_gemm_q<CQ_QUANT_FP16>(a, stream);
+    case CQ_QUANT_INT8: return launch_pf_gemm_q<CQ_QUANT_INT8>(a, stream);
+    default: return launch_pf_gemm_q<CQ_QUANT_INT4>(a, stream);
   }
-  CQ_HIP(hipGetLastError());
-  return CQ_OK;
 }
 
 int launch_pf_attention(const PfAttnArgs& a, hipStream_t stream) {

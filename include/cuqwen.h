@@ -132,7 +132,7 @@ int cq_decode(cq_state* s, int32_t token, int32_t pos0, int32_t n_steps,
  * one qwen_forward per prompt token with no penalty history; this entry
  * point gives the same result with tokens[0..n_tokens-1) pushed through the
  * layers in batches (matrix-core GEMMs and a causal attention kernel, up to
- * 512 tokens per pass) and the last token run as a decode step.  Fills the
+ * 2048 tokens per pass) and the last token run as a decode step.  Fills the
  * KV cache for positions [pos0, pos0 + n_tokens); *token_out receives the
  * greedy id after the last prompt token and cq_state_logits its logits.
  * Errors: CQ_ERANGE for positions past max_seq_len or ids outside the

@@ -74,18 +74,18 @@ def test_prefill_tiny_matches_oracle(quant, segments):
 
 
 def test_prefill_crosses_chunks():
-    """A 600-token prompt is two passes of at most 512 tokens."""
-    cfg = tiny_config(2, max_seq_len=1024)
+    """A 2100-token prompt is two passes of at most 2048 tokens."""
+    cfg = tiny_config(2, max_seq_len=4096)
     w = cq.synth_weights(cfg, 5)
     om = orc.Model.synth(cfg, 5, cfg.max_seq_len)
     st = cq.State(cfg, w)
-    prompt = _prompt(cfg, 600, 9)
+    prompt = _prompt(cfg, 2100, 9)
     ot = _oracle_prompt(om, prompt, 0)
     gt = st.prefill(prompt, 0)
     assert _rel(st.logits(), om.logits()) <= TOL
     if _gap(om.logits()) > 1e-2:
         assert gt == ot
-    _check_kv(cfg, st, om.kv, 600)
+    _check_kv(cfg, st, om.kv, 2100)
     st.free()
     w.free()
 
@@ -103,11 +103,13 @@ def _gpu_reference(cfg, w, prompt, pos0, n_ctx):
 
 @pytest.mark.parametrize("model,quant,layers,n,n_ctx", [
     ("7B", "int4", 2, 130, 2000), ("0.5B", "int8", 24, 1024, 0), ("14B", "int4", 2, 64, 100),
-    ("7B", "fp16", 2, 80, 0), ("1.5B", "int4", 3, 200, 4000), ("7B", "int8", 2, 33, 32768 - 40)])
+    ("7B", "fp16", 2, 80, 0), ("1.5B", "int4", 3, 200, 4000), ("7B", "int8", 2, 33, 32768 - 40),
+    ("7B", "int4", 2, 2100, 10)])
 def test_prefill_matches_decode_real_shapes(model, quant, layers, n, n_ctx):
     """BASELINE model shapes: batched prefill equals the decode step run once
     per prompt token (logits within 1e-2, same top-1 where the top-2 gap
-    exceeds 1e-2, same KV cache within 1e-2)."""
+    exceeds 1e-2, same KV cache within 1e-2).  Short prompts take the split-K
+    GEMM path, the 2100-token one the single-pass epilogues."""
     cfg = cq.preset(model, quant).replace(n_layers=layers)
     w = cq.synth_weights(cfg, 0x5157454E)
     prompt = _prompt(cfg, n, 31)
