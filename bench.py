@@ -36,6 +36,8 @@ def parse():
     ap.add_argument("--no-profile", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--prompt", type=int, default=1024, help="prompt tokens of the batched-prefill measurement")
+    ap.add_argument("--configs", action="store_true",
+                    help="also measure decode (and prefill) at every BASELINE config (adds about a minute)")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a 256 MiB device-to-device copy (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -115,6 +117,61 @@ def prefill_leg(cq, cfg, st, n):
             "prefill_by_decode_ms": round(by_decode_ms, 2), "speedup": round(by_decode_ms / (best / 1e3), 2),
             "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": 2500.0, "unit": "TFLOP/s",
                          "frac": round(tflops / 2500.0, 4)}}
+
+
+def bytes_per_token(cfg, ctx):
+    """Algorithmic HBM bytes of one decode step at context ctx: every weight
+    and scale once, the K and V of ctx positions, activations ignored."""
+    d, I, L, V = cfg.dim, cfg.intermediate_size, cfg.n_layers, cfg.vocab_size
+    qd, kvd = cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim
+
+    def w(quant, rows, cols):
+        return rows * cols // 2 + 2 * rows * cols // 128 if quant == 2 else (
+            rows * cols + 2 * rows * cols // 128 if quant == 1 else 2 * rows * cols)
+    layer = (w(cfg.quant_type, qd + 2 * kvd, d) + w(cfg.quant_type, d, qd) + w(cfg.quant_type, 2 * I, d)
+             + w(cfg.quant_type, d, I) + 2 * (qd + 2 * kvd) + 4 * d)
+    lm = w(1, V, d) if cfg.lm_head_fmt == 1 else 2 * V * d
+    return L * layer + lm + 2 * d + ctx * L * 2 * kvd * 2
+
+
+def config_legs(cq):
+    """Decode tok/s and whole-step HBM efficiency at every BASELINE config
+    (synthetic seeded weights, KV prefilled with seeded N(0,1)), plus the
+    prompt phase of configs 2 and 3 through cq_prefill."""
+    legs = [("0.5B", "int8", [1152], 1024), ("1.5B", "int4", [4352], 4096),
+            ("7B", "fp16", [1024, 8192, 32768], 0), ("7B", "int8", [1024, 8192, 32768], 0),
+            ("7B", "int4", [1024, 8192, 32768], 0), ("14B", "int4", [32768], 0)]
+    out = []
+    for model, quant, ctxs, prompt in legs:
+        cfg = cq.preset(model, quant)
+        w = cq.synth_weights(cfg, 0x5157454E)
+        st = cq.State(cfg, w)
+        if prompt:
+            toks = [int(cq.lib.cq_synth_uniform(42, 0, i, cfg.vocab_size)) for i in range(prompt)]
+            st.prefill(toks, 0)
+            st.prefill(toks, 0)
+            pf_ms = st.last_prefill_us() / 1e3
+        for ctx in ctxs:
+            steps = 64
+            pos0 = ctx - steps
+            if not prompt:
+                st.fill_kv(pos0, 77)
+            tok = int(cq.lib.cq_synth_uniform(42, 0, 0, cfg.vocab_size))
+            st.decode(tok, pos0 - 16, 16)
+            st.decode(tok, pos0, steps)
+            us = st.last_decode_us()
+            b = bytes_per_token(cfg, ctx - 1)
+            leg = {"model": f"Qwen2.5-{model}", "quant": quant, "ctx": ctx, "tok_per_s": round(1e6 / us, 1),
+                   "ms_per_token": round(us / 1e3, 4), "bytes_per_token": b,
+                   "GBps": round(b / us / 1e3, 1), "hbm_frac": round(b / us / 1e3 / PEAK_GBPS, 4)}
+            if prompt:
+                leg.update({"prompt_tokens": prompt, "prefill_ms": round(pf_ms, 3),
+                            "prefill_tok_per_s": round(prompt / pf_ms * 1e3, 1)})
+            log(f"[bench] config {leg}")
+            out.append(leg)
+        st.free()
+        w.free()
+    return out
 
 
 def cpu_baseline(cfg, ctx, threads):
@@ -211,6 +268,8 @@ def main():
         src.free()
         dst.free()
 
+    legs = config_legs(cq) if args.configs else None
+
     cpu = None
     if not args.no_cpu_baseline:
         t2 = time.perf_counter()
@@ -228,6 +287,7 @@ def main():
                    "parallelism": "single-gpu"},
         "device_ms_per_step": round(dev_us / 1e3, 5),
         "roofline": roof, "cpu_baseline": cpu, "kernels": kernels, "gemv_config1": g1, "prefill": pf,
+        "configs": legs,
     }
     print(json.dumps(res), flush=True)
 

@@ -93,10 +93,6 @@ __global__ __launch_bounds__(kAttnThreads) void attention_stage1(const AttnArgs 
 constexpr int kMergeDims = 16;
 template <int HD>
 __global__ __launch_bounds__(kWave) void attention_stage2(const AttnArgs a, int Pmax) {
-  const int T = *a.d_pos + 1;
-  int tpp;
-  const int nparts = attn_nparts(T, Pmax, &tpp);
-  if (nparts == 1) return;   // stage 1 wrote the output
   constexpr int NS = HD / kMergeDims;
   const int hq = blockIdx.x / NS, d0 = (blockIdx.x % NS) * kMergeDims;
   const int g = a.n_heads / a.n_kv;
@@ -106,27 +102,39 @@ __global__ __launch_bounds__(kWave) void attention_stage2(const AttnArgs a, int 
   const float* ws_l = ws_m + (size_t)a.n_kv * Pmax * 16;
   const float* ws_o = ws_l + (size_t)a.n_kv * Pmax * 16;
   const size_t base = (size_t)kvh * Pmax;
+  // the first round's slots (partition = lane) are requested before the
+  // position is known: they do not depend on it, and slots past the
+  // partition count are masked below (selected out, so stale contents of
+  // unused slots never reach the sums)
+  auto load_round = [&](int p0, float& mp, float& lp, f4_t* ov) {
+    const size_t slot = (base + min(p0 + lane, Pmax - 1)) * 16 + hh;
+    mp = ws_m[slot];
+    lp = ws_l[slot];
+    const f4_t* op = reinterpret_cast<const f4_t*>(ws_o + slot * HD + d0);
+#pragma unroll
+    for (int i = 0; i < kMergeDims / 4; ++i) ov[i] = op[i];
+  };
+  float mp, lp;
+  f4_t ov[kMergeDims / 4];
+  load_round(0, mp, lp, ov);
+  const int T = *a.d_pos + 1;
+  int tpp;
+  const int nparts = attn_nparts(T, Pmax, &tpp);
+  if (nparts == 1) return;   // stage 1 wrote the output
   float M = -INFINITY, L = 0.f, O[kMergeDims];
 #pragma unroll
   for (int i = 0; i < kMergeDims; ++i) O[i] = 0.f;
   for (int p0 = 0; p0 < nparts; p0 += kWave) {
-    const int p = p0 + lane;
-    const int pc = min(p, nparts - 1);   // clamped: every lane loads, invalid lanes get weight 0
-    const size_t slot = (base + pc) * 16 + hh;
-    const float mp = ws_m[slot], lp = ws_l[slot];
-    f4_t ov[kMergeDims / 4];
-    const f4_t* op = reinterpret_cast<const f4_t*>(ws_o + slot * HD + d0);
-#pragma unroll
-    for (int i = 0; i < kMergeDims / 4; ++i) ov[i] = op[i];
-    const float mv = p < nparts ? mp : -INFINITY;
-    const float Mn = fmaxf(M, wave_max(mv));
+    if (p0 > 0) load_round(p0, mp, lp, ov);
+    const bool valid = p0 + lane < nparts && mp != -INFINITY;
+    const float Mn = fmaxf(M, wave_max(valid ? mp : -INFINITY));
     const float f = M == -INFINITY ? 0.f : __expf(M - Mn);
-    const float w = (p < nparts && mp != -INFINITY) ? __expf(mp - Mn) : 0.f;
-    L = L * f + wave_sum(lp * w);
+    const float w = valid ? __expf(mp - Mn) : 0.f;
+    L = L * f + wave_sum(valid ? lp * w : 0.f);
 #pragma unroll
     for (int i = 0; i < kMergeDims / 4; ++i)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) O[4 * i + e] = O[4 * i + e] * f + wave_sum(ov[i][e] * w);
+      for (int e = 0; e < 4; ++e) O[4 * i + e] = O[4 * i + e] * f + wave_sum(valid ? ov[i][e] * w : 0.f);
     M = Mn;
   }
   const float inv = 1.0f / (L + 1e-9f);
