@@ -35,6 +35,7 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-profile", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-kv8", action="store_true", help="skip the int8 KV cache leg")
     ap.add_argument("--prompt", type=int, default=1024, help="prompt tokens of the batched-prefill measurement")
     ap.add_argument("--configs", action="store_true",
                     help="also measure decode (and prefill) at every BASELINE config (adds about a minute)")
@@ -117,6 +118,28 @@ def prefill_leg(cq, cfg, st, n):
             "prefill_by_decode_ms": round(by_decode_ms, 2), "speedup": round(by_decode_ms / (best / 1e3), 2),
             "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": 2500.0, "unit": "TFLOP/s",
                          "frac": round(tflops / 2500.0, 4)}}
+
+
+def kv8_leg(cq, cfg, w, pos0, args):
+    """The same decode workload with the int8 KV cache (CQ_KV_INT8): tok/s
+    and whole-step bytes (the K/V stream halves)."""
+    st = cq.State(cfg, w, kv_dtype=cq.KV_INT8)
+    st.fill_kv(pos0, 77)
+    tok = int(cq.lib.cq_synth_uniform(42, 0, 0, cfg.vocab_size))
+    warm = st.decode(tok, pos0, args.warmup)
+    cq.synchronize()
+    t0 = time.perf_counter()
+    st.decode(int(warm[-1]), pos0 + args.warmup, args.steps)
+    cq.synchronize()
+    wall = time.perf_counter() - t0
+    us = st.last_decode_us()
+    st.free()
+    kvd = cfg.n_kv_heads * cfg.head_dim
+    # fp16 K/V bytes halve; each position adds two fp32 scales per kv head
+    b = (bytes_per_token(cfg, args.ctx - 1) - (args.ctx - 1) * cfg.n_layers * 2 * kvd
+         + (args.ctx - 1) * cfg.n_layers * 2 * cfg.n_kv_heads * 4)
+    return {"tok_per_s": round(args.steps / wall, 3), "device_ms_per_step": round(us / 1e3, 5),
+            "bytes_per_token": b, "hbm_frac": round(b / us / 1e3 / PEAK_GBPS, 4)}
 
 
 def bytes_per_token(cfg, ctx):
@@ -257,6 +280,10 @@ def main():
         pf = prefill_leg(cq, cfg, st, args.prompt)
         log(f"[bench] prefill: {pf}")
     st.free()
+    kv8 = None
+    if not args.no_kv8:
+        kv8 = kv8_leg(cq, cfg, w, pos0, args)
+        log(f"[bench] int8 KV cache: {kv8}")
     w.free()
     if args.calib_copy:
         n = 256 << 20
@@ -286,7 +313,7 @@ def main():
                    "model": f"Qwen2.5-{args.model}", "global_batch": 1, "seq_len": args.ctx,
                    "parallelism": "single-gpu"},
         "device_ms_per_step": round(dev_us / 1e3, 5),
-        "roofline": roof, "cpu_baseline": cpu, "kernels": kernels, "gemv_config1": g1, "prefill": pf,
+        "roofline": roof, "cpu_baseline": cpu, "kernels": kernels, "gemv_config1": g1, "prefill": pf, "kv_int8": kv8,
         "configs": legs,
     }
     print(json.dumps(res), flush=True)

@@ -87,6 +87,7 @@ def _load():
         "cq_free_weights": (I32, [P]),
         "cq_weights_tensor": (I32, [P, ctypes.c_char_p, I32, ctypes.POINTER(P), ctypes.POINTER(SZ)]),
         "cq_state_create": (I32, [CP, P, ctypes.POINTER(P)]),
+        "cq_state_create_kv": (I32, [CP, P, I32, ctypes.POINTER(P)]),
         "cq_state_destroy": (I32, [P]),
         "cq_forward": (I32, [P, I32, I32, IP, I32, IP]),
         "cq_decode": (I32, [P, I32, I32, I32, IP, I32, IP]),
@@ -128,6 +129,7 @@ def _load():
         "cq_rope": (I32, [P, P, I32, I32, I32, P, ctypes.c_float, P]),
         "cq_gqa_attention_decode": (I32, [P, P, P, P, P, I32, I32, I32, I32, P, P]),
         "cq_attention_workspace_bytes": (SZ, [I32, I32, I32]),
+        "cq_gqa_attention_decode_kv8": (I32, [P, P, P, P, P, P, P, P, P, I32, I32, I32, I32, P, P]),
         "cq_dequantize": (I32, [I32, I32, P, P, P, I32, I32, P]),
         "cq_time_gemv": (I32, [I32, I32, I32, ctypes.POINTER(P), ctypes.POINTER(P), P, P, I32, I32, I32,
                                ctypes.POINTER(ctypes.c_double)]),
@@ -146,7 +148,7 @@ EXPORTED = [
     "cq_last_error", "cq_config_preset", "cq_read_header", "cq_write_synthetic_file", "cq_load_weights",
     "cq_synth_weights", "cq_free_weights", "cq_weights_tensor", "cq_state_create", "cq_state_destroy",
     "cq_forward", "cq_decode", "cq_state_logits", "cq_state_fill_kv", "cq_state_kv_read", "cq_state_kv_write",
-    "cq_prefill", "cq_state_last_prefill_us",
+    "cq_prefill", "cq_state_last_prefill_us", "cq_state_create_kv", "cq_gqa_attention_decode_kv8",
     "cq_state_last_decode_us", "cq_synth_normal", "cq_synth_uniform", "cq_tensor_stream_id", "cq_kv_stream_id",
     "cq_quantize", "cq_device_count", "cq_malloc", "cq_free", "cq_memcpy_h2d", "cq_memcpy_d2h", "cq_memset", "cq_memcpy_d2d",
     "cq_synchronize", "cq_embedding_lookup", "cq_rmsnorm", "cq_gemv", "cq_gemv_add", "cq_fused_attn_block",
@@ -161,6 +163,9 @@ def check(rc):
     if rc != 0:
         raise CuQwenError(rc, lib.cq_last_error().decode(errors="replace"))
     return rc
+
+
+KV_FP16, KV_INT8 = 0, 1
 
 
 def preset(model, quant="int8"):
@@ -305,11 +310,13 @@ def free_weights(weights, cfg=None):
 class State:
     """Decode state (QwenState, include/model.cuh:9-46)."""
 
-    def __init__(self, cfg, weights):
+    def __init__(self, cfg, weights, kv_dtype=0):
+        """kv_dtype: KV_FP16 (the reference's cache) or KV_INT8."""
         self.cfg = cfg
         self.weights = weights
+        self.kv_dtype = kv_dtype
         self.handle = ctypes.c_void_p()
-        check(lib.cq_state_create(ctypes.byref(cfg), weights.handle, ctypes.byref(self.handle)))
+        check(lib.cq_state_create_kv(ctypes.byref(cfg), weights.handle, int(kv_dtype), ctypes.byref(self.handle)))
 
     def forward(self, token, pos, history=None):
         hist = np.ascontiguousarray(history if history is not None else [], dtype=np.int32)

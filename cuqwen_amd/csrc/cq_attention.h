@@ -169,4 +169,152 @@ __device__ __forceinline__ void block_merge_write(const AttnArgs& a, int kvh, in
   }
 }
 
+// ------------------------------------------------------------ int8 KV cache
+// Same element layout as the fp16 cache (kv_k_offset / kv_v_offset count
+// bytes instead of halves), so a lane's 8 elements of a matrix-core operand
+// are 8 contiguous bytes; per-(position, kv head) fp32 scales live in
+// separate [kv_head][max_seq] arrays.  The K scale multiplies the finished
+// score, the V scale multiplies P before the PV product.
+typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
+
+template <int HD>
+struct KVTile8 {
+  u2_t ka[2][HD / 32];
+  u2_t va[HD / 16];
+  f4_t ks[2], vs[2];   // scales of the lane's keys ti*32 + st*16 + 4j + i
+};
+
+__device__ __forceinline__ u2_t load_u2_stream(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u2_t*>(p));
+}
+
+template <int HD>
+__device__ __forceinline__ void load_tile8(KVTile8<HD>& t, const int8_t* kbase, const int8_t* vbase, const float* ksc,
+                                           const float* vsc, int ti, int lane) {
+  const int8_t* kt = kbase + (int64_t)ti * kTileKeys * HD;
+  const int8_t* vt = vbase + (int64_t)ti * kTileKeys * HD;
+#pragma unroll
+  for (int st = 0; st < 2; ++st)
+#pragma unroll
+    for (int kk = 0; kk < HD / 32; ++kk) t.ka[st][kk] = load_u2_stream(kt + st * 16 * HD + (kk * 64 + lane) * 8);
+#pragma unroll
+  for (int dt = 0; dt < HD / 16; ++dt) t.va[dt] = load_u2_stream(vt + (dt * 64 + lane) * 8);
+  const int j = lane >> 4;
+#pragma unroll
+  for (int st = 0; st < 2; ++st) {
+    t.ks[st] = *reinterpret_cast<const f4_t*>(ksc + ti * kTileKeys + st * 16 + 4 * j);
+    t.vs[st] = *reinterpret_cast<const f4_t*>(vsc + ti * kTileKeys + st * 16 + 4 * j);
+  }
+}
+
+// 8 int8 (natural order) -> 8 exact fp16: (byte ^ 0x80) under the exponent
+// pattern 0x64 is 1024 + q + 128; minus 1152 leaves q.
+__device__ __forceinline__ h8_t i8x8_to_h8(u2_t w, uint32_t magic_v) {
+  const uint32_t f0 = w.x ^ kInt8Flip, f1 = w.y ^ kInt8Flip;
+  const h2_t bias = {(_Float16)-kInt8Bias, (_Float16)-kInt8Bias};
+  u4_t o;
+  o.x = as_u32(as_h2(int8_pair(f0, magic_v, 0)) + bias);
+  o.y = as_u32(as_h2(int8_pair(f0, magic_v, 1)) + bias);
+  o.z = as_u32(as_h2(int8_pair(f1, magic_v, 0)) + bias);
+  o.w = as_u32(as_h2(int8_pair(f1, magic_v, 1)) + bias);
+  return __builtin_bit_cast(h8_t, o);
+}
+
+// One 32-key tile of the online softmax over the int8 cache.  Keys at or past
+// t_lane (this lane's column limit) are masked; P of masked keys is exactly 0
+// (int8 data is always finite, stale scales are selected out).  Rounding as
+// the fp16 path: score = half(s * k_scale * 1/sqrt(hd)), P = half(p *
+// v_scale) for the product, the row sum over the unrounded p.
+template <int HD>
+__device__ __forceinline__ void attend_tile8(KVTile8<HD>& t, const h8_t* qb, int ti, int t_lane, float scale, int j,
+                                             float& m, float& l, f4_t* o, uint32_t magic_v) {
+  constexpr int KK = HD / 32, DT = HD / 16;
+  f4_t s[2];
+#pragma unroll
+  for (int st = 0; st < 2; ++st) {
+    s[st] = f4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk)
+      s[st] = __builtin_amdgcn_mfma_f32_16x16x32_f16(i8x8_to_h8(t.ka[st][kk], magic_v), qb[kk], s[st], 0, 0, 0);
+  }
+  const int key0 = ti * kTileKeys + 4 * j;
+  float sv[8];
+  float mt = -INFINITY;
+#pragma unroll
+  for (int st = 0; st < 2; ++st)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float v = (float)(_Float16)(s[st][i] * t.ks[st][i] * scale);
+      if (key0 + st * 16 + i >= t_lane) v = -INFINITY;
+      sv[st * 4 + i] = v;
+      mt = fmaxf(mt, v);
+    }
+  mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
+  mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
+  const float mn = fmaxf(m, mt);
+  const float alpha = m == -INFINITY ? 0.f : __expf(m - mn);
+  m = mn;
+  l *= alpha;
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
+  h8_t pb;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float p = sv[e] == -INFINITY ? 0.f : __expf(sv[e] - mn);
+    l += p;
+    pb[e] = sv[e] == -INFINITY ? (_Float16)0.f : (_Float16)(p * t.vs[e >> 2][e & 3]);
+  }
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+    o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(i8x8_to_h8(t.va[dt], magic_v), pb, o[dt], 0, 0, 0);
+}
+
+// Per-row int8 quantization (s = max|x| / 127, q = rint(x / s) clamped to
+// +-127, a zero row keeps s = 0) of the HD-element row x held by one wave
+// (HD / 64 consecutive elements per lane); returns s, writes q[0..HD/64).
+template <int HD>
+__device__ __forceinline__ float quant_row8_wave(const float* x, int8_t* q) {
+  constexpr int E = HD / kWave;
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < E; ++i) amax = fmaxf(amax, fabsf(x[i]));
+  amax = wave_max(amax);
+  const float s = amax / 127.0f;
+#pragma unroll
+  for (int i = 0; i < E; ++i) q[i] = s == 0.f ? (int8_t)0 : (int8_t)fminf(127.f, fmaxf(-127.f, rintf(x[i] / s)));
+  return s;
+}
+
+// Replaces key kp (0..31) of a loaded tile by the new row (kq / vq: HD int8
+// each in LDS, scales ksn / vsn).
+template <int HD>
+__device__ __forceinline__ void patch_key8(KVTile8<HD>& t, int kp, const int8_t* kq, const int8_t* vq, float ksn,
+                                           float vsn, int lane) {
+  // register indices stay compile-time (unrolled, selected by compares), so
+  // the tile never leaves the register file
+  const int kst = kp >> 4, r = kp & 15, j = lane >> 4;
+  const bool krow = (lane & 15) == r, vslot = j == (r >> 2);
+#pragma unroll
+  for (int st = 0; st < 2; ++st) {
+    if (st != kst) continue;
+    if (krow) {
+#pragma unroll
+      for (int kk = 0; kk < HD / 32; ++kk) t.ka[st][kk] = *reinterpret_cast<const u2_t*>(kq + kk * 32 + j * 8);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (!vslot || i != (r & 3)) continue;
+      t.ks[st][i] = ksn;
+      t.vs[st][i] = vsn;
+#pragma unroll
+      for (int dt = 0; dt < HD / 16; ++dt) {
+        const uint32_t b = (uint8_t)vq[dt * 16 + (lane & 15)];
+        const int e = st * 4 + i, sh = (e & 3) * 8;
+        if (e < 4) t.va[dt].x = (t.va[dt].x & ~(0xFFu << sh)) | (b << sh);
+        else t.va[dt].y = (t.va[dt].y & ~(0xFFu << sh)) | (b << sh);
+      }
+    }
+  }
+}
+
 }  // namespace cq

@@ -84,6 +84,92 @@ __global__ __launch_bounds__(kAttnThreads) void attention_stage1(const AttnArgs 
   block_merge_write<HD>(a, kvh, part, nparts, g, m, l, o);
 }
 
+// Stage 1 over the int8 cache.  The wave whose tiles include the step's new
+// position first quantizes the new k / v rows of its kv head (one row per
+// wave reduction), writes them and their scales into the cache for later
+// steps, and patches them into its loaded tile: no other wave of the launch
+// reads that position, so no block synchronisation is needed.
+template <int HD>
+__global__ __launch_bounds__(kAttnThreads) void attention_stage1_kv8(const AttnArgs a) {
+  constexpr int KK = HD / 32, DT = HD / 16, E = HD / kWave;
+  const int kvh = blockIdx.y, part = blockIdx.x;
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int g = a.n_heads / a.n_kv;
+  const int pos = *a.d_pos, T = pos + 1;
+  const int n_tiles = (T + kTileKeys - 1) / kTileKeys;
+  int tpp;
+  const int nparts = attn_nparts(T, gridDim.x, &tpp);
+  if (part >= nparts) return;
+  const int tile0 = part * tpp, tile1 = min(tile0 + tpp, n_tiles);
+  const int h = lane & 15, j = lane >> 4;
+  const float scale = 1.0f / sqrtf((float)HD);
+  const uint32_t magic = vgpr_const(0x64646464u);
+  const int8_t* kbase = a.kcache8 + (int64_t)kvh * a.max_seq * HD;
+  const int8_t* vbase = a.vcache8 + (int64_t)kvh * a.max_seq * HD;
+  const float* ksc = a.kscale + (int64_t)kvh * a.max_seq;
+  const float* vsc = a.vscale + (int64_t)kvh * a.max_seq;
+
+  // the new row (position pos) belongs to tile n_tiles - 1 of the last partition
+  __shared__ __align__(16) int8_t newq[2][HD];
+  __shared__ float news[2];
+  const int last = n_tiles - 1;
+  const bool owns_new = part == nparts - 1 && ((last - tile0) % kAttnWaves) == wave;
+  if (owns_new) {
+#pragma unroll
+    for (int kind = 0; kind < 2; ++kind) {
+      const _Float16* src = reinterpret_cast<const _Float16*>(kind ? a.v_new : a.k_new) + (int64_t)kvh * HD + lane * E;
+      float x[E];
+      int8_t qv[E];
+#pragma unroll
+      for (int i = 0; i < E; ++i) x[i] = (float)src[i];
+      const float sc = quant_row8_wave<HD>(x, qv);
+      int8_t* cache = kind ? a.vcache8 : a.kcache8;
+#pragma unroll
+      for (int i = 0; i < E; ++i) {
+        const int d = lane * E + i;
+        newq[kind][d] = qv[i];
+        cache[kind ? kv_v_offset(kvh, pos, d, a.max_seq, HD) : kv_k_offset(kvh, pos, d, a.max_seq, HD)] = qv[i];
+      }
+      if (lane == 0) {
+        news[kind] = sc;
+        (kind ? a.vscale : a.kscale)[(int64_t)kvh * a.max_seq + pos] = sc;
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+
+  KVTile8<HD> A, B;
+  int ti = tile0 + wave;
+  if (ti < tile1) load_tile8<HD>(A, kbase, vbase, ksc, vsc, ti, lane);
+  h8_t qb[KK];
+  {
+    const _Float16* q = reinterpret_cast<const _Float16*>(a.q) + (int64_t)(kvh * g + h) * HD;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      if (h < g) qb[kk] = __builtin_bit_cast(h8_t, load_u4(q + kk * 32 + j * 8));
+      else qb[kk] = h8_t{0, 0, 0, 0, 0, 0, 0, 0};
+    }
+  }
+  float m = -INFINITY, l = 0.f;
+  f4_t o[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) o[dt] = f4_t{0.f, 0.f, 0.f, 0.f};
+  const int kp = pos & (kTileKeys - 1);
+  for (; ti < tile1; ti += 2 * kAttnWaves) {
+    const int t1 = ti + kAttnWaves;
+    if (t1 < tile1) load_tile8<HD>(B, kbase, vbase, ksc, vsc, t1, lane);
+    if (owns_new && ti == last) patch_key8<HD>(A, kp, newq[0], newq[1], news[0], news[1], lane);
+    attend_tile8<HD>(A, qb, ti, T, scale, j, m, l, o, magic);
+    if (t1 >= tile1) break;
+    if (t1 + kAttnWaves < tile1) load_tile8<HD>(A, kbase, vbase, ksc, vsc, t1 + kAttnWaves, lane);
+    if (owns_new && t1 == last) patch_key8<HD>(B, kp, newq[0], newq[1], news[0], news[1], lane);
+    attend_tile8<HD>(B, qb, t1, T, scale, j, m, l, o, magic);
+  }
+  l += __shfl_xor(l, 16, kWave);
+  l += __shfl_xor(l, 32, kWave);
+  block_merge_write<HD>(a, kvh, part, nparts, g, m, l, o);
+}
+
 // Stage 2: log-sum-exp merge of the partitions (kernels.cu:222-288) with
 // 1/(L + 1e-9).  One wave per (query head, 16-dim slice), so the few MB of
 // partials are spread over n_heads * hd/16 CUs instead of n_heads; lane p
@@ -149,12 +235,19 @@ int launch_attention(const AttnArgs& a, hipStream_t stream) {
   if (a.n_kv <= 0 || a.n_heads % a.n_kv || a.n_heads / a.n_kv > 16 || a.n_kv > 64)
     return fail(CQ_EINVAL, "attention: need n_heads/n_kv_heads <= 16 and n_kv_heads <= 64");
   if (a.max_seq <= 0 || a.max_seq % kTileKeys) return fail(CQ_EINVAL, "attention: max_seq_len must be a multiple of 32");
-  if (!a.q || !a.kcache || !a.vcache || !a.out || !a.d_pos || !a.workspace)
-    return fail(CQ_EINVAL, "attention: null pointer");
+  const bool kv8 = a.kcache8 != nullptr;
+  if (!a.q || !a.out || !a.d_pos || !a.workspace) return fail(CQ_EINVAL, "attention: null pointer");
+  if (kv8 ? (!a.vcache8 || !a.kscale || !a.vscale || !a.k_new || !a.v_new) : (!a.kcache || !a.vcache))
+    return fail(CQ_EINVAL, "attention: null cache pointer");
   const int P = attention_max_parts(a.n_kv);
   const dim3 grid(P, a.n_kv);
-  if (a.head_dim == 128) hipLaunchKernelGGL(attention_stage1<128>, grid, dim3(kAttnThreads), 0, stream, a);
-  else hipLaunchKernelGGL(attention_stage1<64>, grid, dim3(kAttnThreads), 0, stream, a);
+  if (kv8) {
+    if (a.head_dim == 128) hipLaunchKernelGGL(attention_stage1_kv8<128>, grid, dim3(kAttnThreads), 0, stream, a);
+    else hipLaunchKernelGGL(attention_stage1_kv8<64>, grid, dim3(kAttnThreads), 0, stream, a);
+  } else {
+    if (a.head_dim == 128) hipLaunchKernelGGL(attention_stage1<128>, grid, dim3(kAttnThreads), 0, stream, a);
+    else hipLaunchKernelGGL(attention_stage1<64>, grid, dim3(kAttnThreads), 0, stream, a);
+  }
   if (a.head_dim == 128)
     hipLaunchKernelGGL(attention_stage2<128>, dim3(a.n_heads * (128 / kMergeDims)), dim3(kWave), 0, stream, a, P);
   else

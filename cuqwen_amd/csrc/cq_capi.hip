@@ -168,6 +168,20 @@ extern "C" int cq_gqa_attention_decode(const void* q, const void* kc, const void
   return launch_attention(a, as_stream(stream));
 }
 
+extern "C" int cq_gqa_attention_decode_kv8(const void* q, const void* k_new, const void* v_new, void* k_cache8,
+                                           void* v_cache8, float* k_scale, float* v_scale, void* out,
+                                           const int32_t* d_pos, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
+                                           int32_t max_seq_len, void* workspace, void* stream) {
+  AttnArgs a;
+  a.q = (const __half*)q; a.out = (__half*)out;
+  a.kcache8 = (int8_t*)k_cache8; a.vcache8 = (int8_t*)v_cache8; a.kscale = k_scale; a.vscale = v_scale;
+  a.k_new = (const __half*)k_new; a.v_new = (const __half*)v_new;
+  a.d_pos = d_pos; a.n_heads = n_heads; a.n_kv = n_kv_heads; a.head_dim = head_dim; a.max_seq = max_seq_len;
+  a.workspace = workspace;
+  if (!k_cache8) return fail(CQ_EINVAL, "attention: null cache pointer");
+  return launch_attention(a, as_stream(stream));
+}
+
 extern "C" int cq_dequantize(int32_t quant_type, int32_t group_size, const void* W, const void* scale, float* out,
                              int32_t rows, int32_t cols, void* stream) {
   return launch_dequant(quant_type, group_size, W, (const __half*)scale, out, rows, cols, as_stream(stream));

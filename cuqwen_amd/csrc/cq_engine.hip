@@ -8,6 +8,7 @@
 #include "cq_internal.h"
 
 #include <algorithm>
+#include <cmath>
 #include <cstdio>
 #include <cstring>
 #include <memory>
@@ -155,7 +156,9 @@ struct cq_state {
   char* arena = nullptr;
   __half *x = nullptr, *xb = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *inter = nullptr, *logits = nullptr;
   __half *kcache = nullptr, *vcache = nullptr;
-  size_t layer_kv_halves = 0;
+  size_t layer_kv_halves = 0;       // K (or V) elements of one layer: n_kv * max_seq * head_dim
+  int kv_dtype = CQ_KV_FP16;        // CQ_KV_INT8: kcache / vcache hold int8, scales below
+  float *kscale = nullptr, *vscale = nullptr;   // [layer][kv_head][max_seq] (int8 cache)
   void* attn_ws = nullptr;
   unsigned long long* argmax_ws = nullptr;
   StepCtl* ctl = nullptr;
@@ -185,8 +188,9 @@ int layer_gemvs(const cq_state* s, int l, GemvArgs* qkv, GemvArgs* o, GemvArgs* 
   const cq_config& c = s->cfg;
   const LayerW& L = s->w->layers[l];
   const int qd = c.n_heads * c.head_dim;
-  __half* kc = s->kcache + (size_t)l * s->layer_kv_halves;
-  __half* vc = s->vcache + (size_t)l * s->layer_kv_halves;
+  const bool kv8 = s->kv_dtype == CQ_KV_INT8;
+  __half* kc = kv8 ? nullptr : s->kcache + (size_t)l * s->layer_kv_halves;
+  __half* vc = kv8 ? nullptr : s->vcache + (size_t)l * s->layer_kv_halves;
   if (qkv) {
     GemvArgs a;
     a.mode = GM_QKV; a.quant = c.quant_type; a.x = s->x; a.norm_w = L.in_norm; a.eps = c.norm_eps;
@@ -194,6 +198,7 @@ int layer_gemvs(const cq_state* s, int l, GemvArgs* qkv, GemvArgs* o, GemvArgs* 
     a.W[0] = L.wq; a.W[1] = L.wk; a.W[2] = L.wv; a.S[0] = L.sq; a.S[1] = L.sk; a.S[2] = L.sv;
     a.bias[0] = L.bq; a.bias[1] = L.bk; a.bias[2] = L.bv;
     a.out[0] = s->q;
+    if (kv8) { a.out[1] = s->k; a.out[2] = s->v; }   // quantized into the cache by the attention kernel
     a.n_heads = c.n_heads; a.n_kv = c.n_kv_heads; a.head_dim = c.head_dim; a.d_pos = &s->ctl->pos;
     a.rope_theta = c.rope_theta; a.rope_inv_freq = s->rope_inv_freq;
     a.kcache = kc; a.vcache = vc; a.max_seq = c.max_seq_len;
@@ -225,8 +230,18 @@ AttnArgs layer_attn(const cq_state* s, int l) {
   const cq_config& c = s->cfg;
   AttnArgs a;
   a.q = s->q;
-  a.kcache = s->kcache + (size_t)l * s->layer_kv_halves;
-  a.vcache = s->vcache + (size_t)l * s->layer_kv_halves;
+  if (s->kv_dtype == CQ_KV_INT8) {
+    const size_t ls = (size_t)l * c.n_kv_heads * c.max_seq_len;
+    a.kcache8 = reinterpret_cast<int8_t*>(s->kcache) + (size_t)l * s->layer_kv_halves;
+    a.vcache8 = reinterpret_cast<int8_t*>(s->vcache) + (size_t)l * s->layer_kv_halves;
+    a.kscale = s->kscale + ls;
+    a.vscale = s->vscale + ls;
+    a.k_new = s->k;
+    a.v_new = s->v;
+  } else {
+    a.kcache = s->kcache + (size_t)l * s->layer_kv_halves;
+    a.vcache = s->vcache + (size_t)l * s->layer_kv_halves;
+  }
   a.out = s->xb;
   a.d_pos = &s->ctl->pos;
   a.n_heads = c.n_heads; a.n_kv = c.n_kv_heads; a.head_dim = c.head_dim; a.max_seq = c.max_seq_len;
@@ -319,6 +334,43 @@ __global__ void fill_kv_kernel(__half* kc, __half* vc, int n_layers, int n_kv, i
     kc[lo + kv_k_offset(h, t, d, max_seq, hd)] = __ushort_as_half(synth_half(seed, kv_stream(l, h, 0), e, mul, 0.f));
     vc[lo + kv_v_offset(h, t, d, max_seq, hd)] = __ushort_as_half(synth_half(seed, kv_stream(l, h, 1), e, mul, 0.f));
   }
+}
+
+// int8 cache: one thread per (layer, kv head, position) row of K or V: the
+// generator's fp16 values, quantized with s = max|x| / 127, q = rint(x / s).
+__global__ void fill_kv8_kernel(int8_t* kc, int8_t* vc, float* ks, float* vs, int n_layers, int n_kv, int n_pos,
+                                int max_seq, int hd, uint64_t seed, float mul) {
+  const int64_t rows = (int64_t)n_layers * n_kv * n_pos * 2;
+  for (int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r < rows; r += (int64_t)gridDim.x * blockDim.x) {
+    const int kind = (int)(r & 1);
+    const int64_t rr = r >> 1;
+    const int t = (int)(rr % n_pos);
+    const int lh = (int)(rr / n_pos);
+    const int l = lh / n_kv, h = lh % n_kv;
+    const uint64_t st = kv_stream(l, h, kind);
+    float amax = 0.f;
+    for (int d = 0; d < hd; ++d)
+      amax = fmaxf(amax, fabsf(h2f_bits(synth_half(seed, st, (uint64_t)t * hd + d, mul, 0.f))));
+    const float sc = amax / 127.0f;
+    const size_t lo = (size_t)l * n_kv * max_seq * hd;
+    int8_t* c = kind ? vc : kc;
+    for (int d = 0; d < hd; ++d) {
+      const float x = h2f_bits(synth_half(seed, st, (uint64_t)t * hd + d, mul, 0.f));
+      const int8_t q = sc == 0.f ? (int8_t)0 : (int8_t)fminf(127.f, fmaxf(-127.f, rintf(x / sc)));
+      c[lo + (kind ? kv_v_offset(h, t, d, max_seq, hd) : kv_k_offset(h, t, d, max_seq, hd))] = q;
+    }
+    (kind ? vs : ks)[((size_t)l * n_kv + h) * max_seq + t] = sc;
+  }
+}
+
+// The same quantization on the host (cq_state_kv_write of an int8 cache).
+void quant_row8_host(const uint16_t* x, int n, int8_t* q, float* s) {
+  float amax = 0.f;
+  for (int i = 0; i < n; ++i) amax = std::max(amax, std::fabs(h2f_bits(x[i])));
+  const float sc = amax / 127.0f;
+  *s = sc;
+  for (int i = 0; i < n; ++i)
+    q[i] = sc == 0.f ? (int8_t)0 : (int8_t)std::max(-127.f, std::min(127.f, std::nearbyint(h2f_bits(x[i]) / sc)));
 }
 
 }  // namespace
@@ -435,7 +487,12 @@ extern "C" int cq_weights_tensor(const cq_weights* w, const char* name, int32_t 
 }
 
 extern "C" int cq_state_create(const cq_config* cfg, const cq_weights* w, cq_state** out) {
+  return cq_state_create_kv(cfg, w, CQ_KV_FP16, out);
+}
+
+extern "C" int cq_state_create_kv(const cq_config* cfg, const cq_weights* w, int32_t kv_dtype, cq_state** out) {
   if (!cfg || !w || !out) return fail(CQ_EINVAL, "state_create: null argument");
+  if (kv_dtype != CQ_KV_FP16 && kv_dtype != CQ_KV_INT8) return fail(CQ_EINVAL, "state_create: unknown KV cache type");
   CQ_TRY(validate_config(*cfg));
   if (std::memcmp(cfg, &w->cfg, offsetof(cq_config, norm_eps)) != 0)
     return fail(CQ_EINVAL, "state_create: config does not match the weights");
@@ -444,8 +501,10 @@ extern "C" int cq_state_create(const cq_config* cfg, const cq_weights* w, cq_sta
   s->w = w;
   const cq_config& c = *cfg;
   const size_t d = c.dim, qd = (size_t)c.n_heads * c.head_dim, kvd = (size_t)c.n_kv_heads * c.head_dim;
+  s->kv_dtype = kv_dtype;
   s->layer_kv_halves = (size_t)c.n_kv_heads * c.max_seq_len * c.head_dim;
-  const size_t kv_bytes = (size_t)c.n_layers * s->layer_kv_halves * 2;
+  const size_t kv_bytes = (size_t)c.n_layers * s->layer_kv_halves * (kv_dtype == CQ_KV_INT8 ? 1 : 2);
+  const size_t sc_bytes = kv_dtype == CQ_KV_INT8 ? (size_t)c.n_layers * c.n_kv_heads * c.max_seq_len * 4 : 0;
   // one arena: small activations, control block, history, stamps, workspaces, K, V
   size_t off = 0;
   auto take = [&](size_t bytes) { size_t o = off; off = align_up(off + bytes); return o; };
@@ -456,7 +515,7 @@ extern "C" int cq_state_create(const cq_config* cfg, const cq_weights* w, cq_sta
                o_attn = take(attention_workspace_bytes(c.n_heads, c.n_kv_heads, c.head_dim)),
                o_arg = take(kArgmaxPartials * 8 + 64), o_rope = take((size_t)c.head_dim / 2 * sizeof(double));
   const size_t small = off;
-  const size_t o_kc = take(kv_bytes), o_vc = take(kv_bytes);
+  const size_t o_kc = take(kv_bytes), o_vc = take(kv_bytes), o_ks = take(sc_bytes), o_vs = take(sc_bytes);
   if (hipMalloc(&s->arena, off) != hipSuccess) return fail(CQ_ENOMEM, "state_create: device allocation failed");
   char* a = s->arena;
   s->x = (__half*)(a + o_x); s->xb = (__half*)(a + o_xb); s->q = (__half*)(a + o_q); s->k = (__half*)(a + o_k);
@@ -464,6 +523,7 @@ extern "C" int cq_state_create(const cq_config* cfg, const cq_weights* w, cq_sta
   s->ctl = (StepCtl*)(a + o_ctl); s->history = (int*)(a + o_hist); s->tokens_dev = (int*)(a + o_tok);
   s->stamp = (uint32_t*)(a + o_stamp); s->attn_ws = a + o_attn; s->argmax_ws = (unsigned long long*)(a + o_arg);
   s->kcache = (__half*)(a + o_kc); s->vcache = (__half*)(a + o_vc);
+  if (sc_bytes) { s->kscale = (float*)(a + o_ks); s->vscale = (float*)(a + o_vs); }
   s->rope_inv_freq = (double*)(a + o_rope);
   int rc = CQ_OK;
   auto chk = [&](hipError_t e, const char* what) {
@@ -472,6 +532,10 @@ extern "C" int cq_state_create(const cq_config* cfg, const cq_weights* w, cq_sta
   chk(hipMemset(a, 0, small), "hipMemset");
   chk(hipMemset(a + o_kc, 0, kv_bytes), "hipMemset K");   // model.cu:37-38
   chk(hipMemset(a + o_vc, 0, kv_bytes), "hipMemset V");
+  if (sc_bytes) {
+    chk(hipMemset(a + o_ks, 0, sc_bytes), "hipMemset K scales");
+    chk(hipMemset(a + o_vs, 0, sc_bytes), "hipMemset V scales");
+  }
   StepCtl init{};
   init.epoch = 1u;
   init.max_history = c.max_seq_len;
@@ -560,56 +624,96 @@ extern "C" int cq_state_fill_kv(cq_state* s, int32_t n_pos, uint64_t seed) {
   if (n_pos < 0 || n_pos > s->cfg.max_seq_len) return fail(CQ_ERANGE, "fill_kv: n_pos outside [0, max_seq_len]");
   if (n_pos == 0) return CQ_OK;
   const cq_config& c = s->cfg;
-  hipLaunchKernelGGL(fill_kv_kernel, dim3(8192), dim3(256), 0, s->stream, s->kcache, s->vcache, c.n_layers,
-                     c.n_kv_heads, n_pos, c.max_seq_len, c.head_dim, seed, synth_mul(1.0));
+  if (s->kv_dtype == CQ_KV_INT8)
+    hipLaunchKernelGGL(fill_kv8_kernel, dim3(4096), dim3(256), 0, s->stream, reinterpret_cast<int8_t*>(s->kcache),
+                       reinterpret_cast<int8_t*>(s->vcache), s->kscale, s->vscale, c.n_layers, c.n_kv_heads, n_pos,
+                       c.max_seq_len, c.head_dim, seed, synth_mul(1.0));
+  else
+    hipLaunchKernelGGL(fill_kv_kernel, dim3(8192), dim3(256), 0, s->stream, s->kcache, s->vcache, c.n_layers,
+                       c.n_kv_heads, n_pos, c.max_seq_len, c.head_dim, seed, synth_mul(1.0));
   CQ_HIP(hipGetLastError());
   CQ_HIP(hipStreamSynchronize(s->stream));
   return CQ_OK;
 }
 
-static int kv_slab(cq_state* s, int layer, int kv_head, int kind, int n_pos, __half** base, size_t* halves) {
+// One (layer, kv head, K or V) slab of the cache: `elems` elements (whole
+// tiles covering n_pos positions) at `base`, element size 2 (fp16) or 1
+// (int8, with `scales` pointing at the slab's per-position scales).
+static int kv_slab(cq_state* s, int layer, int kv_head, int kind, int n_pos, char** base, size_t* elems,
+                   float** scales) {
   const cq_config& c = s->cfg;
   if (layer < 0 || layer >= c.n_layers || kv_head < 0 || kv_head >= c.n_kv_heads || (kind != 0 && kind != 1))
     return fail(CQ_EINVAL, "kv access: bad layer / head / kind");
   if (n_pos < 0 || n_pos > c.max_seq_len) return fail(CQ_ERANGE, "kv access: n_pos outside [0, max_seq_len]");
   const int tile = kind == 0 ? 16 : 32;
   const int tiles = (n_pos + tile - 1) / tile;
-  *halves = (size_t)tiles * tile * c.head_dim;
-  *base = (kind == 0 ? s->kcache : s->vcache) + (size_t)layer * s->layer_kv_halves +
-          (size_t)kv_head * c.max_seq_len * c.head_dim;
+  const size_t es = s->kv_dtype == CQ_KV_INT8 ? 1 : 2;
+  *elems = (size_t)tiles * tile * c.head_dim;
+  const size_t first = (size_t)layer * s->layer_kv_halves + (size_t)kv_head * c.max_seq_len * c.head_dim;
+  *base = reinterpret_cast<char*>(kind == 0 ? s->kcache : s->vcache) + first * es;
+  *scales = nullptr;
+  if (es == 1)
+    *scales = (kind == 0 ? s->kscale : s->vscale) + ((size_t)layer * c.n_kv_heads + kv_head) * c.max_seq_len;
   return CQ_OK;
+}
+
+static size_t kv_index(int kind, int t, int d, int ms, int hd) {
+  return (size_t)(kind == 0 ? kv_k_offset(0, t, d, ms, hd) : kv_v_offset(0, t, d, ms, hd));
 }
 
 extern "C" int cq_state_kv_read(cq_state* s, int32_t layer, int32_t kv_head, int32_t kind, int32_t n_pos,
                                 uint16_t* host_out) {
   if (!s || !host_out) return fail(CQ_EINVAL, "kv_read: null argument");
-  __half* base;
-  size_t halves;
-  CQ_TRY(kv_slab(s, layer, kv_head, kind, n_pos, &base, &halves));
-  std::vector<uint16_t> tmp(halves);
-  CQ_HIP(hipStreamSynchronize(s->stream));
-  CQ_HIP(hipMemcpy(tmp.data(), base, halves * 2, hipMemcpyDeviceToHost));
+  char* base;
+  size_t elems;
+  float* scales;
+  CQ_TRY(kv_slab(s, layer, kv_head, kind, n_pos, &base, &elems, &scales));
   const int hd = s->cfg.head_dim, ms = s->cfg.max_seq_len;
+  CQ_HIP(hipStreamSynchronize(s->stream));
+  if (!scales) {
+    std::vector<uint16_t> tmp(elems);
+    CQ_HIP(hipMemcpy(tmp.data(), base, elems * 2, hipMemcpyDeviceToHost));
+    for (int t = 0; t < n_pos; ++t)
+      for (int d = 0; d < hd; ++d) host_out[(size_t)t * hd + d] = tmp[kv_index(kind, t, d, ms, hd)];
+    return CQ_OK;
+  }
+  // int8: the dequantized value half(q * s)
+  std::vector<int8_t> tmp(elems);
+  std::vector<float> sc(n_pos > 0 ? n_pos : 1);
+  CQ_HIP(hipMemcpy(tmp.data(), base, elems, hipMemcpyDeviceToHost));
+  if (n_pos) CQ_HIP(hipMemcpy(sc.data(), scales, (size_t)n_pos * 4, hipMemcpyDeviceToHost));
   for (int t = 0; t < n_pos; ++t)
-    for (int d = 0; d < hd; ++d)
-      host_out[(size_t)t * hd + d] = tmp[(size_t)(kind == 0 ? kv_k_offset(0, t, d, ms, hd) : kv_v_offset(0, t, d, ms, hd))];
+    for (int d = 0; d < hd; ++d) host_out[(size_t)t * hd + d] = f2h_bits((float)tmp[kv_index(kind, t, d, ms, hd)] * sc[t]);
   return CQ_OK;
 }
 
 extern "C" int cq_state_kv_write(cq_state* s, int32_t layer, int32_t kv_head, int32_t kind, int32_t n_pos,
                                  const uint16_t* host_in) {
   if (!s || !host_in) return fail(CQ_EINVAL, "kv_write: null argument");
-  __half* base;
-  size_t halves;
-  CQ_TRY(kv_slab(s, layer, kv_head, kind, n_pos, &base, &halves));
-  std::vector<uint16_t> tmp(halves);
-  CQ_HIP(hipStreamSynchronize(s->stream));
-  CQ_HIP(hipMemcpy(tmp.data(), base, halves * 2, hipMemcpyDeviceToHost));
+  char* base;
+  size_t elems;
+  float* scales;
+  CQ_TRY(kv_slab(s, layer, kv_head, kind, n_pos, &base, &elems, &scales));
   const int hd = s->cfg.head_dim, ms = s->cfg.max_seq_len;
-  for (int t = 0; t < n_pos; ++t)
-    for (int d = 0; d < hd; ++d)
-      tmp[(size_t)(kind == 0 ? kv_k_offset(0, t, d, ms, hd) : kv_v_offset(0, t, d, ms, hd))] = host_in[(size_t)t * hd + d];
-  CQ_HIP(hipMemcpy(base, tmp.data(), halves * 2, hipMemcpyHostToDevice));
+  CQ_HIP(hipStreamSynchronize(s->stream));
+  if (!scales) {
+    std::vector<uint16_t> tmp(elems);
+    CQ_HIP(hipMemcpy(tmp.data(), base, elems * 2, hipMemcpyDeviceToHost));
+    for (int t = 0; t < n_pos; ++t)
+      for (int d = 0; d < hd; ++d) tmp[kv_index(kind, t, d, ms, hd)] = host_in[(size_t)t * hd + d];
+    CQ_HIP(hipMemcpy(base, tmp.data(), elems * 2, hipMemcpyHostToDevice));
+    return CQ_OK;
+  }
+  // int8: each position's row quantized with s = max|x| / 127
+  std::vector<int8_t> tmp(elems), q(hd);
+  std::vector<float> sc(n_pos > 0 ? n_pos : 1);
+  CQ_HIP(hipMemcpy(tmp.data(), base, elems, hipMemcpyDeviceToHost));
+  for (int t = 0; t < n_pos; ++t) {
+    quant_row8_host(host_in + (size_t)t * hd, hd, q.data(), &sc[t]);
+    for (int d = 0; d < hd; ++d) tmp[kv_index(kind, t, d, ms, hd)] = q[d];
+  }
+  CQ_HIP(hipMemcpy(base, tmp.data(), elems, hipMemcpyHostToDevice));
+  if (n_pos) CQ_HIP(hipMemcpy(scales, sc.data(), (size_t)n_pos * 4, hipMemcpyHostToDevice));
   return CQ_OK;
 }
 
@@ -656,8 +760,14 @@ int prefill_batched(cq_state* s, const int32_t* tokens, int n, int pos0) {
     CQ_TRY(launch_pf_embed(s->w->embed, s->pf_tokens, M, d, s->pf_x, st));
     for (int l = 0; l < c.n_layers; ++l) {
       const LayerW& L = s->w->layers[l];
-      _Float16* kc = (_Float16*)(s->kcache + (size_t)l * s->layer_kv_halves);
-      _Float16* vc = (_Float16*)(s->vcache + (size_t)l * s->layer_kv_halves);
+      const bool kv8 = s->kv_dtype == CQ_KV_INT8;
+      _Float16* kc = kv8 ? nullptr : (_Float16*)(s->kcache + (size_t)l * s->layer_kv_halves);
+      _Float16* vc = kv8 ? nullptr : (_Float16*)(s->vcache + (size_t)l * s->layer_kv_halves);
+      int8_t* kc8 = kv8 ? reinterpret_cast<int8_t*>(s->kcache) + (size_t)l * s->layer_kv_halves : nullptr;
+      int8_t* vc8 = kv8 ? reinterpret_cast<int8_t*>(s->vcache) + (size_t)l * s->layer_kv_halves : nullptr;
+      const size_t ls = (size_t)l * c.n_kv_heads * c.max_seq_len;
+      float* ksc = kv8 ? s->kscale + ls : nullptr;
+      float* vsc = kv8 ? s->vscale + ls : nullptr;
       CQ_TRY(launch_pf_norm(s->pf_x, L.in_norm, c.norm_eps, M, d, s->pf_a, s->pf_inv, st));
       PfGemmArgs g;
       g.mode = GM_QKV; g.quant = c.quant_type; g.A = (const _Float16*)s->pf_a; g.inv = s->pf_inv;
@@ -668,12 +778,14 @@ int prefill_batched(cq_state* s, const int32_t* tokens, int n, int pos0) {
       g.rows[0] = qd; g.rows[1] = kvd; g.rows[2] = kvd;
       g.out = (_Float16*)s->pf_q; g.head_dim = c.head_dim; g.pos0 = pos0 + c0; g.max_seq = c.max_seq_len;
       g.inv_freq = s->rope_inv_freq; g.kcache = kc; g.vcache = vc;
+      g.kcache8 = kc8; g.vcache8 = vc8; g.kscale = ksc; g.vscale = vsc;
       g.part = s->pf_part; g.part_bytes = kPrefillPartBytes;
       CQ_TRY(launch_pf_gemm(g, st));
       PfAttnArgs at;
       at.q = (const _Float16*)s->pf_q; at.kcache = kc; at.vcache = vc; at.out = (_Float16*)s->pf_ao;
       at.M = M; at.pos0 = pos0 + c0; at.n_heads = c.n_heads; at.n_kv = c.n_kv_heads; at.head_dim = c.head_dim;
       at.max_seq = c.max_seq_len;
+      at.kcache8 = kc8; at.vcache8 = vc8; at.kscale = ksc; at.vscale = vsc;
       CQ_TRY(launch_pf_attention(at, st));
       if (l == c.n_layers - 1) break;   // the last layer's residual stream feeds nothing here
       PfGemmArgs o;

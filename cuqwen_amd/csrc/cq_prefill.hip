@@ -138,6 +138,19 @@ __device__ __forceinline__ void pf_qkv_store(const PfGemmArgs& a, int mat, int l
   }
 }
 
+// One (token, kv head) row into the int8 cache: q = rint(x / s) clamped to
+// +-127 (s = max|x| / 127, a zero row keeps s = 0), element d from value(d).
+template <typename F>
+__device__ __forceinline__ void pf_kv8_store(const PfGemmArgs& a, int mat, int kvh, int pos, float sc, F value) {
+  const int hd = a.head_dim;
+  int8_t* c = mat == 1 ? a.kcache8 : a.vcache8;
+  for (int d = 0; d < hd; ++d) {
+    const int8_t q = sc == 0.f ? (int8_t)0 : (int8_t)fminf(127.f, fmaxf(-127.f, rintf(value(d) / sc)));
+    c[mat == 1 ? kv_k_offset(kvh, pos, d, a.max_seq, hd) : kv_v_offset(kvh, pos, d, a.max_seq, hd)] = q;
+  }
+  (mat == 1 ? a.kscale : a.vscale)[(int64_t)kvh * a.max_seq + pos] = sc;
+}
+
 template <int Q>
 __device__ __forceinline__ void pf_load_w(const PfGemmArgs& a, const char* rowp, int ks, int j, u4_t* w) {
   constexpr int L = PfW<Q>::LOADS;
@@ -363,7 +376,29 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm_kernel(const PfGemmArgs a)
       float y0 = (float)ot[nl0 * kPfBM + ml], y1 = (float)ot[nl1 * kPfBM + ml];
       const int pos = a.pos0 + m, i = local % hd;
       if (mat < 2) rope_rotate(y0, y1, pos, a.inv_freq[i]);
-      pf_qkv_store(a, mat, local, m, (_Float16)y0, (_Float16)y1);
+      if (a.kcache8 && mat > 0) {
+        // int8 cache: rotated values back into the tile, quantized per head below
+        ot[nl0 * kPfBM + ml] = (_Float16)y0;
+        ot[nl1 * kPfBM + ml] = (_Float16)y1;
+      } else {
+        pf_qkv_store(a, mat, local, m, (_Float16)y0, (_Float16)y1);
+      }
+    }
+    if (a.kcache8) {
+      __syncthreads();
+      const int heads = kPfBN / hd;
+      for (int idx = threadIdx.x; idx < heads * kPfBM; idx += kPfThreads) {
+        const int hb = idx / kPfBM, ml = idx % kPfBM;
+        const int n0 = nb0 + hb * hd, m = m0 + ml;
+        if (n0 >= a.N || m >= a.M) continue;
+        int local;
+        const int mat = pf_mat(a, n0, &local);
+        if (mat == 0) continue;
+        float amax = 0.f;
+        for (int d = 0; d < hd; ++d) amax = fmaxf(amax, fabsf((float)ot[(hb * hd + d) * kPfBM + ml]));
+        pf_kv8_store(a, mat, local / hd, a.pos0 + m, amax / 127.0f,
+                     [&](int d) { return (float)ot[(hb * hd + d) * kPfBM + ml]; });
+      }
     }
   }
 }
@@ -381,17 +416,42 @@ __global__ __launch_bounds__(256) void pf_split_epilogue(const PfGemmArgs a, int
   };
   if constexpr (MODE == GM_QKV) {
     const int hd = a.head_dim, half = hd / 2, np = a.N / 2;
-    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < (int64_t)a.M * np;
+    // fp16 value of row n (bias added, before RoPE) of token m
+    auto raw = [&](int m, int n) {
+      int local;
+      const int mat = pf_mat(a, n, &local);
+      const _Float16* b = a.bias[mat];
+      return (float)(_Float16)(sum(0, m, n) * a.inv[m] + (b ? (float)b[local] : 0.f));
+    };
+    const int np_store = a.kcache8 ? a.rows[0] / 2 : np;   // int8 cache: k / v rows go per head below
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < (int64_t)a.M * np_store;
          idx += (int64_t)gridDim.x * blockDim.x) {
-      const int m = (int)(idx / np), p = (int)(idx % np);
+      const int m = (int)(idx / np_store), p = (int)(idx % np_store);
       const int n0 = (p / half) * hd + p % half, n1 = n0 + half;
       int local;
       const int mat = pf_mat(a, n0, &local);
-      const _Float16* b = a.bias[mat];
-      float y0 = (float)(_Float16)(sum(0, m, n0) * a.inv[m] + (b ? (float)b[local] : 0.f));
-      float y1 = (float)(_Float16)(sum(0, m, n1) * a.inv[m] + (b ? (float)b[local + half] : 0.f));
+      float y0 = raw(m, n0), y1 = raw(m, n1);
       if (mat < 2) rope_rotate(y0, y1, a.pos0 + m, a.inv_freq[local % hd]);
       pf_qkv_store(a, mat, local, m, (_Float16)y0, (_Float16)y1);
+    }
+    if (a.kcache8) {
+      const int n_kv = a.rows[1] / hd;
+      for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < (int64_t)a.M * 2 * n_kv;
+           idx += (int64_t)gridDim.x * blockDim.x) {
+        const int m = (int)(idx / (2 * n_kv)), r = (int)(idx % (2 * n_kv));
+        const int mat = 1 + r / n_kv, kvh = r % n_kv;
+        const int nb = a.rows[0] + (mat == 2 ? a.rows[1] : 0) + kvh * hd;
+        // element d of the rotated (k) or plain (v) row, recomputed per use
+        auto value = [&](int d) {
+          const int i = d % half;
+          float y0 = raw(m, nb + i), y1 = raw(m, nb + i + half);
+          if (mat == 1) rope_rotate(y0, y1, a.pos0 + m, a.inv_freq[i]);
+          return (float)(_Float16)(d < half ? y0 : y1);
+        };
+        float amax = 0.f;
+        for (int d = 0; d < hd; ++d) amax = fmaxf(amax, fabsf(value(d)));
+        pf_kv8_store(a, mat, kvh, a.pos0 + m, amax / 127.0f, value);
+      }
     }
   } else {
     for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < MN; idx += (int64_t)gridDim.x * blockDim.x) {
@@ -466,7 +526,7 @@ __device__ __forceinline__ void pf_attend_tile(KVTile<HD>& t, const h8_t* qb, in
   for (int dt = 0; dt < DT; ++dt) o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(t.va[dt], pb, o[dt], 0, 0, 0);
 }
 
-template <int HD>
+template <int HD, bool KV8>
 __global__ __launch_bounds__(kAttnThreads) void pf_attention_kernel(const PfAttnArgs a) {
   constexpr int KK = HD / 32, DT = HD / 16;
   const int t0 = blockIdx.x * 16, hq = blockIdx.y;
@@ -480,9 +540,6 @@ __global__ __launch_bounds__(kAttnThreads) void pf_attention_kernel(const PfAttn
   const float scale = 1.0f / sqrtf((float)HD);
   const _Float16* kbase = a.kcache + (int64_t)kvh * a.max_seq * HD;
   const _Float16* vbase = a.vcache + (int64_t)kvh * a.max_seq * HD;
-  KVTile<HD> A, B;
-  int ti = wave;
-  if (ti < n_tiles) load_tile<HD>(A, kbase, vbase, ti, lane);
   h8_t qb[KK];
   const _Float16* q = a.q + (int64_t)tcol * a.n_heads * HD + hq * HD;
 #pragma unroll
@@ -491,13 +548,34 @@ __global__ __launch_bounds__(kAttnThreads) void pf_attention_kernel(const PfAttn
   f4_t o[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) o[dt] = f4_t{0.f, 0.f, 0.f, 0.f};
-  for (; ti < n_tiles; ti += 2 * kAttnWaves) {
-    const int t1 = ti + kAttnWaves;
-    if (t1 < n_tiles) load_tile<HD>(B, kbase, vbase, t1, lane);
-    pf_attend_tile<HD>(A, qb, ti, t_lane, t_max, scale, j, m, l, o);
-    if (t1 >= n_tiles) break;
-    if (t1 + kAttnWaves < n_tiles) load_tile<HD>(A, kbase, vbase, t1 + kAttnWaves, lane);
-    pf_attend_tile<HD>(B, qb, t1, t_lane, t_max, scale, j, m, l, o);
+  int ti = wave;
+  if constexpr (KV8) {
+    const int8_t* kb8 = a.kcache8 + (int64_t)kvh * a.max_seq * HD;
+    const int8_t* vb8 = a.vcache8 + (int64_t)kvh * a.max_seq * HD;
+    const float* ksc = a.kscale + (int64_t)kvh * a.max_seq;
+    const float* vsc = a.vscale + (int64_t)kvh * a.max_seq;
+    const uint32_t magic = vgpr_const(0x64646464u);
+    KVTile8<HD> A, B;
+    if (ti < n_tiles) load_tile8<HD>(A, kb8, vb8, ksc, vsc, ti, lane);
+    for (; ti < n_tiles; ti += 2 * kAttnWaves) {
+      const int t1 = ti + kAttnWaves;
+      if (t1 < n_tiles) load_tile8<HD>(B, kb8, vb8, ksc, vsc, t1, lane);
+      attend_tile8<HD>(A, qb, ti, t_lane, scale, j, m, l, o, magic);
+      if (t1 >= n_tiles) break;
+      if (t1 + kAttnWaves < n_tiles) load_tile8<HD>(A, kb8, vb8, ksc, vsc, t1 + kAttnWaves, lane);
+      attend_tile8<HD>(B, qb, t1, t_lane, scale, j, m, l, o, magic);
+    }
+  } else {
+    KVTile<HD> A, B;
+    if (ti < n_tiles) load_tile<HD>(A, kbase, vbase, ti, lane);
+    for (; ti < n_tiles; ti += 2 * kAttnWaves) {
+      const int t1 = ti + kAttnWaves;
+      if (t1 < n_tiles) load_tile<HD>(B, kbase, vbase, t1, lane);
+      pf_attend_tile<HD>(A, qb, ti, t_lane, t_max, scale, j, m, l, o);
+      if (t1 >= n_tiles) break;
+      if (t1 + kAttnWaves < n_tiles) load_tile<HD>(A, kbase, vbase, t1 + kAttnWaves, lane);
+      pf_attend_tile<HD>(B, qb, t1, t_lane, t_max, scale, j, m, l, o);
+    }
   }
   l += __shfl_xor(l, 16, kWave);
   l += __shfl_xor(l, 32, kWave);
@@ -582,7 +660,9 @@ int launch_pf_gemm(const PfGemmArgs& a, hipStream_t stream) {
   if (a.quant != CQ_QUANT_FP16 && !a.S[0]) return fail(CQ_EINVAL, "prefill gemm: quantized weights need scales");
   if (a.mode == GM_SWIGLU && (!a.W[1] || !a.inv)) return fail(CQ_EINVAL, "prefill gemm: swiglu needs gate, up and the norm");
   if (a.mode == GM_QKV) {
-    if (!a.inv || !a.W[1] || !a.W[2] || !a.kcache || !a.vcache || !a.inv_freq) return fail(CQ_EINVAL, "prefill gemm: qkv operands");
+    if (!a.inv || !a.W[1] || !a.W[2] || !a.inv_freq) return fail(CQ_EINVAL, "prefill gemm: qkv operands");
+    if (a.kcache8 ? (!a.vcache8 || !a.kscale || !a.vscale) : (!a.kcache || !a.vcache))
+      return fail(CQ_EINVAL, "prefill gemm: qkv cache pointers");
     if (kPfBN % a.head_dim || a.rows[0] % a.head_dim || a.rows[1] % a.head_dim || a.rows[0] + a.rows[1] + a.rows[2] != a.N)
       return fail(CQ_EINVAL, "prefill gemm: qkv rows must be whole heads");
   }
@@ -597,8 +677,14 @@ int launch_pf_attention(const PfAttnArgs& a, hipStream_t stream) {
   if (a.head_dim != 64 && a.head_dim != 128) return fail(CQ_EINVAL, "prefill attention: head_dim must be 64 or 128");
   if (a.M <= 0 || a.pos0 < 0 || a.pos0 + a.M > a.max_seq) return fail(CQ_ERANGE, "prefill attention: positions");
   const dim3 grid((a.M + 15) / 16, a.n_heads);
-  if (a.head_dim == 128) hipLaunchKernelGGL(pf_attention_kernel<128>, grid, dim3(kAttnThreads), 0, stream, a);
-  else hipLaunchKernelGGL(pf_attention_kernel<64>, grid, dim3(kAttnThreads), 0, stream, a);
+  if (a.kcache8) {
+    if (!a.vcache8 || !a.kscale || !a.vscale) return fail(CQ_EINVAL, "prefill attention: int8 cache pointers");
+    if (a.head_dim == 128) hipLaunchKernelGGL((pf_attention_kernel<128, true>), grid, dim3(kAttnThreads), 0, stream, a);
+    else hipLaunchKernelGGL((pf_attention_kernel<64, true>), grid, dim3(kAttnThreads), 0, stream, a);
+  } else {
+    if (a.head_dim == 128) hipLaunchKernelGGL((pf_attention_kernel<128, false>), grid, dim3(kAttnThreads), 0, stream, a);
+    else hipLaunchKernelGGL((pf_attention_kernel<64, false>), grid, dim3(kAttnThreads), 0, stream, a);
+  }
   CQ_HIP(hipGetLastError());
   return CQ_OK;
 }

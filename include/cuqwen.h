@@ -110,6 +110,22 @@ int cq_state_create(const cq_config* cfg, const cq_weights* w, cq_state** out);
 /* free_qwen_state() (include/model.cuh:49). */
 int cq_state_destroy(cq_state* s);
 
+/* KV cache element types.  The reference keeps the cache in fp16
+ * (src/model.cu:37-38); an int8 cache is its roadmap item (README.md:147).
+ * CQ_KV_INT8 stores each (position, kv head) row of K and of V as
+ * q = clamp(rint(x / s), -127, 127) with s = max|x| / 127 in fp32 (a zero row
+ * keeps s = 0), halving the bytes the attention streams.  Scores are
+ * half((q . k_q) * s_k / sqrt(head_dim)), P is rounded as half(p * s_v) for
+ * the PV product. */
+#define CQ_KV_FP16 0
+#define CQ_KV_INT8 1
+
+/* malloc_qwen_state with a choice of KV cache element type (CQ_KV_*);
+ * cq_state_create is cq_state_create_kv(..., CQ_KV_FP16, ...).  With an int8
+ * cache, cq_state_kv_read returns half(q * s) and cq_state_kv_write
+ * quantizes each position's row as above. */
+int cq_state_create_kv(const cq_config* cfg, const cq_weights* w, int32_t kv_dtype, cq_state** out);
+
 /* qwen_forward() (include/model.cuh:51-60, src/model.cu:183-223): one decode
  * step for `token` at position `pos`, repetition penalty over
  * history[0..history_len), greedy argmax; synchronous; *token_out receives
@@ -289,6 +305,18 @@ int cq_gqa_attention_decode(const void* q, const void* layer_k_cache, const void
                             const int32_t* d_pos, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
                             int32_t max_seq_len, void* workspace, void* stream);
 size_t cq_attention_workspace_bytes(int32_t n_heads, int32_t n_kv_heads, int32_t head_dim);
+
+/* The same decode attention over an int8 layer cache (see CQ_KV_INT8; no
+ * counterpart in the reference): k_new / v_new ([n_kv_heads * head_dim]
+ * fp16) are quantized into position *d_pos of k_cache8 / v_cache8 (same
+ * tiled element layout as the fp16 cache, one byte per element, see
+ * cq_kv_*_offset) with their scales into k_scale / v_scale
+ * ([n_kv_heads][max_seq_len] fp32), then attn_out is computed over keys
+ * [0, *d_pos].  `workspace` as for cq_gqa_attention_decode. */
+int cq_gqa_attention_decode_kv8(const void* q, const void* k_new, const void* v_new, void* k_cache8, void* v_cache8,
+                                float* k_scale, float* v_scale, void* attn_out, const int32_t* d_pos,
+                                int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, int32_t max_seq_len,
+                                void* workspace, void* stream);
 
 /* Dequantise rows of a quantized matrix to fp32 with the device unpacking
  * path of the GEMVs (q * fp16 scale): out[rows][cols].  Test hook for the

@@ -307,6 +307,102 @@ void attention(const uint16_t* q, const uint16_t* K, const uint16_t* V, uint16_t
   }
 }
 
+// ------------------------------------------------------------ int8 KV
+// An extension of the reference (its KV cache is fp16, src/model.cu:37-38;
+// a quantized cache is its roadmap item, README.md:147): each (position,
+// kv head) row of K and of V is stored as q = clamp(rint(x / s), -127, 127)
+// with s = max|x| / 127 in fp32 (a zero row keeps s = 0 and q = 0).
+void quant_row_i8(const uint16_t* x, int n, int8_t* q, float* s) {
+  float amax = 0.f;
+  for (int i = 0; i < n; ++i) amax = std::max(amax, std::fabs(h2f(x[i])));
+  const float sc = amax / 127.0f;
+  *s = sc;
+  for (int i = 0; i < n; ++i) {
+    if (sc == 0.f) { q[i] = 0; continue; }
+    const float r = std::nearbyint(h2f(x[i]) / sc);   // round half to even
+    q[i] = (int8_t)std::max(-127.f, std::min(127.f, r));
+  }
+}
+
+// Attention over an int8 cache Kq/Vq [n_kv][stride][hd] with row scales
+// Ks/Vs [n_kv][stride].  mode 1: softmax over q.(kq*ks)/sqrt(hd) of (vq*vs)
+// in double.  mode 0: the device's rounding points: score =
+// half((q.kq) * ks * 1/sqrt(hd)) with the dot in fp32, e = exp(s - m_part),
+// P = half(e * vs) for the PV product while the partition sum adds the
+// unrounded e, partitions merged like attention() above.
+void attention_i8(const uint16_t* q, const int8_t* Kq, const float* Ks, const int8_t* Vq, const float* Vs,
+                  uint16_t* out, int n_heads, int n_kv, int hd, int64_t stride, int T, int mode, int nparts) {
+  const int g = n_heads / n_kv;
+  const float scale = 1.0f / std::sqrt((float)hd);
+#pragma omp parallel for schedule(dynamic)
+  for (int h = 0; h < n_heads; ++h) {
+    const int kvh = h / g;
+    const uint16_t* qh = q + (int64_t)h * hd;
+    const int8_t* Kh = Kq + (int64_t)kvh * stride * hd;
+    const int8_t* Vh = Vq + (int64_t)kvh * stride * hd;
+    const float* ksh = Ks + (int64_t)kvh * stride;
+    const float* vsh = Vs + (int64_t)kvh * stride;
+    if (mode == 1) {
+      std::vector<double> s(T);
+      double mx = -INFINITY;
+      for (int t = 0; t < T; ++t) {
+        double a = 0.0;
+        for (int d = 0; d < hd; ++d) a += (double)h2f(qh[d]) * ((double)Kh[(int64_t)t * hd + d] * ksh[t]);
+        s[t] = a / std::sqrt((double)hd);
+        mx = std::max(mx, s[t]);
+      }
+      double L = 0.0;
+      std::vector<double> o(hd, 0.0);
+      for (int t = 0; t < T; ++t) {
+        const double e = std::exp(s[t] - mx);
+        L += e;
+        for (int d = 0; d < hd; ++d) o[d] += e * ((double)Vh[(int64_t)t * hd + d] * vsh[t]);
+      }
+      for (int d = 0; d < hd; ++d) out[(int64_t)h * hd + d] = f2h((float)(o[d] / L));
+      continue;
+    }
+    const int chunk = (T + nparts - 1) / nparts;
+    const int nonempty = (T + chunk - 1) / chunk;
+    std::vector<float> pm(nonempty), ps(nonempty), po((size_t)nonempty * hd);
+    for (int p = 0; p < nonempty; ++p) {
+      const int t0 = p * chunk, t1 = std::min(t0 + chunk, T);
+      std::vector<float> sc(t1 - t0);
+      float mx = -1e30f;
+      for (int t = t0; t < t1; ++t) {
+        float a = 0.f;
+        for (int d = 0; d < hd; ++d) a += h2f(qh[d]) * (float)Kh[(int64_t)t * hd + d];
+        sc[t - t0] = rh(a * ksh[t] * scale);
+        mx = std::max(mx, sc[t - t0]);
+      }
+      float sum = 0.f;
+      std::vector<float> pv(hd, 0.f);
+      for (int t = t0; t < t1; ++t) {
+        const float e = std::exp(sc[t - t0] - mx);
+        sum += e;
+        const float P = rh(e * vsh[t]);
+        for (int d = 0; d < hd; ++d) pv[d] += P * (float)Vh[(int64_t)t * hd + d];
+      }
+      pm[p] = mx;
+      ps[p] = sum;
+      for (int d = 0; d < hd; ++d) po[(size_t)p * hd + d] = pv[d];
+    }
+    float M = -1e30f;
+    for (int p = 0; p < nonempty; ++p) M = std::max(M, pm[p]);
+    std::vector<float> r(nonempty);
+    float L = 0.f;
+    for (int p = 0; p < nonempty; ++p) {
+      r[p] = std::exp(pm[p] - M);
+      L += ps[p] * r[p];
+    }
+    const float inv = 1.0f / (L + 1e-9f);
+    for (int d = 0; d < hd; ++d) {
+      float a = 0.f;
+      for (int p = 0; p < nonempty; ++p) a += po[(size_t)p * hd + d] * r[p];
+      out[(int64_t)h * hd + d] = f2h(a * inv);
+    }
+  }
+}
+
 // ---------------------------------------------------------------- argmax
 // kernels.cu:907-961: order-preserving key, ties -> lowest index.
 uint64_t argmax_key(float v, int idx) {
@@ -358,6 +454,9 @@ struct Model {
   std::vector<Layer> L;
   int kv_slots = 0;
   std::vector<uint16_t> K, V;   // [layers][kv][kv_slots][hd]
+  int kv8 = 0;                  // int8 cache: Kq/Vq [layers][kv][kv_slots][hd], Ks/Vs [layers][kv][kv_slots]
+  std::vector<int8_t> Kq, Vq;
+  std::vector<float> Ks, Vs;
   std::vector<uint16_t> logits;
   int nparts = 64;
 };
@@ -407,9 +506,30 @@ bool read_mat(FILE* f, Mat& m, int64_t rows, int64_t cols, int quant) {
 void alloc_kv(Model& m, int slots) {
   m.kv_slots = slots;
   const size_t n = (size_t)m.c.layers * m.c.kv * slots * m.c.hd;
-  m.K.assign(n, 0);
-  m.V.assign(n, 0);
+  const size_t rows = (size_t)m.c.layers * m.c.kv * slots;
+  if (m.kv8) {
+    m.K.clear(); m.V.clear();
+    m.Kq.assign(n, 0); m.Vq.assign(n, 0); m.Ks.assign(rows, 0.f); m.Vs.assign(rows, 0.f);
+  } else {
+    m.Kq.clear(); m.Vq.clear(); m.Ks.clear(); m.Vs.clear();
+    m.K.assign(n, 0); m.V.assign(n, 0);
+  }
   m.logits.assign(m.c.vocab, 0);
+}
+
+// Store one position's k (or v) rows of every kv head of layer l.
+void store_kv(Model& m, int l, int pos, const uint16_t* k, const uint16_t* v) {
+  const Cfg& c = m.c;
+  for (int h = 0; h < c.kv; ++h) {
+    const size_t row = ((size_t)l * c.kv + h) * m.kv_slots + pos;
+    if (m.kv8) {
+      quant_row_i8(k + h * c.hd, c.hd, m.Kq.data() + row * c.hd, m.Ks.data() + row);
+      quant_row_i8(v + h * c.hd, c.hd, m.Vq.data() + row * c.hd, m.Vs.data() + row);
+    } else {
+      std::memcpy(m.K.data() + row * c.hd, k + h * c.hd, c.hd * 2);
+      std::memcpy(m.V.data() + row * c.hd, v + h * c.hd, c.hd * 2);
+    }
+  }
 }
 
 // src/model.cu:76-181: one decode step; returns the argmax id.
@@ -435,13 +555,15 @@ int forward(Model& m, int token, int pos, const int* hist, int hlen, int mode) {
     rope(q.data(), c.heads, c.hd, pos, 1e6f);
     rope(k.data(), c.kv, c.hd, pos, 1e6f);
     const size_t lo = (size_t)l * c.kv * m.kv_slots * c.hd;
-    for (int h = 0; h < c.kv; ++h)
-      for (int e = 0; e < c.hd; ++e) {
-        m.K[lo + ((size_t)h * m.kv_slots + pos) * c.hd + e] = k[h * c.hd + e];
-        m.V[lo + ((size_t)h * m.kv_slots + pos) * c.hd + e] = v[h * c.hd + e];
-      }
-    attention(q.data(), m.K.data() + lo, m.V.data() + lo, att.data(), c.heads, c.kv, c.hd, m.kv_slots, pos + 1, mode,
-              m.nparts);
+    store_kv(m, l, pos, k.data(), v.data());
+    if (m.kv8) {
+      const size_t ls = (size_t)l * c.kv * m.kv_slots;
+      attention_i8(q.data(), m.Kq.data() + lo, m.Ks.data() + ls, m.Vq.data() + lo, m.Vs.data() + ls, att.data(),
+                   c.heads, c.kv, c.hd, m.kv_slots, pos + 1, mode, m.nparts);
+    } else {
+      attention(q.data(), m.K.data() + lo, m.V.data() + lo, att.data(), c.heads, c.kv, c.hd, m.kv_slots, pos + 1,
+                mode, m.nparts);
+    }
 #pragma omp parallel for
     for (int64_t r = 0; r < d; ++r) x[r] = f2h(h2f(x[r]) + gemv(Ly.wo, att.data(), r));   // kernels.cu:671
     rmsnorm(x.data(), Ly.post_norm.data(), xn.data(), d, eps, mode);
@@ -500,6 +622,11 @@ void or_rope(uint16_t* v, int n_heads, int hd, int pos, float theta) { rope(v, n
 void or_attention(const uint16_t* q, const uint16_t* K, const uint16_t* V, uint16_t* out, int n_heads, int n_kv,
                   int hd, int64_t stride, int T, int mode, int nparts) {
   attention(q, K, V, out, n_heads, n_kv, hd, stride, T, mode, nparts);
+}
+void or_quant_row_i8(const uint16_t* x, int n, int8_t* q, float* s) { quant_row_i8(x, n, q, s); }
+void or_attention_i8(const uint16_t* q, const int8_t* Kq, const float* Ks, const int8_t* Vq, const float* Vs,
+                     uint16_t* out, int n_heads, int n_kv, int hd, int64_t stride, int T, int mode, int nparts) {
+  attention_i8(q, Kq, Ks, Vq, Vs, out, n_heads, n_kv, hd, stride, T, mode, nparts);
 }
 int or_argmax(const uint16_t* logits, int vocab) { return argmax(logits, vocab); }
 void or_penalty(uint16_t* logits, const int* hist, int n, int vocab, float pen) { penalty(logits, hist, n, vocab, pen); }
@@ -583,15 +710,35 @@ void or_model_set_nparts(void* h, int nparts) { static_cast<Model*>(h)->nparts =
 void or_model_fill_kv(void* h, int n_pos, uint64_t seed) {
   Model& m = *static_cast<Model*>(h);
   const float mul = gen_mul(1.0);
+  const int hd = m.c.hd;
   for (int l = 0; l < m.c.layers; ++l)
     for (int kh = 0; kh < m.c.kv; ++kh) {
-      const size_t base = ((size_t)l * m.c.kv + kh) * m.kv_slots * m.c.hd;
+      const size_t row0 = ((size_t)l * m.c.kv + kh) * m.kv_slots;
 #pragma omp parallel for
-      for (int64_t e = 0; e < (int64_t)n_pos * m.c.hd; ++e) {
-        m.K[base + e] = gen_half(seed, kv_stream(l, kh, 0), (uint64_t)e, mul, 0.f);
-        m.V[base + e] = gen_half(seed, kv_stream(l, kh, 1), (uint64_t)e, mul, 0.f);
+      for (int t = 0; t < n_pos; ++t) {
+        std::vector<uint16_t> kr(hd), vr(hd);
+        for (int d = 0; d < hd; ++d) {
+          const uint64_t e = (uint64_t)t * hd + d;
+          kr[d] = gen_half(seed, kv_stream(l, kh, 0), e, mul, 0.f);
+          vr[d] = gen_half(seed, kv_stream(l, kh, 1), e, mul, 0.f);
+        }
+        const size_t row = row0 + t;
+        if (m.kv8) {
+          quant_row_i8(kr.data(), hd, m.Kq.data() + row * hd, m.Ks.data() + row);
+          quant_row_i8(vr.data(), hd, m.Vq.data() + row * hd, m.Vs.data() + row);
+        } else {
+          std::memcpy(m.K.data() + row * hd, kr.data(), hd * 2);
+          std::memcpy(m.V.data() + row * hd, vr.data(), hd * 2);
+        }
       }
     }
+}
+
+// Switch the cache to int8 (1) or fp16 (0); clears it.
+void or_model_set_kv8(void* h, int on) {
+  Model& m = *static_cast<Model*>(h);
+  m.kv8 = on;
+  alloc_kv(m, m.kv_slots);
 }
 
 int or_model_forward(void* h, int token, int pos, const int* hist, int hlen, int mode) {
@@ -604,10 +751,26 @@ void or_model_logits(void* h, uint16_t* out) {
   std::memcpy(out, m.logits.data(), m.logits.size() * 2);
 }
 // Raw access for tests: kind 0/1 = K/V of (layer, kv_head) positions [0, n).
+// (int8 cache: the dequantized value half(q * s) of each element.)
 void or_model_kv(void* h, int layer, int kv_head, int kind, int n, uint16_t* out) {
   Model& m = *static_cast<Model*>(h);
-  const size_t base = ((size_t)layer * m.c.kv + kv_head) * m.kv_slots * m.c.hd;
-  std::memcpy(out, (kind ? m.V : m.K).data() + base, (size_t)n * m.c.hd * 2);
+  const size_t row0 = ((size_t)layer * m.c.kv + kv_head) * m.kv_slots;
+  if (m.kv8) {
+    const std::vector<int8_t>& Q = kind ? m.Vq : m.Kq;
+    const std::vector<float>& S = kind ? m.Vs : m.Ks;
+    for (int t = 0; t < n; ++t)
+      for (int d = 0; d < m.c.hd; ++d)
+        out[(size_t)t * m.c.hd + d] = f2h((float)Q[(row0 + t) * m.c.hd + d] * S[row0 + t]);
+    return;
+  }
+  std::memcpy(out, (kind ? m.V : m.K).data() + row0 * m.c.hd, (size_t)n * m.c.hd * 2);
+}
+// Raw int8 rows and scales (int8 cache only).
+void or_model_kv8(void* h, int layer, int kv_head, int kind, int n, int8_t* q, float* sc) {
+  Model& m = *static_cast<Model*>(h);
+  const size_t row0 = ((size_t)layer * m.c.kv + kv_head) * m.kv_slots;
+  std::memcpy(q, (kind ? m.Vq : m.Kq).data() + row0 * m.c.hd, (size_t)n * m.c.hd);
+  std::memcpy(sc, (kind ? m.Vs : m.Ks).data() + row0, (size_t)n * 4);
 }
 // Copy one tensor out for op-level tests: kind = generator kind, which: 0
 // weights/values, 1 scales.  Returns bytes copied (0 when absent).

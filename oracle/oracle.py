@@ -39,6 +39,10 @@ def _load():
         "or_rope": (None, [P, I, I, I, F]),
         "or_attention": (None, [P, P, P, P, I, I, I, I64, I, I, I]),
         "or_argmax": (I, [P, I]),
+        "or_quant_row_i8": (None, [P, I, P, P]),
+        "or_attention_i8": (None, [P, P, P, P, P, P, I, I, I, I64, I, I, I]),
+        "or_model_set_kv8": (None, [P, I]),
+        "or_model_kv8": (None, [P, I, I, I, I, P, P]),
         "or_penalty": (None, [P, P, I, I, F]),
         "or_model_synth": (P, [P, U64, I]),
         "or_model_load": (P, [ctypes.c_char_p, I]),
@@ -120,6 +124,28 @@ def attention(q, K, V, n_heads, n_kv, hd, T, mode=0, nparts=64):
     return out
 
 
+def quant_rows_i8(x):
+    """int8 KV quantization of each row of x (fp16 [n][hd]): (q int8, s fp32)."""
+    x = np.ascontiguousarray(x, dtype=np.float16)
+    n, hd = x.shape
+    q = np.zeros((n, hd), dtype=np.int8)
+    s = np.zeros(n, dtype=np.float32)
+    for i in range(n):
+        lib.or_quant_row_i8(_p(x[i]), hd, _p(q[i]), _p(s[i:i + 1]))
+    return q, s
+
+
+def attention_i8(q, Kq, Ks, Vq, Vs, n_heads, n_kv, hd, T, mode=0, nparts=64):
+    """Attention over an int8 cache: Kq/Vq [n_kv][T][hd] int8, Ks/Vs [n_kv][T] fp32."""
+    Kq, Vq = np.ascontiguousarray(Kq, dtype=np.int8), np.ascontiguousarray(Vq, dtype=np.int8)
+    Ks, Vs = np.ascontiguousarray(Ks, dtype=np.float32), np.ascontiguousarray(Vs, dtype=np.float32)
+    out = np.zeros(n_heads * hd, dtype=np.uint16)
+    qq = np.ascontiguousarray(q, dtype=np.float16)
+    lib.or_attention_i8(_p(qq), _p(Kq), _p(Ks), _p(Vq), _p(Vs), _p(out), n_heads, n_kv, hd, Kq.shape[1], T, mode,
+                        nparts)
+    return out.view(np.float16)
+
+
 def argmax(logits):
     l = np.ascontiguousarray(logits, dtype=np.float16)
     return lib.or_argmax(_p(l), l.size)
@@ -153,6 +179,16 @@ class Model:
 
     def set_nparts(self, n):
         lib.or_model_set_nparts(self.h, n)
+
+    def set_kv8(self, on=True):
+        """int8 KV cache (clears the cache)."""
+        lib.or_model_set_kv8(self.h, 1 if on else 0)
+
+    def kv8(self, layer, kv_head, kind, n):
+        q = np.zeros((n, self.cfg.head_dim), dtype=np.int8)
+        s = np.zeros(n, dtype=np.float32)
+        lib.or_model_kv8(self.h, layer, kv_head, kind, n, _p(q), _p(s))
+        return q, s
 
     def fill_kv(self, n_pos, seed):
         lib.or_model_fill_kv(self.h, n_pos, seed)

@@ -1,0 +1,217 @@
+"""GPU int8 KV cache (CQ_KV_INT8, the reference's roadmap item README.md:147)
+against the host oracle's int8 mode: per-(position, kv head) quantization
+bit-exact, attention within 1e-2, decode and prefill parity."""
+import numpy as np
+import pytest
+
+import cuqwen_amd as cq
+from oracle import oracle as orc
+from tests.conftest import tiny_config
+from tests.gpu_util import Pool, rel_err, k_offsets, v_offsets
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-2
+
+
+@pytest.fixture
+def g():
+    p = Pool()
+    yield p
+    p.close()
+
+
+def _gap(logits):
+    l = np.sort(logits.astype(np.float64))
+    return l[-1] - l[-2]
+
+
+def _tile8(Kq, Vq, max_seq):
+    n_kv, T, hd = Kq.shape
+    kc = np.zeros(n_kv * max_seq * hd, dtype=np.int8)
+    vc = np.zeros(n_kv * max_seq * hd, dtype=np.int8)
+    kc[k_offsets(n_kv, T, hd, max_seq).ravel()] = Kq.ravel()
+    vc[v_offsets(n_kv, T, hd, max_seq).ravel()] = Vq.ravel()
+    return kc, vc
+
+
+@pytest.mark.parametrize("H,KV,hd,T", [(28, 4, 128, 1), (28, 4, 128, 33), (14, 2, 64, 300), (12, 2, 128, 4100),
+                                       (28, 4, 128, 32768), (40, 8, 128, 5000)])
+def test_attention_kv8_matches_oracle(g, H, KV, hd, T):
+    """Positions [0, T-1) come quantized in the cache; the new row (position
+    T-1) arrives in fp16 and must be stored exactly as the oracle quantizes
+    it, scale included; the output matches the oracle's int8 attention."""
+    ms = ((T + 31) // 32) * 32
+    rng = np.random.default_rng(T + H)
+    q = rng.standard_normal(H * hd).astype(np.float16)
+    K = rng.standard_normal((KV, T, hd)).astype(np.float16)
+    V = rng.standard_normal((KV, T, hd)).astype(np.float16)
+    Kq, Ks = orc.quant_rows_i8(K.reshape(-1, hd))
+    Vq, Vs = orc.quant_rows_i8(V.reshape(-1, hd))
+    Kq, Vq, Ks, Vs = Kq.reshape(KV, T, hd), Vq.reshape(KV, T, hd), Ks.reshape(KV, T), Vs.reshape(KV, T)
+    # the device starts with positions [0, T-1) only; T-1 is garbage until the call
+    Kd, Vd = Kq.copy(), Vq.copy()
+    Kd[:, T - 1] = 99
+    Vd[:, T - 1] = -99
+    kc, vc = _tile8(Kd, Vd, ms)
+    ksd = np.zeros((KV, ms), np.float32)
+    vsd = np.zeros((KV, ms), np.float32)
+    ksd[:, :T - 1], vsd[:, :T - 1] = Ks[:, :T - 1], Vs[:, :T - 1]
+    ksd[:, T - 1], vsd[:, T - 1] = np.inf, np.nan
+    pk, pv, pks, pvs = g.put(kc), g.put(vc), g.put(ksd), g.put(vsd)
+    knew = np.ascontiguousarray(K[:, T - 1].reshape(-1))
+    vnew = np.ascontiguousarray(V[:, T - 1].reshape(-1))
+    ws = g.empty(cq.lib.cq_attention_workspace_bytes(H, KV, hd), zero=True)
+    out = g.empty(H * hd * 2)
+    cq.check(cq.lib.cq_gqa_attention_decode_kv8(g.put(q), g.put(knew), g.put(vnew), pk, pv, pks, pvs, out.ptr,
+                                                g.i32(T - 1), H, KV, hd, ms, ws.ptr, None))
+    got = out.to_array(np.float16)
+    assert rel_err(got, orc.attention_i8(q, Kq, Ks, Vq, Vs, H, KV, hd, T, mode=1)) <= TOL
+    assert rel_err(got, orc.attention_i8(q, Kq, Ks, Vq, Vs, H, KV, hd, T, mode=0)) <= TOL
+    # the new row and its scales, bit-exact
+    kc2 = np.zeros_like(kc)
+    vc2 = np.zeros_like(vc)
+    ks2 = np.zeros_like(ksd)
+    vs2 = np.zeros_like(vsd)
+    cq.check(cq.lib.cq_memcpy_d2h(kc2.ctypes.data, pk, kc2.nbytes))
+    cq.check(cq.lib.cq_memcpy_d2h(vc2.ctypes.data, pv, vc2.nbytes))
+    cq.check(cq.lib.cq_memcpy_d2h(ks2.ctypes.data, pks, ks2.nbytes))
+    cq.check(cq.lib.cq_memcpy_d2h(vs2.ctypes.data, pvs, vs2.nbytes))
+    ko, vo = k_offsets(KV, T, hd, ms), v_offsets(KV, T, hd, ms)
+    np.testing.assert_array_equal(kc2[ko[:, T - 1]], Kq[:, T - 1])
+    np.testing.assert_array_equal(vc2[vo[:, T - 1]], Vq[:, T - 1])
+    np.testing.assert_array_equal(ks2[:, T - 1], Ks[:, T - 1])
+    np.testing.assert_array_equal(vs2[:, T - 1], Vs[:, T - 1])
+
+
+def test_state_kv8_fill_and_write_read():
+    """The int8 filler equals the oracle's (dequantized values bit-exact);
+    kv_write quantizes each row and kv_read returns half(q * s)."""
+    cfg = tiny_config(1)
+    w = cq.synth_weights(cfg, 1)
+    st = cq.State(cfg, w, kv_dtype=cq.KV_INT8)
+    om = orc.Model.synth(cfg, 1, cfg.max_seq_len)
+    om.set_kv8(True)
+    st.fill_kv(100, 77)
+    om.fill_kv(100, 77)
+    for layer in range(cfg.n_layers):
+        for h in range(cfg.n_kv_heads):
+            for kind in (0, 1):
+                np.testing.assert_array_equal(st.kv_read(layer, h, kind, 100).view(np.uint16),
+                                              om.kv(layer, h, kind, 100).view(np.uint16))
+    rows = (np.random.default_rng(2).standard_normal((40, cfg.head_dim)) * 3).astype(np.float16)
+    cq.check(cq.lib.cq_state_kv_write(st.handle, 1, 0, 1, 40, rows.view(np.uint16).ctypes.data))
+    q, s = orc.quant_rows_i8(rows)
+    want = (q.astype(np.float32) * s[:, None]).astype(np.float16)
+    np.testing.assert_array_equal(st.kv_read(1, 0, 1, 40).view(np.uint16), want.view(np.uint16))
+    st.free()
+    w.free()
+
+
+@pytest.mark.parametrize("quant", [0, 1, 2])
+def test_decode_kv8_tiny_matches_oracle(quant):
+    """Teacher-forced decode with an int8 cache against the oracle's int8
+    mode: logits within 1e-2, top-1 where the gap exceeds 1e-2, the cache
+    rows bit-exact."""
+    cfg = tiny_config(quant)
+    w = cq.synth_weights(cfg, 4)
+    om = orc.Model.synth(cfg, 4, cfg.max_seq_len)
+    om.set_kv8(True)
+    st = cq.State(cfg, w, kv_dtype=cq.KV_INT8)
+    tok, hist, checked = 5, [], 0
+    for pos in range(40):
+        ot = om.forward(tok, pos, hist)
+        gt = st.forward(tok, pos, hist)
+        ol = om.logits()
+        assert rel_err(st.logits(), ol) <= TOL, pos
+        if _gap(ol) > 1e-2:
+            assert gt == ot, pos
+            checked += 1
+        hist.append(ot)
+        tok = ot
+    assert checked >= 30
+    for layer in range(cfg.n_layers):
+        for h in range(cfg.n_kv_heads):
+            for kind in (0, 1):
+                assert rel_err(st.kv_read(layer, h, kind, 40), om.kv(layer, h, kind, 40)) <= TOL
+    st.free()
+    w.free()
+
+
+def test_decode_kv8_7b_int4_32k_matches_oracle():
+    """The bench workload's shapes (7B INT4, 28 layers, int8 lm_head) with an
+    int8 cache prefilled to just below 32768."""
+    cfg = cq.preset("7B", "int4")
+    n_ctx, steps = 32768 - 4, 4
+    w = cq.synth_weights(cfg, 0x5157454E)
+    om = orc.Model.synth(cfg, 0x5157454E, n_ctx + steps)
+    om.set_kv8(True)
+    om.fill_kv(n_ctx, 77)
+    st = cq.State(cfg, w, kv_dtype=cq.KV_INT8)
+    st.fill_kv(n_ctx, 77)
+    tok = int(cq.lib.cq_synth_uniform(44, 0, 0, cfg.vocab_size))
+    hist, checked = [], 0
+    for i in range(steps):
+        ot = om.forward(tok, n_ctx + i, hist)
+        gt = st.forward(tok, n_ctx + i, hist)
+        ol = om.logits()
+        assert rel_err(st.logits(), ol) <= TOL, i
+        if _gap(ol) > 1e-2:
+            assert gt == ot
+            checked += 1
+        hist.append(ot)
+        tok = ot
+    assert checked >= 3
+    st.free()
+    w.free()
+
+
+@pytest.mark.parametrize("quant,n", [(2, 70), (1, 600), (0, 17)])
+def test_prefill_kv8_matches_oracle(quant, n):
+    """Batched prefill into an int8 cache (GEMM epilogue quantization, both
+    the split-K and the single-pass epilogue) against the oracle's int8 mode
+    run token by token."""
+    cfg = tiny_config(quant, max_seq_len=1024)
+    w = cq.synth_weights(cfg, 6)
+    om = orc.Model.synth(cfg, 6, cfg.max_seq_len)
+    om.set_kv8(True)
+    st = cq.State(cfg, w, kv_dtype=cq.KV_INT8)
+    prompt = [int(cq.lib.cq_synth_uniform(8, 0, i, cfg.vocab_size)) for i in range(n)]
+    ot = None
+    for i, t in enumerate(prompt):
+        ot = om.forward(t, i, [])
+    gt = st.prefill(prompt, 0)
+    assert rel_err(st.logits(), om.logits()) <= TOL
+    if _gap(om.logits()) > 1e-2:
+        assert gt == ot
+    for layer in range(cfg.n_layers):
+        for h in range(cfg.n_kv_heads):
+            for kind in (0, 1):
+                assert rel_err(st.kv_read(layer, h, kind, n), om.kv(layer, h, kind, n)) <= TOL
+    st.free()
+    w.free()
+
+
+@pytest.mark.parametrize("model,quant,layers,n,n_ctx", [("7B", "int4", 2, 130, 2000), ("7B", "int4", 2, 2100, 0),
+                                                        ("0.5B", "int8", 4, 300, 0)])
+def test_prefill_kv8_matches_decode_kv8_real_shapes(model, quant, layers, n, n_ctx):
+    cfg = cq.preset(model, quant).replace(n_layers=layers)
+    w = cq.synth_weights(cfg, 0x5157454E)
+    prompt = [int(cq.lib.cq_synth_uniform(31, 0, i, cfg.vocab_size)) for i in range(n)]
+    ref = cq.State(cfg, w, kv_dtype=cq.KV_INT8)
+    st = cq.State(cfg, w, kv_dtype=cq.KV_INT8)
+    if n_ctx:
+        ref.fill_kv(n_ctx, 77)
+        st.fill_kv(n_ctx, 77)
+    rt = None
+    for i, t in enumerate(prompt):
+        rt = ref.forward(t, n_ctx + i, [])
+    gt = st.prefill(prompt, n_ctx)
+    assert rel_err(st.logits(), ref.logits()) <= TOL
+    if _gap(ref.logits()) > 1e-2:
+        assert gt == rt
+    for layer in (0, layers - 1):
+        for kind in (0, 1):
+            assert rel_err(st.kv_read(layer, 0, kind, n_ctx + n), ref.kv_read(layer, 0, kind, n_ctx + n)) <= TOL
+    st.free()
+    ref.free()
+    w.free()

@@ -216,6 +216,81 @@ def test_attention_partition_count_invariance():
         assert np.max(np.abs(o - outs[0])) < 5e-3
 
 
+# ------------------------------------------------------------ int8 KV
+def test_quant_row_i8_known_answers():
+    """s = max|x|/127; the largest element maps to +-127; half-even ties
+    (x/s = 2.5 -> 2, 3.5 -> 4); an all-zero row keeps s = 0."""
+    x = np.array([[127, 2.5, 3.5, -2.5, 0.25, 1],
+                  [-63.5, 1, 0, 0, 0, 0.5],
+                  [0, 0, 0, 0, 0, 0]], dtype=np.float16)
+    q, s = orc.quant_rows_i8(x)
+    assert s[0] == np.float32(1.0) and s[1] == np.float32(63.5) / np.float32(127) and s[2] == 0
+    assert list(q[0]) == [127, 2, 4, -2, 0, 1]
+    assert q[1][0] == -127 and q[1][1] == 2 and q[1][5] == 1
+    assert not q[2].any()
+
+
+def test_quant_row_i8_error_bound():
+    """|x - q s| <= s/2 for every element (round to nearest), s exact."""
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal((200, 128)) * rng.uniform(0.01, 30, (200, 1))).astype(np.float16)
+    q, s = orc.quant_rows_i8(x)
+    xf = x.astype(np.float64)
+    np.testing.assert_array_equal(s, (np.abs(x.astype(np.float32)).max(1) / np.float32(127)))
+    # (an fp32 tie x/s = k + 1/2 may sit a few ulps past the exact half)
+    assert np.all(np.abs(xf - q.astype(np.float64) * s[:, None]) <= s[:, None] / 2 * (1 + 1e-5))
+    assert np.all(np.abs(q).max(1) == 127)
+
+
+def _dequant(q, s):
+    return q.astype(np.float64) * s.astype(np.float64)[..., None]
+
+
+@pytest.mark.parametrize("T", [1, 2, 33, 300])
+def test_attention_i8_matches_textbook_on_dequantized_cache(T):
+    rng = np.random.default_rng(T + 5)
+    H, KV, hd = 14, 2, 64
+    q = rng.standard_normal(H * hd).astype(np.float16)
+    K = rng.standard_normal((KV, 320, hd)).astype(np.float16)
+    V = rng.standard_normal((KV, 320, hd)).astype(np.float16)
+    Kq, Ks = orc.quant_rows_i8(K.reshape(-1, hd))
+    Vq, Vs = orc.quant_rows_i8(V.reshape(-1, hd))
+    Kq, Vq, Ks, Vs = Kq.reshape(KV, 320, hd), Vq.reshape(KV, 320, hd), Ks.reshape(KV, 320), Vs.reshape(KV, 320)
+    want = _attn_np(q, _dequant(Kq, Ks), _dequant(Vq, Vs), H, KV, hd, T)
+    for mode in (0, 1):
+        got = orc.attention_i8(q, Kq, Ks, Vq, Vs, H, KV, hd, T, mode).astype(np.float64)
+        tol = 2e-3 if mode == 1 else 1e-2
+        assert np.max(np.abs(got - want)) <= tol * max(1.0, np.max(np.abs(want)))
+    if T == 1:   # one key: the output is the dequantized value row itself
+        one = orc.attention_i8(q, Kq, Ks, Vq, Vs, H, KV, hd, 1, 1).reshape(H, hd).astype(np.float64)
+        deq = _dequant(Vq[:, 0], Vs[:, 0])
+        assert np.allclose(one, np.repeat(deq, H // KV, axis=0), rtol=1e-3, atol=1e-3)
+
+
+def test_model_kv8_layer0_rows_are_quantized_fp16_rows():
+    """Layer 0's k / v depend only on the token and position, so the int8
+    model stores exactly the quantization of the fp16 model's rows; later
+    layers differ only through the attention, which stays within 1e-2."""
+    import cuqwen_amd as cq
+    from tests.conftest import tiny_config
+    cfg = tiny_config(2)
+    a = orc.Model.synth(cfg, 5, 64)
+    b = orc.Model.synth(cfg, 5, 64)
+    b.set_kv8(True)
+    toks = [3, 77, 1000, 5, 9, 2000, 31]
+    for i, t in enumerate(toks):
+        a.forward(t, i, [])
+        b.forward(t, i, [])
+        la, lb = a.logits().astype(np.float64), b.logits().astype(np.float64)
+        assert np.max(np.abs(la - lb)) <= 5e-2 * np.max(np.abs(la))
+    for kind in (0, 1):
+        for h in range(cfg.n_kv_heads):
+            q, s = b.kv8(0, h, kind, len(toks))
+            wq, ws = orc.quant_rows_i8(a.kv(0, h, kind, len(toks)))
+            np.testing.assert_array_equal(q, wq)
+            np.testing.assert_array_equal(s, ws)
+
+
 # ---------------------------------------------------------------- argmax
 def test_argmax_ties_lowest_index_and_specials():
     """kernels.cu:907-961: ties -> lowest index; NaN sorts above +inf."""
