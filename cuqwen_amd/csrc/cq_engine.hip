@@ -768,7 +768,7 @@ int prefill_batched(cq_state* s, const int32_t* tokens, int n, int pos0) {
       const size_t ls = (size_t)l * c.n_kv_heads * c.max_seq_len;
       float* ksc = kv8 ? s->kscale + ls : nullptr;
       float* vsc = kv8 ? s->vscale + ls : nullptr;
-      CQ_TRY(launch_pf_norm(s->pf_x, L.in_norm, c.norm_eps, M, d, s->pf_a, s->pf_inv, st));
+      CQ_TRY(launch_pf_norm(s->pf_x, L.in_norm, c.norm_eps, M, d, s->pf_a, s->pf_inv, c.quant_type, st));
       PfGemmArgs g;
       g.mode = GM_QKV; g.quant = c.quant_type; g.A = (const _Float16*)s->pf_a; g.inv = s->pf_inv;
       g.M = M; g.N = qd + 2 * kvd; g.K = d;
@@ -786,6 +786,7 @@ int prefill_batched(cq_state* s, const int32_t* tokens, int n, int pos0) {
       at.M = M; at.pos0 = pos0 + c0; at.n_heads = c.n_heads; at.n_kv = c.n_kv_heads; at.head_dim = c.head_dim;
       at.max_seq = c.max_seq_len;
       at.kcache8 = kc8; at.vcache8 = vc8; at.kscale = ksc; at.vscale = vsc;
+      at.int4_layout = c.quant_type == CQ_QUANT_INT4;
       CQ_TRY(launch_pf_attention(at, st));
       if (l == c.n_layers - 1) break;   // the last layer's residual stream feeds nothing here
       PfGemmArgs o;
@@ -793,7 +794,7 @@ int prefill_batched(cq_state* s, const int32_t* tokens, int n, int pos0) {
       o.W[0] = L.wo; o.S[0] = (const _Float16*)L.so; o.rows[0] = d; o.out = (_Float16*)s->pf_x;
       o.part = s->pf_part; o.part_bytes = kPrefillPartBytes;
       CQ_TRY(launch_pf_gemm(o, st));
-      CQ_TRY(launch_pf_norm(s->pf_x, L.post_norm, c.norm_eps, M, d, s->pf_a, s->pf_inv, st));
+      CQ_TRY(launch_pf_norm(s->pf_x, L.post_norm, c.norm_eps, M, d, s->pf_a, s->pf_inv, c.quant_type, st));
       PfGemmArgs m1;
       m1.mode = GM_SWIGLU; m1.quant = c.quant_type; m1.A = (const _Float16*)s->pf_a; m1.inv = s->pf_inv;
       m1.M = M; m1.N = I; m1.K = d; m1.W[0] = L.wg; m1.W[1] = L.wu;

@@ -77,7 +77,8 @@ int attention_max_parts(int n_kv);
 
 // ---------------------------------------------------------------- prefill
 // M-token GEMM on the matrix cores (cq_prefill.hip).  A: [M][K] activations
-// in the permuted 8-group layout; rows[]: rows of W[0..2] (QKV: q, k, v;
+// in the layout of the weights' format (int4: permuted 8-groups, odd
+// elements / 16; int8 / fp16: natural); rows[]: rows of W[0..2] (QKV: q, k, v;
 // otherwise rows[0] = N); out: RESID -> [M][N] residual (natural, in place),
 // SWIGLU -> [M][N] (permuted), QKV -> q [M][rows[0]] (natural) + KV cache.
 struct PfGemmArgs {
@@ -114,8 +115,9 @@ struct PfAttnArgs {
   const int8_t* vcache8 = nullptr;
   const float* kscale = nullptr;
   const float* vscale = nullptr;
+  bool int4_layout = false;   // out in the int4 GEMM input layout (else natural order)
 };
-int launch_pf_norm(const __half* x, const __half* w, float eps, int M, int dim, __half* A, float* inv,
+int launch_pf_norm(const __half* x, const __half* w, float eps, int M, int dim, __half* A, float* inv, int quant,
                    hipStream_t stream);
 int launch_pf_embed(const __half* embed, const int* tokens, int M, int dim, __half* x, hipStream_t stream);
 int launch_pf_gemm(const PfGemmArgs& a, hipStream_t stream);

@@ -27,6 +27,7 @@
 #include "cq_gemv.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace cq {
 
@@ -39,17 +40,25 @@ constexpr int kPfLdsStride = kPfK + 8;     // halves per token row in LDS (16-by
 constexpr int kPfTargetBlocks = 512;       // split K below this many blocks (2 per CU)
 constexpr int kPfMaxSplit = 8;
 
-// position of element k in the permuted activation layout
-__device__ __forceinline__ int pf_pos(int k) {
+// Activation layout of the GEMM inputs, chosen by the weights' format so the
+// A operand needs no shuffle: int4 stores each 8-group in the order
+// [0,4,1,5,2,6,3,7] with the odd elements divided by 16 (the unpack yields the
+// odd nibbles as 16 n without a shift); int8 and fp16 keep natural order.
+__device__ __forceinline__ int pf_pos(int k, bool int4) {
+  if (!int4) return k;
   const int e = k & 7;
   return (k & ~7) | (e < 4 ? 2 * e : 2 * e - 7);
+}
+// value stored for element k (exact: a power-of-two scale)
+__device__ __forceinline__ _Float16 pf_val(float v, int k, bool int4) {
+  return (_Float16)((int4 && (k & 1)) ? v * 0.0625f : v);
 }
 
 // ------------------------------------------------------------- row norm
 // One block per token row: A[m] = half(x * w) (permuted), inv[m] =
 // rsqrt(mean(x^2) + half(eps)).  Without w, A = x (permuted) and no inv.
 __global__ __launch_bounds__(256) void pf_norm_rows(const _Float16* x, const _Float16* w, float eps, int dim,
-                                                    _Float16* A, float* inv) {
+                                                    _Float16* A, float* inv, bool int4) {
   __shared__ float red[16];
   const int m = blockIdx.x;
   const _Float16* xr = x + (int64_t)m * dim;
@@ -58,7 +67,9 @@ __global__ __launch_bounds__(256) void pf_norm_rows(const _Float16* x, const _Fl
   for (int k = threadIdx.x; k < dim; k += blockDim.x) {
     const float v = (float)xr[k];
     ss = fmaf(v, v, ss);
-    ar[pf_pos(k)] = w ? (_Float16)(v * (float)w[k]) : xr[k];
+    // half(x * w) first (the decode GEMVs' staging), then the layout's scale
+    const float y = w ? (float)(_Float16)(v * (float)w[k]) : v;
+    ar[pf_pos(k, int4)] = pf_val(y, k, int4);
   }
   if (w) {
     ss = block_sum(ss, red);
@@ -82,30 +93,28 @@ template <> struct PfW<CQ_QUANT_FP16> { static constexpr int LOADS = 4; };
 // The A operand (8 fp16 weights in the order [0,4,1,5,2,6,3,7] of true k
 // j*32 + s*8 + e) for sub-step s from the lane's loaded bytes.
 template <int Q>
-__device__ __forceinline__ h8_t pf_unpack(const u4_t* w, int s) {
+__device__ __forceinline__ h8_t pf_unpack(const u4_t* w, int s, uint32_t m_lo, uint32_t m_hi, uint32_t magic) {
   u4_t o;
   if constexpr (Q == CQ_QUANT_INT4) {
-    const uint32_t f = w[0][s] ^ kInt4Flip;   // nibble = q + 8
-    const h2_t bias = {(_Float16)-1032.f, (_Float16)-1032.f};
-    o.x = as_u32(as_h2((f & 0x000F000Fu) | 0x64006400u) + bias);
-    o.y = as_u32(as_h2(((f >> 4) & 0x000F000Fu) | 0x64006400u) + bias);
-    o.z = as_u32(as_h2(((f >> 8) & 0x000F000Fu) | 0x64006400u) + bias);
-    o.w = as_u32(as_h2(((f >> 12) & 0x000F000Fu) | 0x64006400u) + bias);
+    // word s: nibbles e0..e7 of true k j*32 + s*8 + e; after ^0x88888888 each
+    // is n = q + 8.  (1024 + n) - 1032 = q for e0 e4 e2 e6; the odd nibbles
+    // stay in place: (1024 + 16 n) - 1152 = 16 q against activations / 16.
+    const uint32_t f = w[0][s] ^ kInt4Flip, f8 = f >> 8;
+    const h2_t blo = {(_Float16)-1032.f, (_Float16)-1032.f}, bhi = {(_Float16)-1152.f, (_Float16)-1152.f};
+    o.x = as_u32(as_h2(and_or(f, m_lo, 0x64006400u)) + blo);    // (e0, e4)
+    o.y = as_u32(as_h2(and_or(f, m_hi, 0x64006400u)) + bhi);    // (16 e1, 16 e5)
+    o.z = as_u32(as_h2(and_or(f8, m_lo, 0x64006400u)) + blo);   // (e2, e6)
+    o.w = as_u32(as_h2(and_or(f8, m_hi, 0x64006400u)) + bhi);   // (16 e3, 16 e7)
   } else if constexpr (Q == CQ_QUANT_INT8) {
-    // bytes 8s..8s+7 of the lane's 32: words w0 (b0..b3), w1 (b4..b7)
-    const uint32_t w0 = w[s >> 1][(s & 1) * 2] ^ kInt8Flip, w1 = w[s >> 1][(s & 1) * 2 + 1] ^ kInt8Flip;
-    const h2_t bias = {(_Float16)-1152.f, (_Float16)-1152.f};
-    // (byte i of w0, 0, byte i of w1, 0) | 0x6400 6400 = (1024 + u0, 1024 + u4)
-    o.x = as_u32(as_h2(__builtin_amdgcn_perm(w1, w0, 0x0c040c00u) | 0x64006400u) + bias);
-    o.y = as_u32(as_h2(__builtin_amdgcn_perm(w1, w0, 0x0c050c01u) | 0x64006400u) + bias);
-    o.z = as_u32(as_h2(__builtin_amdgcn_perm(w1, w0, 0x0c060c02u) | 0x64006400u) + bias);
-    o.w = as_u32(as_h2(__builtin_amdgcn_perm(w1, w0, 0x0c070c03u) | 0x64006400u) + bias);
+    // bytes 8s..8s+7 in natural order: (1152 + q) pairs, minus 1152
+    const uint32_t f0 = w[s >> 1][(s & 1) * 2] ^ kInt8Flip, f1 = w[s >> 1][(s & 1) * 2 + 1] ^ kInt8Flip;
+    const h2_t b = {(_Float16)-kInt8Bias, (_Float16)-kInt8Bias};
+    o.x = as_u32(as_h2(int8_pair(f0, magic, 0)) + b);
+    o.y = as_u32(as_h2(int8_pair(f0, magic, 1)) + b);
+    o.z = as_u32(as_h2(int8_pair(f1, magic, 0)) + b);
+    o.w = as_u32(as_h2(int8_pair(f1, magic, 1)) + b);
   } else {
-    const u4_t h = w[s];   // halves e0..e7 in words (e0,e1) (e2,e3) (e4,e5) (e6,e7)
-    o.x = __builtin_amdgcn_perm(h.z, h.x, 0x05040100u);   // (e0, e4)
-    o.y = __builtin_amdgcn_perm(h.z, h.x, 0x07060302u);   // (e1, e5)
-    o.z = __builtin_amdgcn_perm(h.w, h.y, 0x05040100u);   // (e2, e6)
-    o.w = __builtin_amdgcn_perm(h.w, h.y, 0x07060302u);   // (e3, e7)
+    o = w[s];   // fp16, natural order
   }
   return __builtin_bit_cast(h8_t, o);
 }
@@ -226,25 +235,28 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm_kernel(const PfGemmArgs a)
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt) acc[mt][rt][tt] = f4_t{0.f, 0.f, 0.f, 0.f};
 
-  u4_t xv[4], wv[NMAT][RT][L];
-  x_load(kb, xv);
-#pragma unroll
-  for (int mt = 0; mt < NMAT; ++mt)
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt) pf_load_w<Q>(a, rowp[mt][rt], kb, j, wv[mt][rt]);
-  x_store(0, xv);
-  __syncthreads();
-
-  for (int ks = kb; ks < ke; ++ks) {
-    const int buf = (ks - kb) & 1;
-    // next step's activations and weights in flight during this step's MMAs
-    u4_t wn[NMAT][RT][L];
-    const int kn = min(ks + 1, ke - 1);
-    x_load(kn, xv);
+  // Two-step-ahead pipeline, unrolled by two so both register sets keep
+  // compile-time indices: at step k the weights of step k+2 are requested
+  // right after step k's weights are unpacked, the activations of step k+2
+  // at the start of step k (stored into LDS at the end of step k+1).
+  u4_t xv[2][4], wv[2][NMAT][RT][L];
+  auto load_w_step = [&](int ks, u4_t (&w)[NMAT][RT][L]) {
 #pragma unroll
     for (int mt = 0; mt < NMAT; ++mt)
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt) pf_load_w<Q>(a, rowp[mt][rt], kn, j, wn[mt][rt]);
+      for (int rt = 0; rt < RT; ++rt) pf_load_w<Q>(a, rowp[mt][rt], ks, j, w[mt][rt]);
+  };
+  x_load(kb, xv[0]);
+  x_load(min(kb + 1, ke - 1), xv[1]);
+  load_w_step(kb, wv[0]);
+  load_w_step(min(kb + 1, ke - 1), wv[1]);
+  x_store(0, xv[0]);
+  __syncthreads();
+
+  const UnpackRegs uk = unpack_regs();
+  auto step = [&](auto I, int ks) {
+    constexpr int S = decltype(I)::value;   // register set and LDS buffer of this step
+    x_load(min(ks + 2, ke - 1), xv[S]);
     _Float16 sc[NMAT][RT][4];
     if constexpr (Q != CQ_QUANT_FP16) {
 #pragma unroll
@@ -254,7 +266,14 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm_kernel(const PfGemmArgs a)
 #pragma unroll
           for (int v = 0; v < 4; ++v) sc[mt][rt][v] = srow[mt][rt][v][ks];
     }
-
+    h8_t wa[NMAT][RT][4];
+#pragma unroll
+    for (int mt = 0; mt < NMAT; ++mt)
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) wa[mt][rt][s4] = pf_unpack<Q>(wv[S][mt][rt], s4, uk.m_lo, uk.m_hi, uk.magic);
+    load_w_step(min(ks + 2, ke - 1), wv[S]);
     f4_t part[NMAT][RT][4];
 #pragma unroll
     for (int mt = 0; mt < NMAT; ++mt)
@@ -264,20 +283,18 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm_kernel(const PfGemmArgs a)
         for (int tt = 0; tt < 4; ++tt)
           part[mt][rt][tt] = Q == CQ_QUANT_FP16 ? acc[mt][rt][tt] : f4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
+    for (int s4 = 0; s4 < 4; ++s4) {
       h8_t xb[4];
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt)
-        xb[tt] = *reinterpret_cast<const h8_t*>(&xs[buf][(tt * 16 + r) * kPfLdsStride + j * 32 + s * 8]);
+        xb[tt] = *reinterpret_cast<const h8_t*>(&xs[S][(tt * 16 + r) * kPfLdsStride + j * 32 + s4 * 8]);
 #pragma unroll
       for (int mt = 0; mt < NMAT; ++mt)
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) {
-          const h8_t wa = pf_unpack<Q>(wv[mt][rt], s);
+        for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
           for (int tt = 0; tt < 4; ++tt)
-            part[mt][rt][tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, xb[tt], part[mt][rt][tt], 0, 0, 0);
-        }
+            part[mt][rt][tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[mt][rt][s4], xb[tt], part[mt][rt][tt], 0, 0, 0);
     }
 #pragma unroll
     for (int mt = 0; mt < NMAT; ++mt)
@@ -292,14 +309,13 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm_kernel(const PfGemmArgs a)
             for (int v = 0; v < 4; ++v) acc[mt][rt][tt][v] = fmaf((float)sc[mt][rt][v], part[mt][rt][tt][v], acc[mt][rt][tt][v]);
           }
         }
-#pragma unroll
-    for (int mt = 0; mt < NMAT; ++mt)
-#pragma unroll
-      for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-        for (int i = 0; i < L; ++i) wv[mt][rt][i] = wn[mt][rt][i];
-    if (ks + 1 < ke) x_store(buf ^ 1, xv);
+    // the activations of step ks+1 (requested one step ago) into the other buffer
+    if (ks + 1 < ke) x_store(S ^ 1, xv[S ^ 1]);
     __syncthreads();
+  };
+  for (int ks = kb; ks < ke; ks += 2) {
+    step(std::integral_constant<int, 0>{}, ks);
+    if (ks + 1 < ke) step(std::integral_constant<int, 1>{}, ks + 1);
   }
 
   if constexpr (SPLIT) {
@@ -344,7 +360,7 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm_kernel(const PfGemmArgs a)
           const float s = a.inv[m];
           const float g = acc[0][0][tt][v] * s, u = acc[1][0][tt][v] * s;
           const float sig = 1.f / (1.f + expf(-g));   // kernels.cu:566
-          a.out[(int64_t)m * a.N + pf_pos(n)] = (_Float16)((g * sig) * u);
+          a.out[(int64_t)m * a.N + pf_pos(n, Q == CQ_QUANT_INT4)] = pf_val((float)(_Float16)((g * sig) * u), n, Q == CQ_QUANT_INT4);
         }
       }
   } else {
@@ -462,7 +478,8 @@ __global__ __launch_bounds__(256) void pf_split_epilogue(const PfGemmArgs a, int
       } else {
         const float g = sum(0, m, n) * a.inv[m], u = sum(1, m, n) * a.inv[m];
         const float sig = 1.f / (1.f + expf(-g));
-        a.out[(int64_t)m * a.N + pf_pos(n)] = (_Float16)((g * sig) * u);
+        a.out[(int64_t)m * a.N + pf_pos(n, a.quant == CQ_QUANT_INT4)] =
+            pf_val((float)(_Float16)((g * sig) * u), n, a.quant == CQ_QUANT_INT4);
       }
     }
   }
@@ -602,15 +619,17 @@ __global__ __launch_bounds__(kAttnThreads) void pf_attention_kernel(const PfAttn
       L += wl[w][c] * f;
       O += wo[w][c][d] * f;
     }
-    a.out[(int64_t)(t0 + c) * qd + pf_pos(hq * HD + d)] = (_Float16)(O * (1.0f / (L + 1e-9f)));
+    const int k = hq * HD + d;
+    a.out[(int64_t)(t0 + c) * qd + pf_pos(k, a.int4_layout)] =
+        pf_val((float)(_Float16)(O * (1.0f / (L + 1e-9f))), k, a.int4_layout);
   }
 }
 
 // ------------------------------------------------------------------ host
 int launch_pf_norm(const __half* x, const __half* w, float eps, int M, int dim, __half* A, float* inv,
-                   hipStream_t stream) {
+                   int quant, hipStream_t stream) {
   hipLaunchKernelGGL(pf_norm_rows, dim3(M), dim3(256), 0, stream, (const _Float16*)x, (const _Float16*)w, eps, dim,
-                     (_Float16*)A, inv);
+                     (_Float16*)A, inv, quant == CQ_QUANT_INT4);
   CQ_HIP(hipGetLastError());
   return CQ_OK;
 }
