@@ -85,7 +85,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_stage1(const AttnArgs 
 }
 
 // Stage 1 over the int8 cache.  The wave whose tiles include the step's new
-// position first quantizes the new k / v rows of its kv head (one row per
+// position quantizes the new k / v rows of its kv head (one row per
 // wave reduction), writes them and their scales into the cache for later
 // steps, and patches them into its loaded tile: no other wave of the launch
 // reads that position, so no block synchronisation is needed.
@@ -109,7 +109,25 @@ __global__ __launch_bounds__(kAttnThreads) void attention_stage1_kv8(const AttnA
   const float* ksc = a.kscale + (int64_t)kvh * a.max_seq;
   const float* vsc = a.vscale + (int64_t)kvh * a.max_seq;
 
-  // the new row (position pos) belongs to tile n_tiles - 1 of the last partition
+  KVTile8<HD> A, B;
+  int ti = tile0 + wave;
+  if (ti < tile1) load_tile8<HD>(A, kbase, vbase, ksc, vsc, ti, lane);
+  h8_t qb[KK];
+  {
+    const _Float16* q = reinterpret_cast<const _Float16*>(a.q) + (int64_t)(kvh * g + h) * HD;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      if (h < g) qb[kk] = __builtin_bit_cast(h8_t, load_u4(q + kk * 32 + j * 8));
+      else qb[kk] = h8_t{0, 0, 0, 0, 0, 0, 0, 0};
+    }
+  }
+  // q goes out before the second tile: loads return in issue order, so the
+  // first tile's scores wait only for the first tile and q
+  if (ti + kAttnWaves < tile1) load_tile8<HD>(B, kbase, vbase, ksc, vsc, ti + kAttnWaves, lane);
+  // the new row (position pos) belongs to tile n_tiles - 1 of the last partition;
+  // its owner quantizes it while its first tiles are in flight (the loaded
+  // tile's copy of that position is replaced by the patch, so whether the
+  // load sees the old or the new bytes does not matter)
   __shared__ __align__(16) int8_t newq[2][HD];
   __shared__ float news[2];
   const int last = n_tiles - 1;
@@ -138,32 +156,22 @@ __global__ __launch_bounds__(kAttnThreads) void attention_stage1_kv8(const AttnA
     __builtin_amdgcn_wave_barrier();
   }
 
-  KVTile8<HD> A, B;
-  int ti = tile0 + wave;
-  if (ti < tile1) load_tile8<HD>(A, kbase, vbase, ksc, vsc, ti, lane);
-  h8_t qb[KK];
-  {
-    const _Float16* q = reinterpret_cast<const _Float16*>(a.q) + (int64_t)(kvh * g + h) * HD;
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk) {
-      if (h < g) qb[kk] = __builtin_bit_cast(h8_t, load_u4(q + kk * 32 + j * 8));
-      else qb[kk] = h8_t{0, 0, 0, 0, 0, 0, 0, 0};
-    }
-  }
   float m = -INFINITY, l = 0.f;
   f4_t o[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) o[dt] = f4_t{0.f, 0.f, 0.f, 0.f};
   const int kp = pos & (kTileKeys - 1);
+  // A and B each hold (or have in flight) one tile; a buffer is refilled as
+  // soon as its tile has been computed
   for (; ti < tile1; ti += 2 * kAttnWaves) {
     const int t1 = ti + kAttnWaves;
-    if (t1 < tile1) load_tile8<HD>(B, kbase, vbase, ksc, vsc, t1, lane);
     if (owns_new && ti == last) patch_key8<HD>(A, kp, newq[0], newq[1], news[0], news[1], lane);
     attend_tile8<HD>(A, qb, ti, T, scale, j, m, l, o, magic);
-    if (t1 >= tile1) break;
     if (t1 + kAttnWaves < tile1) load_tile8<HD>(A, kbase, vbase, ksc, vsc, t1 + kAttnWaves, lane);
+    if (t1 >= tile1) break;
     if (owns_new && t1 == last) patch_key8<HD>(B, kp, newq[0], newq[1], news[0], news[1], lane);
     attend_tile8<HD>(B, qb, t1, T, scale, j, m, l, o, magic);
+    if (t1 + 2 * kAttnWaves < tile1) load_tile8<HD>(B, kbase, vbase, ksc, vsc, t1 + 2 * kAttnWaves, lane);
   }
   l += __shfl_xor(l, 16, kWave);
   l += __shfl_xor(l, 32, kWave);

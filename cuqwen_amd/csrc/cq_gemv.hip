@@ -260,15 +260,25 @@ static int launch_q(const GemvArgs& a, hipStream_t stream) {
   const bool norm = a.norm_w != nullptr;
   if constexpr (MODE == GM_STORE) {
     // Short matrices (e.g. the 896-row down-projection shape of BASELINE
-    // config 1) need more, smaller blocks than the 150K-row lm_head.
+    // config 1) need more, smaller blocks than the 150K-row lm_head, and one
+    // row per wave in few, wide steps (measured at K=4864 N=896 W8: R=1 U=3
+    // 4.13 us per launch, R=2 U=2 4.92, R=1 U=5 4.21).
     if (a.N < 16384 && !norm) {
-      if (a.group == 0) return launch_variant<Q, MODE, 2, 2, false, false, 256>(a, stream, 4 * kNumCUs);
-      return launch_variant<Q, MODE, 2, 2, false, true, 256>(a, stream, 4 * kNumCUs);
+      if (a.group == 0) return launch_variant<Q, MODE, 1, 3, false, false, 256>(a, stream, 4 * kNumCUs);
+      return launch_variant<Q, MODE, 1, 3, false, true, 256>(a, stream, 4 * kNumCUs);
     }
     if (a.group == 0) return norm ? launch_t<Q, MODE, true, false>(a, stream) : launch_t<Q, MODE, false, false>(a, stream);
     return norm ? launch_t<Q, MODE, true, true>(a, stream) : launch_t<Q, MODE, false, true>(a, stream);
   } else if constexpr (MODE == GM_RESID) {
     if (norm) return fail(CQ_EINVAL, "gemv: residual mode takes no norm");
+    // Few rows (the 0.5B / 1.5B projections, N < 2048): 1024-thread blocks
+    // would leave most CUs idle (896 rows = 56 blocks); 512-thread blocks,
+    // two per CU (measured decode step 0.5B INT8 666 -> 640 us, 1.5B INT4
+    // 965 -> 931 us; the 3584-row 7B shapes are faster with the fat blocks).
+    if (a.N < 2048) {
+      if (a.K / QTraits<Q>::EPC <= 2 * kWave) return launch_variant<Q, MODE, 1, 1, false, true, 512>(a, stream, 2 * kNumCUs);
+      return launch_variant<Q, MODE, 1, 2, false, true, 512>(a, stream, 2 * kNumCUs);
+    }
     // short rows (at most two 64-chunk steps, e.g. the 7B o_proj) stream
     // faster one chunk per lane per step; long rows (down) two
     if (a.K / QTraits<Q>::EPC <= 2 * kWave) {
