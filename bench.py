@@ -35,7 +35,7 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-profile", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
-    ap.add_argument("--no-kv8", action="store_true", help="skip the int8 KV cache leg")
+    ap.add_argument("--no-kv8", action="store_true", help="skip the int8 and fp8 KV cache legs")
     ap.add_argument("--prompt", type=int, default=1024, help="prompt tokens of the batched-prefill measurement")
     ap.add_argument("--configs", action="store_true",
                     help="also measure decode (and prefill) at every BASELINE config (adds about a minute)")
@@ -120,10 +120,10 @@ def prefill_leg(cq, cfg, st, n):
                          "frac": round(tflops / 2500.0, 4)}}
 
 
-def kv8_leg(cq, cfg, w, pos0, args):
-    """The same decode workload with the int8 KV cache (CQ_KV_INT8): tok/s
-    and whole-step bytes (the K/V stream halves)."""
-    st = cq.State(cfg, w, kv_dtype=cq.KV_INT8)
+def kv8_leg(cq, cfg, w, pos0, args, fmt):
+    """The same decode workload with a quantized KV cache (CQ_KV_INT8 or
+    CQ_KV_FP8): tok/s and whole-step bytes (the K/V stream halves)."""
+    st = cq.State(cfg, w, kv_dtype=fmt)
     st.fill_kv(pos0, 77)
     tok = int(cq.lib.cq_synth_uniform(42, 0, 0, cfg.vocab_size))
     warm = st.decode(tok, pos0, args.warmup)
@@ -280,10 +280,12 @@ def main():
         pf = prefill_leg(cq, cfg, st, args.prompt)
         log(f"[bench] prefill: {pf}")
     st.free()
-    kv8 = None
+    kv8 = kvf8 = None
     if not args.no_kv8:
-        kv8 = kv8_leg(cq, cfg, w, pos0, args)
+        kv8 = kv8_leg(cq, cfg, w, pos0, args, cq.KV_INT8)
         log(f"[bench] int8 KV cache: {kv8}")
+        kvf8 = kv8_leg(cq, cfg, w, pos0, args, cq.KV_FP8)
+        log(f"[bench] fp8 (E4M3) KV cache: {kvf8}")
     w.free()
     if args.calib_copy:
         n = 256 << 20
@@ -313,7 +315,7 @@ def main():
                    "model": f"Qwen2.5-{args.model}", "global_batch": 1, "seq_len": args.ctx,
                    "parallelism": "single-gpu"},
         "device_ms_per_step": round(dev_us / 1e3, 5),
-        "roofline": roof, "cpu_baseline": cpu, "kernels": kernels, "gemv_config1": g1, "prefill": pf, "kv_int8": kv8,
+        "roofline": roof, "cpu_baseline": cpu, "kernels": kernels, "gemv_config1": g1, "prefill": pf, "kv_int8": kv8, "kv_fp8": kvf8,
         "configs": legs,
     }
     print(json.dumps(res), flush=True)

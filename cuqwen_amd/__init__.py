@@ -130,6 +130,7 @@ def _load():
         "cq_gqa_attention_decode": (I32, [P, P, P, P, P, I32, I32, I32, I32, P, P]),
         "cq_attention_workspace_bytes": (SZ, [I32, I32, I32]),
         "cq_gqa_attention_decode_kv8": (I32, [P, P, P, P, P, P, P, P, P, I32, I32, I32, I32, P, P]),
+        "cq_gqa_attention_decode_fp8": (I32, [P, P, P, P, P, P, P, P, P, I32, I32, I32, I32, P, P]),
         "cq_dequantize": (I32, [I32, I32, P, P, P, I32, I32, P]),
         "cq_time_gemv": (I32, [I32, I32, I32, ctypes.POINTER(P), ctypes.POINTER(P), P, P, I32, I32, I32,
                                ctypes.POINTER(ctypes.c_double)]),
@@ -149,6 +150,7 @@ EXPORTED = [
     "cq_synth_weights", "cq_free_weights", "cq_weights_tensor", "cq_state_create", "cq_state_destroy",
     "cq_forward", "cq_decode", "cq_state_logits", "cq_state_fill_kv", "cq_state_kv_read", "cq_state_kv_write",
     "cq_prefill", "cq_state_last_prefill_us", "cq_state_create_kv", "cq_gqa_attention_decode_kv8",
+    "cq_gqa_attention_decode_fp8",
     "cq_state_last_decode_us", "cq_synth_normal", "cq_synth_uniform", "cq_tensor_stream_id", "cq_kv_stream_id",
     "cq_quantize", "cq_device_count", "cq_malloc", "cq_free", "cq_memcpy_h2d", "cq_memcpy_d2h", "cq_memset", "cq_memcpy_d2d",
     "cq_synchronize", "cq_embedding_lookup", "cq_rmsnorm", "cq_gemv", "cq_gemv_add", "cq_fused_attn_block",
@@ -165,7 +167,7 @@ def check(rc):
     return rc
 
 
-KV_FP16, KV_INT8 = 0, 1
+KV_FP16, KV_INT8, KV_FP8 = 0, 1, 2
 
 
 def preset(model, quant="int8"):
@@ -311,7 +313,7 @@ class State:
     """Decode state (QwenState, include/model.cuh:9-46)."""
 
     def __init__(self, cfg, weights, kv_dtype=0):
-        """kv_dtype: KV_FP16 (the reference's cache) or KV_INT8."""
+        """kv_dtype: KV_FP16 (the reference's cache), KV_INT8 or KV_FP8 (E4M3)."""
         self.cfg = cfg
         self.weights = weights
         self.kv_dtype = kv_dtype

@@ -169,7 +169,8 @@ __device__ __forceinline__ void block_merge_write(const AttnArgs& a, int kvh, in
   }
 }
 
-// ------------------------------------------------------------ int8 KV cache
+// ------------------------------------------------------- quantized KV cache
+// One byte per element, int8 (CQ_KV_INT8) or OCP E4M3 (CQ_KV_FP8) codes.
 // Same element layout as the fp16 cache (kv_k_offset / kv_v_offset count
 // bytes instead of halves), so a lane's 8 elements of a matrix-core operand
 // are 8 contiguous bytes; per-(position, kv head) fp32 scales live in
@@ -220,12 +221,40 @@ __device__ __forceinline__ h8_t i8x8_to_h8(u2_t w, uint32_t magic_v) {
   return __builtin_bit_cast(h8_t, o);
 }
 
+// 8 E4M3 codes (natural order) -> 8 exact fp16 with the gfx950 converter
+// (every E4M3 value is an fp16 value; the scale operand 1.0 leaves them).
+__device__ __forceinline__ h8_t f8x8_to_h8(u2_t w) {
+  u4_t o;
+  o.x = as_u32(__builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w.x, 1.0f, false));
+  o.y = as_u32(__builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w.x, 1.0f, true));
+  o.z = as_u32(__builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w.y, 1.0f, false));
+  o.w = as_u32(__builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w.y, 1.0f, true));
+  return __builtin_bit_cast(h8_t, o);
+}
+
+// 8 codes of a quantized cache in format F (CQ_KV_INT8 / CQ_KV_FP8) as fp16.
+template <int F>
+__device__ __forceinline__ h8_t codes_to_h8(u2_t w, uint32_t magic_v) {
+  if constexpr (F == CQ_KV_FP8) return f8x8_to_h8(w);
+  else return i8x8_to_h8(w, magic_v);
+}
+
+// Largest code magnitude of a format (s = max|x| / it) and the code of one
+// scaled element v = x / s: int8 rint clamped to +-127, E4M3 round to
+// nearest even.
+template <int F> __device__ __forceinline__ constexpr float kv_code_max() { return F == CQ_KV_FP8 ? 448.f : 127.f; }
+template <int F>
+__device__ __forceinline__ int8_t kv_encode(float v) {
+  if constexpr (F == CQ_KV_FP8) return (int8_t)e4m3_bits(v);
+  else return (int8_t)fminf(127.f, fmaxf(-127.f, rintf(v)));
+}
+
 // One 32-key tile of the online softmax over the int8 cache.  Keys at or past
 // t_lane (this lane's column limit) are masked; P of masked keys is exactly 0
 // (int8 data is always finite, stale scales are selected out).  Rounding as
 // the fp16 path: score = half(s * k_scale * 1/sqrt(hd)), P = half(p *
 // v_scale) for the product, the row sum over the unrounded p.
-template <int HD>
+template <int HD, int F = CQ_KV_INT8>
 __device__ __forceinline__ void attend_tile8(KVTile8<HD>& t, const h8_t* qb, int ti, int t_lane, float scale, int j,
                                              float& m, float& l, f4_t* o, uint32_t magic_v) {
   constexpr int KK = HD / 32, DT = HD / 16;
@@ -235,7 +264,7 @@ __device__ __forceinline__ void attend_tile8(KVTile8<HD>& t, const h8_t* qb, int
     s[st] = f4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk)
-      s[st] = __builtin_amdgcn_mfma_f32_16x16x32_f16(i8x8_to_h8(t.ka[st][kk], magic_v), qb[kk], s[st], 0, 0, 0);
+      s[st] = __builtin_amdgcn_mfma_f32_16x16x32_f16(codes_to_h8<F>(t.ka[st][kk], magic_v), qb[kk], s[st], 0, 0, 0);
   }
   const int key0 = ti * kTileKeys + 4 * j;
   float sv[8];
@@ -266,22 +295,23 @@ __device__ __forceinline__ void attend_tile8(KVTile8<HD>& t, const h8_t* qb, int
   }
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt)
-    o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(i8x8_to_h8(t.va[dt], magic_v), pb, o[dt], 0, 0, 0);
+    o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(codes_to_h8<F>(t.va[dt], magic_v), pb, o[dt], 0, 0, 0);
 }
 
-// Per-row int8 quantization (s = max|x| / 127, q = rint(x / s) clamped to
-// +-127, a zero row keeps s = 0) of the HD-element row x held by one wave
-// (HD / 64 consecutive elements per lane); returns s, writes q[0..HD/64).
-template <int HD>
+// Per-row quantization in format F (s = max|x| / code max, q = code of
+// x / s, a zero row keeps s = 0 and q = 0) of the HD-element row x held by
+// one wave (HD / 64 consecutive elements per lane); returns s, writes
+// q[0..HD/64).
+template <int HD, int F>
 __device__ __forceinline__ float quant_row8_wave(const float* x, int8_t* q) {
   constexpr int E = HD / kWave;
   float amax = 0.f;
 #pragma unroll
   for (int i = 0; i < E; ++i) amax = fmaxf(amax, fabsf(x[i]));
   amax = wave_max(amax);
-  const float s = amax / 127.0f;
+  const float s = amax / kv_code_max<F>();
 #pragma unroll
-  for (int i = 0; i < E; ++i) q[i] = s == 0.f ? (int8_t)0 : (int8_t)fminf(127.f, fmaxf(-127.f, rintf(x[i] / s)));
+  for (int i = 0; i < E; ++i) q[i] = s == 0.f ? (int8_t)0 : kv_encode<F>(x[i] / s);
   return s;
 }
 

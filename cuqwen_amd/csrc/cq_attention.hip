@@ -84,12 +84,12 @@ __global__ __launch_bounds__(kAttnThreads) void attention_stage1(const AttnArgs 
   block_merge_write<HD>(a, kvh, part, nparts, g, m, l, o);
 }
 
-// Stage 1 over the int8 cache.  The wave whose tiles include the step's new
+// Stage 1 over a quantized cache (format F: int8 or E4M3 codes).  The wave whose tiles include the step's new
 // position quantizes the new k / v rows of its kv head (one row per
 // wave reduction), writes them and their scales into the cache for later
 // steps, and patches them into its loaded tile: no other wave of the launch
 // reads that position, so no block synchronisation is needed.
-template <int HD>
+template <int HD, int F>
 __global__ __launch_bounds__(kAttnThreads) void attention_stage1_kv8(const AttnArgs a) {
   constexpr int KK = HD / 32, DT = HD / 16, E = HD / kWave;
   const int kvh = blockIdx.y, part = blockIdx.x;
@@ -140,7 +140,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_stage1_kv8(const AttnA
       int8_t qv[E];
 #pragma unroll
       for (int i = 0; i < E; ++i) x[i] = (float)src[i];
-      const float sc = quant_row8_wave<HD>(x, qv);
+      const float sc = quant_row8_wave<HD, F>(x, qv);
       int8_t* cache = kind ? a.vcache8 : a.kcache8;
 #pragma unroll
       for (int i = 0; i < E; ++i) {
@@ -166,11 +166,11 @@ __global__ __launch_bounds__(kAttnThreads) void attention_stage1_kv8(const AttnA
   for (; ti < tile1; ti += 2 * kAttnWaves) {
     const int t1 = ti + kAttnWaves;
     if (owns_new && ti == last) patch_key8<HD>(A, kp, newq[0], newq[1], news[0], news[1], lane);
-    attend_tile8<HD>(A, qb, ti, T, scale, j, m, l, o, magic);
+    attend_tile8<HD, F>(A, qb, ti, T, scale, j, m, l, o, magic);
     if (t1 + kAttnWaves < tile1) load_tile8<HD>(A, kbase, vbase, ksc, vsc, t1 + kAttnWaves, lane);
     if (t1 >= tile1) break;
     if (owns_new && t1 == last) patch_key8<HD>(B, kp, newq[0], newq[1], news[0], news[1], lane);
-    attend_tile8<HD>(B, qb, t1, T, scale, j, m, l, o, magic);
+    attend_tile8<HD, F>(B, qb, t1, T, scale, j, m, l, o, magic);
     if (t1 + 2 * kAttnWaves < tile1) load_tile8<HD>(B, kbase, vbase, ksc, vsc, t1 + 2 * kAttnWaves, lane);
   }
   l += __shfl_xor(l, 16, kWave);
@@ -245,13 +245,17 @@ int launch_attention(const AttnArgs& a, hipStream_t stream) {
   if (a.max_seq <= 0 || a.max_seq % kTileKeys) return fail(CQ_EINVAL, "attention: max_seq_len must be a multiple of 32");
   const bool kv8 = a.kcache8 != nullptr;
   if (!a.q || !a.out || !a.d_pos || !a.workspace) return fail(CQ_EINVAL, "attention: null pointer");
+  if (kv8 && a.kv_fmt != CQ_KV_INT8 && a.kv_fmt != CQ_KV_FP8) return fail(CQ_EINVAL, "attention: unknown KV code format");
   if (kv8 ? (!a.vcache8 || !a.kscale || !a.vscale || !a.k_new || !a.v_new) : (!a.kcache || !a.vcache))
     return fail(CQ_EINVAL, "attention: null cache pointer");
   const int P = attention_max_parts(a.n_kv);
   const dim3 grid(P, a.n_kv);
-  if (kv8) {
-    if (a.head_dim == 128) hipLaunchKernelGGL(attention_stage1_kv8<128>, grid, dim3(kAttnThreads), 0, stream, a);
-    else hipLaunchKernelGGL(attention_stage1_kv8<64>, grid, dim3(kAttnThreads), 0, stream, a);
+  if (kv8 && a.kv_fmt == CQ_KV_FP8) {
+    if (a.head_dim == 128) hipLaunchKernelGGL((attention_stage1_kv8<128, CQ_KV_FP8>), grid, dim3(kAttnThreads), 0, stream, a);
+    else hipLaunchKernelGGL((attention_stage1_kv8<64, CQ_KV_FP8>), grid, dim3(kAttnThreads), 0, stream, a);
+  } else if (kv8) {
+    if (a.head_dim == 128) hipLaunchKernelGGL((attention_stage1_kv8<128, CQ_KV_INT8>), grid, dim3(kAttnThreads), 0, stream, a);
+    else hipLaunchKernelGGL((attention_stage1_kv8<64, CQ_KV_INT8>), grid, dim3(kAttnThreads), 0, stream, a);
   } else {
     if (a.head_dim == 128) hipLaunchKernelGGL(attention_stage1<128>, grid, dim3(kAttnThreads), 0, stream, a);
     else hipLaunchKernelGGL(attention_stage1<64>, grid, dim3(kAttnThreads), 0, stream, a);

@@ -168,11 +168,12 @@ extern "C" int cq_gqa_attention_decode(const void* q, const void* kc, const void
   return launch_attention(a, as_stream(stream));
 }
 
-extern "C" int cq_gqa_attention_decode_kv8(const void* q, const void* k_new, const void* v_new, void* k_cache8,
-                                           void* v_cache8, float* k_scale, float* v_scale, void* out,
-                                           const int32_t* d_pos, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
-                                           int32_t max_seq_len, void* workspace, void* stream) {
+static int attention_decode_q(int fmt, const void* q, const void* k_new, const void* v_new, void* k_cache8,
+                              void* v_cache8, float* k_scale, float* v_scale, void* out, const int32_t* d_pos,
+                              int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, int32_t max_seq_len,
+                              void* workspace, void* stream) {
   AttnArgs a;
+  a.kv_fmt = fmt;
   a.q = (const __half*)q; a.out = (__half*)out;
   a.kcache8 = (int8_t*)k_cache8; a.vcache8 = (int8_t*)v_cache8; a.kscale = k_scale; a.vscale = v_scale;
   a.k_new = (const __half*)k_new; a.v_new = (const __half*)v_new;
@@ -180,6 +181,22 @@ extern "C" int cq_gqa_attention_decode_kv8(const void* q, const void* k_new, con
   a.workspace = workspace;
   if (!k_cache8) return fail(CQ_EINVAL, "attention: null cache pointer");
   return launch_attention(a, as_stream(stream));
+}
+
+extern "C" int cq_gqa_attention_decode_kv8(const void* q, const void* k_new, const void* v_new, void* k_cache8,
+                                           void* v_cache8, float* k_scale, float* v_scale, void* out,
+                                           const int32_t* d_pos, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
+                                           int32_t max_seq_len, void* workspace, void* stream) {
+  return attention_decode_q(CQ_KV_INT8, q, k_new, v_new, k_cache8, v_cache8, k_scale, v_scale, out, d_pos, n_heads,
+                            n_kv_heads, head_dim, max_seq_len, workspace, stream);
+}
+
+extern "C" int cq_gqa_attention_decode_fp8(const void* q, const void* k_new, const void* v_new, void* k_cache8,
+                                           void* v_cache8, float* k_scale, float* v_scale, void* out,
+                                           const int32_t* d_pos, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
+                                           int32_t max_seq_len, void* workspace, void* stream) {
+  return attention_decode_q(CQ_KV_FP8, q, k_new, v_new, k_cache8, v_cache8, k_scale, v_scale, out, d_pos, n_heads,
+                            n_kv_heads, head_dim, max_seq_len, workspace, stream);
 }
 
 extern "C" int cq_dequantize(int32_t quant_type, int32_t group_size, const void* W, const void* scale, float* out,

@@ -45,6 +45,15 @@ CQ_HD uint32_t float_bits(float f) {
   return u;
 #endif
 }
+CQ_HD float bits_float(uint32_t u) {
+#ifdef __HIP_DEVICE_COMPILE__
+  return __uint_as_float(u);
+#else
+  float f;
+  __builtin_memcpy(&f, &u, 4);
+  return f;
+#endif
+}
 // float -> IEEE binary16, round to nearest even, in integer arithmetic only,
 // so the generator and the quantizer give the same bits on host and device
 // whatever the hardware's fp16 denormal mode.
@@ -69,6 +78,38 @@ CQ_HD uint16_t f2h_bits(float f) {
   return (uint16_t)(sign | q);
 }
 CQ_HD float h2f_bits(uint16_t h) { return __half2float(__ushort_as_half(h)); }
+
+// ------------------------------------------------------- E4M3 (OCP fp8)
+// Codes of the fp8 KV cache: sign, 4 exponent bits (bias 7), 3 mantissa
+// bits, subnormals m * 2^-9, largest finite 448 (0x7E); no infinities.
+// Finite v to E4M3 with round to nearest, ties to an even mantissa, values
+// past 448 saturating (the quantizer never produces them: |x / s| <= 448),
+// in integer arithmetic so host and device give the same code.
+CQ_HD uint8_t e4m3_bits(float v) {
+  const uint32_t x = float_bits(v);
+  const uint8_t sign = (uint8_t)((x >> 24) & 0x80u);
+  const uint32_t ax = x & 0x7FFFFFFFu;
+  if (ax >= 0x43E80000u) return sign | 0x7Eu;   // >= 464, the 448 / 480 midpoint (ties to 448, even)
+  if (ax < 0x3C800000u) {                        // below 2^-6: the subnormal grid, units of 2^-9
+    if (ax < 0x3A800000u) return sign;           // at most 2^-10 (the tie with 0 goes to 0)
+    const uint32_t e = ax >> 23, m = (ax & 0x7FFFFFu) | 0x800000u;
+    const uint32_t shift = 141u - e;             // value / 2^-9 = m * 2^(e - 141): shift 21..24
+    uint32_t q = m >> shift;
+    const uint32_t rem = m & ((1u << shift) - 1u), half = 1u << (shift - 1u);
+    if (rem > half || (rem == half && (q & 1u))) ++q;
+    return (uint8_t)(sign | q);                  // q = 8 is 2^-6, code 0x08
+  }
+  uint32_t code = ((((ax >> 23) - 120u)) << 3) | ((ax >> 20) & 7u);   // exponent - 127 + 7
+  const uint32_t rem = ax & 0xFFFFFu;
+  if (rem > 0x80000u || (rem == 0x80000u && (code & 1u))) ++code;   // a carry moves to the next binade
+  return (uint8_t)(sign | (code > 0x7Eu ? 0x7Eu : code));
+}
+// Value of a finite E4M3 code.
+CQ_HD float e4m3_value(uint8_t b) {
+  const uint32_t e = (b >> 3) & 15u, m = b & 7u;
+  const float a = e == 0 ? (float)m * 0.001953125f : bits_float(((e + 120u) << 23) | (m << 20));
+  return (b & 0x80u) ? -a : a;
+}
 
 // -------------------------------------------------- synthetic generator
 // splitmix64 finaliser (Steele, Lea, Flood 2014).

@@ -157,8 +157,8 @@ struct cq_state {
   __half *x = nullptr, *xb = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *inter = nullptr, *logits = nullptr;
   __half *kcache = nullptr, *vcache = nullptr;
   size_t layer_kv_halves = 0;       // K (or V) elements of one layer: n_kv * max_seq * head_dim
-  int kv_dtype = CQ_KV_FP16;        // CQ_KV_INT8: kcache / vcache hold int8, scales below
-  float *kscale = nullptr, *vscale = nullptr;   // [layer][kv_head][max_seq] (int8 cache)
+  int kv_dtype = CQ_KV_FP16;        // CQ_KV_INT8 / CQ_KV_FP8: kcache / vcache hold 1-byte codes, scales below
+  float *kscale = nullptr, *vscale = nullptr;   // [layer][kv_head][max_seq] (quantized cache)
   void* attn_ws = nullptr;
   unsigned long long* argmax_ws = nullptr;
   StepCtl* ctl = nullptr;
@@ -188,7 +188,7 @@ int layer_gemvs(const cq_state* s, int l, GemvArgs* qkv, GemvArgs* o, GemvArgs* 
   const cq_config& c = s->cfg;
   const LayerW& L = s->w->layers[l];
   const int qd = c.n_heads * c.head_dim;
-  const bool kv8 = s->kv_dtype == CQ_KV_INT8;
+  const bool kv8 = s->kv_dtype != CQ_KV_FP16;
   __half* kc = kv8 ? nullptr : s->kcache + (size_t)l * s->layer_kv_halves;
   __half* vc = kv8 ? nullptr : s->vcache + (size_t)l * s->layer_kv_halves;
   if (qkv) {
@@ -230,8 +230,9 @@ AttnArgs layer_attn(const cq_state* s, int l) {
   const cq_config& c = s->cfg;
   AttnArgs a;
   a.q = s->q;
-  if (s->kv_dtype == CQ_KV_INT8) {
+  if (s->kv_dtype != CQ_KV_FP16) {
     const size_t ls = (size_t)l * c.n_kv_heads * c.max_seq_len;
+    a.kv_fmt = s->kv_dtype;
     a.kcache8 = reinterpret_cast<int8_t*>(s->kcache) + (size_t)l * s->layer_kv_halves;
     a.vcache8 = reinterpret_cast<int8_t*>(s->vcache) + (size_t)l * s->layer_kv_halves;
     a.kscale = s->kscale + ls;
@@ -336,10 +337,16 @@ __global__ void fill_kv_kernel(__half* kc, __half* vc, int n_layers, int n_kv, i
   }
 }
 
-// int8 cache: one thread per (layer, kv head, position) row of K or V: the
-// generator's fp16 values, quantized with s = max|x| / 127, q = rint(x / s).
-__global__ void fill_kv8_kernel(int8_t* kc, int8_t* vc, float* ks, float* vs, int n_layers, int n_kv, int n_pos,
-                                int max_seq, int hd, uint64_t seed, float mul) {
+// Quantized cache: one thread per (layer, kv head, position) row of K or V:
+// the generator's fp16 values, quantized with s = max|x| / code max and q =
+// the code of x / s (int8: rint clamped to +-127; E4M3: round to nearest even).
+__device__ __forceinline__ int8_t quant_code(int fmt, float v) {
+  return fmt == CQ_KV_FP8 ? (int8_t)e4m3_bits(v) : (int8_t)fminf(127.f, fmaxf(-127.f, rintf(v)));
+}
+CQ_HD float code_max(int fmt) { return fmt == CQ_KV_FP8 ? 448.0f : 127.0f; }
+
+__global__ void fill_kv8_kernel(int fmt, int8_t* kc, int8_t* vc, float* ks, float* vs, int n_layers, int n_kv,
+                                int n_pos, int max_seq, int hd, uint64_t seed, float mul) {
   const int64_t rows = (int64_t)n_layers * n_kv * n_pos * 2;
   for (int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r < rows; r += (int64_t)gridDim.x * blockDim.x) {
     const int kind = (int)(r & 1);
@@ -351,27 +358,33 @@ __global__ void fill_kv8_kernel(int8_t* kc, int8_t* vc, float* ks, float* vs, in
     float amax = 0.f;
     for (int d = 0; d < hd; ++d)
       amax = fmaxf(amax, fabsf(h2f_bits(synth_half(seed, st, (uint64_t)t * hd + d, mul, 0.f))));
-    const float sc = amax / 127.0f;
+    const float sc = amax / code_max(fmt);
     const size_t lo = (size_t)l * n_kv * max_seq * hd;
     int8_t* c = kind ? vc : kc;
     for (int d = 0; d < hd; ++d) {
       const float x = h2f_bits(synth_half(seed, st, (uint64_t)t * hd + d, mul, 0.f));
-      const int8_t q = sc == 0.f ? (int8_t)0 : (int8_t)fminf(127.f, fmaxf(-127.f, rintf(x / sc)));
+      const int8_t q = sc == 0.f ? (int8_t)0 : quant_code(fmt, x / sc);
       c[lo + (kind ? kv_v_offset(h, t, d, max_seq, hd) : kv_k_offset(h, t, d, max_seq, hd))] = q;
     }
     (kind ? vs : ks)[((size_t)l * n_kv + h) * max_seq + t] = sc;
   }
 }
 
-// The same quantization on the host (cq_state_kv_write of an int8 cache).
-void quant_row8_host(const uint16_t* x, int n, int8_t* q, float* s) {
+// The same quantization on the host (cq_state_kv_write of a quantized cache).
+void quant_row8_host(int fmt, const uint16_t* x, int n, int8_t* q, float* s) {
   float amax = 0.f;
   for (int i = 0; i < n; ++i) amax = std::max(amax, std::fabs(h2f_bits(x[i])));
-  const float sc = amax / 127.0f;
+  const float sc = amax / code_max(fmt);
   *s = sc;
-  for (int i = 0; i < n; ++i)
-    q[i] = sc == 0.f ? (int8_t)0 : (int8_t)std::max(-127.f, std::min(127.f, std::nearbyint(h2f_bits(x[i]) / sc)));
+  for (int i = 0; i < n; ++i) {
+    const float v = sc == 0.f ? 0.f : h2f_bits(x[i]) / sc;
+    q[i] = sc == 0.f ? (int8_t)0
+                     : fmt == CQ_KV_FP8 ? (int8_t)e4m3_bits(v) : (int8_t)std::max(-127.f, std::min(127.f, std::nearbyint(v)));
+  }
 }
+
+// Value of one stored code (before its row scale).
+float code_value(int fmt, int8_t b) { return fmt == CQ_KV_FP8 ? e4m3_value((uint8_t)b) : (float)b; }
 
 }  // namespace
 
@@ -492,7 +505,8 @@ extern "C" int cq_state_create(const cq_config* cfg, const cq_weights* w, cq_sta
 
 extern "C" int cq_state_create_kv(const cq_config* cfg, const cq_weights* w, int32_t kv_dtype, cq_state** out) {
   if (!cfg || !w || !out) return fail(CQ_EINVAL, "state_create: null argument");
-  if (kv_dtype != CQ_KV_FP16 && kv_dtype != CQ_KV_INT8) return fail(CQ_EINVAL, "state_create: unknown KV cache type");
+  if (kv_dtype != CQ_KV_FP16 && kv_dtype != CQ_KV_INT8 && kv_dtype != CQ_KV_FP8)
+    return fail(CQ_EINVAL, "state_create: unknown KV cache type");
   CQ_TRY(validate_config(*cfg));
   if (std::memcmp(cfg, &w->cfg, offsetof(cq_config, norm_eps)) != 0)
     return fail(CQ_EINVAL, "state_create: config does not match the weights");
@@ -503,8 +517,9 @@ extern "C" int cq_state_create_kv(const cq_config* cfg, const cq_weights* w, int
   const size_t d = c.dim, qd = (size_t)c.n_heads * c.head_dim, kvd = (size_t)c.n_kv_heads * c.head_dim;
   s->kv_dtype = kv_dtype;
   s->layer_kv_halves = (size_t)c.n_kv_heads * c.max_seq_len * c.head_dim;
-  const size_t kv_bytes = (size_t)c.n_layers * s->layer_kv_halves * (kv_dtype == CQ_KV_INT8 ? 1 : 2);
-  const size_t sc_bytes = kv_dtype == CQ_KV_INT8 ? (size_t)c.n_layers * c.n_kv_heads * c.max_seq_len * 4 : 0;
+  const bool kvq = kv_dtype != CQ_KV_FP16;
+  const size_t kv_bytes = (size_t)c.n_layers * s->layer_kv_halves * (kvq ? 1 : 2);
+  const size_t sc_bytes = kvq ? (size_t)c.n_layers * c.n_kv_heads * c.max_seq_len * 4 : 0;
   // one arena: small activations, control block, history, stamps, workspaces, K, V
   size_t off = 0;
   auto take = [&](size_t bytes) { size_t o = off; off = align_up(off + bytes); return o; };
@@ -624,8 +639,8 @@ extern "C" int cq_state_fill_kv(cq_state* s, int32_t n_pos, uint64_t seed) {
   if (n_pos < 0 || n_pos > s->cfg.max_seq_len) return fail(CQ_ERANGE, "fill_kv: n_pos outside [0, max_seq_len]");
   if (n_pos == 0) return CQ_OK;
   const cq_config& c = s->cfg;
-  if (s->kv_dtype == CQ_KV_INT8)
-    hipLaunchKernelGGL(fill_kv8_kernel, dim3(4096), dim3(256), 0, s->stream, reinterpret_cast<int8_t*>(s->kcache),
+  if (s->kv_dtype != CQ_KV_FP16)
+    hipLaunchKernelGGL(fill_kv8_kernel, dim3(4096), dim3(256), 0, s->stream, s->kv_dtype, reinterpret_cast<int8_t*>(s->kcache),
                        reinterpret_cast<int8_t*>(s->vcache), s->kscale, s->vscale, c.n_layers, c.n_kv_heads, n_pos,
                        c.max_seq_len, c.head_dim, seed, synth_mul(1.0));
   else
@@ -638,7 +653,7 @@ extern "C" int cq_state_fill_kv(cq_state* s, int32_t n_pos, uint64_t seed) {
 
 // One (layer, kv head, K or V) slab of the cache: `elems` elements (whole
 // tiles covering n_pos positions) at `base`, element size 2 (fp16) or 1
-// (int8, with `scales` pointing at the slab's per-position scales).
+// (int8 / E4M3 codes, with `scales` pointing at the slab's per-position scales).
 static int kv_slab(cq_state* s, int layer, int kv_head, int kind, int n_pos, char** base, size_t* elems,
                    float** scales) {
   const cq_config& c = s->cfg;
@@ -647,7 +662,7 @@ static int kv_slab(cq_state* s, int layer, int kv_head, int kind, int n_pos, cha
   if (n_pos < 0 || n_pos > c.max_seq_len) return fail(CQ_ERANGE, "kv access: n_pos outside [0, max_seq_len]");
   const int tile = kind == 0 ? 16 : 32;
   const int tiles = (n_pos + tile - 1) / tile;
-  const size_t es = s->kv_dtype == CQ_KV_INT8 ? 1 : 2;
+  const size_t es = s->kv_dtype == CQ_KV_FP16 ? 2 : 1;
   *elems = (size_t)tiles * tile * c.head_dim;
   const size_t first = (size_t)layer * s->layer_kv_halves + (size_t)kv_head * c.max_seq_len * c.head_dim;
   *base = reinterpret_cast<char*>(kind == 0 ? s->kcache : s->vcache) + first * es;
@@ -677,13 +692,14 @@ extern "C" int cq_state_kv_read(cq_state* s, int32_t layer, int32_t kv_head, int
       for (int d = 0; d < hd; ++d) host_out[(size_t)t * hd + d] = tmp[kv_index(kind, t, d, ms, hd)];
     return CQ_OK;
   }
-  // int8: the dequantized value half(q * s)
+  // quantized: the dequantized value half(q * s)
   std::vector<int8_t> tmp(elems);
   std::vector<float> sc(n_pos > 0 ? n_pos : 1);
   CQ_HIP(hipMemcpy(tmp.data(), base, elems, hipMemcpyDeviceToHost));
   if (n_pos) CQ_HIP(hipMemcpy(sc.data(), scales, (size_t)n_pos * 4, hipMemcpyDeviceToHost));
   for (int t = 0; t < n_pos; ++t)
-    for (int d = 0; d < hd; ++d) host_out[(size_t)t * hd + d] = f2h_bits((float)tmp[kv_index(kind, t, d, ms, hd)] * sc[t]);
+    for (int d = 0; d < hd; ++d)
+      host_out[(size_t)t * hd + d] = f2h_bits(code_value(s->kv_dtype, tmp[kv_index(kind, t, d, ms, hd)]) * sc[t]);
   return CQ_OK;
 }
 
@@ -704,12 +720,12 @@ extern "C" int cq_state_kv_write(cq_state* s, int32_t layer, int32_t kv_head, in
     CQ_HIP(hipMemcpy(base, tmp.data(), elems * 2, hipMemcpyHostToDevice));
     return CQ_OK;
   }
-  // int8: each position's row quantized with s = max|x| / 127
+  // quantized: each position's row with s = max|x| / code max
   std::vector<int8_t> tmp(elems), q(hd);
   std::vector<float> sc(n_pos > 0 ? n_pos : 1);
   CQ_HIP(hipMemcpy(tmp.data(), base, elems, hipMemcpyDeviceToHost));
   for (int t = 0; t < n_pos; ++t) {
-    quant_row8_host(host_in + (size_t)t * hd, hd, q.data(), &sc[t]);
+    quant_row8_host(s->kv_dtype, host_in + (size_t)t * hd, hd, q.data(), &sc[t]);
     for (int d = 0; d < hd; ++d) tmp[kv_index(kind, t, d, ms, hd)] = q[d];
   }
   CQ_HIP(hipMemcpy(base, tmp.data(), elems, hipMemcpyHostToDevice));
@@ -760,7 +776,7 @@ int prefill_batched(cq_state* s, const int32_t* tokens, int n, int pos0) {
     CQ_TRY(launch_pf_embed(s->w->embed, s->pf_tokens, M, d, s->pf_x, st));
     for (int l = 0; l < c.n_layers; ++l) {
       const LayerW& L = s->w->layers[l];
-      const bool kv8 = s->kv_dtype == CQ_KV_INT8;
+      const bool kv8 = s->kv_dtype != CQ_KV_FP16;
       _Float16* kc = kv8 ? nullptr : (_Float16*)(s->kcache + (size_t)l * s->layer_kv_halves);
       _Float16* vc = kv8 ? nullptr : (_Float16*)(s->vcache + (size_t)l * s->layer_kv_halves);
       int8_t* kc8 = kv8 ? reinterpret_cast<int8_t*>(s->kcache) + (size_t)l * s->layer_kv_halves : nullptr;
@@ -778,14 +794,14 @@ int prefill_batched(cq_state* s, const int32_t* tokens, int n, int pos0) {
       g.rows[0] = qd; g.rows[1] = kvd; g.rows[2] = kvd;
       g.out = (_Float16*)s->pf_q; g.head_dim = c.head_dim; g.pos0 = pos0 + c0; g.max_seq = c.max_seq_len;
       g.inv_freq = s->rope_inv_freq; g.kcache = kc; g.vcache = vc;
-      g.kcache8 = kc8; g.vcache8 = vc8; g.kscale = ksc; g.vscale = vsc;
+      g.kcache8 = kc8; g.vcache8 = vc8; g.kscale = ksc; g.vscale = vsc; g.kv_fmt = s->kv_dtype;
       g.part = s->pf_part; g.part_bytes = kPrefillPartBytes;
       CQ_TRY(launch_pf_gemm(g, st));
       PfAttnArgs at;
       at.q = (const _Float16*)s->pf_q; at.kcache = kc; at.vcache = vc; at.out = (_Float16*)s->pf_ao;
       at.M = M; at.pos0 = pos0 + c0; at.n_heads = c.n_heads; at.n_kv = c.n_kv_heads; at.head_dim = c.head_dim;
       at.max_seq = c.max_seq_len;
-      at.kcache8 = kc8; at.vcache8 = vc8; at.kscale = ksc; at.vscale = vsc;
+      at.kcache8 = kc8; at.vcache8 = vc8; at.kscale = ksc; at.vscale = vsc; at.kv_fmt = s->kv_dtype;
       at.int4_layout = c.quant_type == CQ_QUANT_INT4;
       CQ_TRY(launch_pf_attention(at, st));
       if (l == c.n_layers - 1) break;   // the last layer's residual stream feeds nothing here

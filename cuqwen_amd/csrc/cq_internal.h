@@ -61,7 +61,7 @@ struct AttnArgs {
   const int* d_pos = nullptr;
   int n_heads = 0, n_kv = 0, head_dim = 0, max_seq = 0;
   void* workspace = nullptr;
-  // int8 cache (kcache8 / vcache8 set, kcache / vcache unused): per-(position,
+  // quantized cache (kcache8 / vcache8 set, kcache / vcache unused): per-(position,
   // kv head) scales [n_kv][max_seq]; the step's new k / v rows arrive in fp16
   // (k_new / v_new, [n_kv * hd]) and are quantized into position *d_pos here
   int8_t* kcache8 = nullptr;
@@ -70,6 +70,7 @@ struct AttnArgs {
   float* vscale = nullptr;
   const __half* k_new = nullptr;
   const __half* v_new = nullptr;
+  int kv_fmt = CQ_KV_INT8;   // codes of kcache8 / vcache8: CQ_KV_INT8 or CQ_KV_FP8
 };
 size_t attention_workspace_bytes(int n_heads, int n_kv, int head_dim);
 int launch_attention(const AttnArgs& a, hipStream_t stream);
@@ -99,11 +100,12 @@ struct PfGemmArgs {
   // split-K workspace (fp32 partials); nullptr: no split
   float* part = nullptr;
   size_t part_bytes = 0;
-  // int8 cache (instead of kcache / vcache): rows quantized per (token, kv head)
+  // quantized cache (instead of kcache / vcache): rows quantized per (token, kv head)
   int8_t* kcache8 = nullptr;
   int8_t* vcache8 = nullptr;
   float* kscale = nullptr;   // [n_kv][max_seq] of this layer
   float* vscale = nullptr;
+  int kv_fmt = CQ_KV_INT8;   // CQ_KV_INT8 / CQ_KV_FP8 codes
 };
 struct PfAttnArgs {
   const _Float16* q = nullptr;   // [M][n_heads * hd] natural
@@ -111,10 +113,11 @@ struct PfAttnArgs {
   const _Float16* vcache = nullptr;
   _Float16* out = nullptr;       // [M][n_heads * hd] permuted
   int M = 0, pos0 = 0, n_heads = 0, n_kv = 0, head_dim = 0, max_seq = 0;
-  const int8_t* kcache8 = nullptr;   // int8 cache instead of kcache / vcache
+  const int8_t* kcache8 = nullptr;   // quantized cache (kv_fmt codes) instead of kcache / vcache
   const int8_t* vcache8 = nullptr;
   const float* kscale = nullptr;
   const float* vscale = nullptr;
+  int kv_fmt = CQ_KV_INT8;
   bool int4_layout = false;   // out in the int4 GEMM input layout (else natural order)
 };
 int launch_pf_norm(const __half* x, const __half* w, float eps, int M, int dim, __half* A, float* inv, int quant,

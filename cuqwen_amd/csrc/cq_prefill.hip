@@ -147,14 +147,18 @@ __device__ __forceinline__ void pf_qkv_store(const PfGemmArgs& a, int mat, int l
   }
 }
 
-// One (token, kv head) row into the int8 cache: q = rint(x / s) clamped to
-// +-127 (s = max|x| / 127, a zero row keeps s = 0), element d from value(d).
+// One (token, kv head) row into the quantized cache: s = max|x| / code max
+// (a zero row keeps s = 0 and q = 0), q = code of x / s (int8: rint clamped
+// to +-127; E4M3: round to nearest even); element d from value(d).
 template <typename F>
-__device__ __forceinline__ void pf_kv8_store(const PfGemmArgs& a, int mat, int kvh, int pos, float sc, F value) {
+__device__ __forceinline__ void pf_kv8_store(const PfGemmArgs& a, int mat, int kvh, int pos, float amax, F value) {
   const int hd = a.head_dim;
+  const bool f8 = a.kv_fmt == CQ_KV_FP8;
+  const float sc = amax / (f8 ? kv_code_max<CQ_KV_FP8>() : kv_code_max<CQ_KV_INT8>());
   int8_t* c = mat == 1 ? a.kcache8 : a.vcache8;
   for (int d = 0; d < hd; ++d) {
-    const int8_t q = sc == 0.f ? (int8_t)0 : (int8_t)fminf(127.f, fmaxf(-127.f, rintf(value(d) / sc)));
+    const float v = value(d) / sc;
+    const int8_t q = sc == 0.f ? (int8_t)0 : (f8 ? kv_encode<CQ_KV_FP8>(v) : kv_encode<CQ_KV_INT8>(v));
     c[mat == 1 ? kv_k_offset(kvh, pos, d, a.max_seq, hd) : kv_v_offset(kvh, pos, d, a.max_seq, hd)] = q;
   }
   (mat == 1 ? a.kscale : a.vscale)[(int64_t)kvh * a.max_seq + pos] = sc;
@@ -393,7 +397,7 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm_kernel(const PfGemmArgs a)
       const int pos = a.pos0 + m, i = local % hd;
       if (mat < 2) rope_rotate(y0, y1, pos, a.inv_freq[i]);
       if (a.kcache8 && mat > 0) {
-        // int8 cache: rotated values back into the tile, quantized per head below
+        // quantized cache: rotated values back into the tile, quantized per head below
         ot[nl0 * kPfBM + ml] = (_Float16)y0;
         ot[nl1 * kPfBM + ml] = (_Float16)y1;
       } else {
@@ -412,7 +416,7 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm_kernel(const PfGemmArgs a)
         if (mat == 0) continue;
         float amax = 0.f;
         for (int d = 0; d < hd; ++d) amax = fmaxf(amax, fabsf((float)ot[(hb * hd + d) * kPfBM + ml]));
-        pf_kv8_store(a, mat, local / hd, a.pos0 + m, amax / 127.0f,
+        pf_kv8_store(a, mat, local / hd, a.pos0 + m, amax,
                      [&](int d) { return (float)ot[(hb * hd + d) * kPfBM + ml]; });
       }
     }
@@ -439,7 +443,7 @@ __global__ __launch_bounds__(256) void pf_split_epilogue(const PfGemmArgs a, int
       const _Float16* b = a.bias[mat];
       return (float)(_Float16)(sum(0, m, n) * a.inv[m] + (b ? (float)b[local] : 0.f));
     };
-    const int np_store = a.kcache8 ? a.rows[0] / 2 : np;   // int8 cache: k / v rows go per head below
+    const int np_store = a.kcache8 ? a.rows[0] / 2 : np;   // quantized cache: k / v rows go per head below
     for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < (int64_t)a.M * np_store;
          idx += (int64_t)gridDim.x * blockDim.x) {
       const int m = (int)(idx / np_store), p = (int)(idx % np_store);
@@ -466,7 +470,7 @@ __global__ __launch_bounds__(256) void pf_split_epilogue(const PfGemmArgs a, int
         };
         float amax = 0.f;
         for (int d = 0; d < hd; ++d) amax = fmaxf(amax, fabsf(value(d)));
-        pf_kv8_store(a, mat, kvh, a.pos0 + m, amax / 127.0f, value);
+        pf_kv8_store(a, mat, kvh, a.pos0 + m, amax, value);
       }
     }
   } else {
@@ -543,7 +547,7 @@ __device__ __forceinline__ void pf_attend_tile(KVTile<HD>& t, const h8_t* qb, in
   for (int dt = 0; dt < DT; ++dt) o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(t.va[dt], pb, o[dt], 0, 0, 0);
 }
 
-template <int HD, bool KV8>
+template <int HD, int KV8>   // KV8: 0 fp16 cache, else the code format of the quantized cache
 __global__ __launch_bounds__(kAttnThreads) void pf_attention_kernel(const PfAttnArgs a) {
   constexpr int KK = HD / 32, DT = HD / 16;
   const int t0 = blockIdx.x * 16, hq = blockIdx.y;
@@ -577,10 +581,10 @@ __global__ __launch_bounds__(kAttnThreads) void pf_attention_kernel(const PfAttn
     for (; ti < n_tiles; ti += 2 * kAttnWaves) {
       const int t1 = ti + kAttnWaves;
       if (t1 < n_tiles) load_tile8<HD>(B, kb8, vb8, ksc, vsc, t1, lane);
-      attend_tile8<HD>(A, qb, ti, t_lane, scale, j, m, l, o, magic);
+      attend_tile8<HD, KV8>(A, qb, ti, t_lane, scale, j, m, l, o, magic);
       if (t1 >= n_tiles) break;
       if (t1 + kAttnWaves < n_tiles) load_tile8<HD>(A, kb8, vb8, ksc, vsc, t1 + kAttnWaves, lane);
-      attend_tile8<HD>(B, qb, t1, t_lane, scale, j, m, l, o, magic);
+      attend_tile8<HD, KV8>(B, qb, t1, t_lane, scale, j, m, l, o, magic);
     }
   } else {
     KVTile<HD> A, B;
@@ -697,12 +701,17 @@ int launch_pf_attention(const PfAttnArgs& a, hipStream_t stream) {
   if (a.M <= 0 || a.pos0 < 0 || a.pos0 + a.M > a.max_seq) return fail(CQ_ERANGE, "prefill attention: positions");
   const dim3 grid((a.M + 15) / 16, a.n_heads);
   if (a.kcache8) {
-    if (!a.vcache8 || !a.kscale || !a.vscale) return fail(CQ_EINVAL, "prefill attention: int8 cache pointers");
-    if (a.head_dim == 128) hipLaunchKernelGGL((pf_attention_kernel<128, true>), grid, dim3(kAttnThreads), 0, stream, a);
-    else hipLaunchKernelGGL((pf_attention_kernel<64, true>), grid, dim3(kAttnThreads), 0, stream, a);
+    if (!a.vcache8 || !a.kscale || !a.vscale) return fail(CQ_EINVAL, "prefill attention: quantized cache pointers");
+    if (a.kv_fmt == CQ_KV_FP8) {
+      if (a.head_dim == 128) hipLaunchKernelGGL((pf_attention_kernel<128, CQ_KV_FP8>), grid, dim3(kAttnThreads), 0, stream, a);
+      else hipLaunchKernelGGL((pf_attention_kernel<64, CQ_KV_FP8>), grid, dim3(kAttnThreads), 0, stream, a);
+    } else {
+      if (a.head_dim == 128) hipLaunchKernelGGL((pf_attention_kernel<128, CQ_KV_INT8>), grid, dim3(kAttnThreads), 0, stream, a);
+      else hipLaunchKernelGGL((pf_attention_kernel<64, CQ_KV_INT8>), grid, dim3(kAttnThreads), 0, stream, a);
+    }
   } else {
-    if (a.head_dim == 128) hipLaunchKernelGGL((pf_attention_kernel<128, false>), grid, dim3(kAttnThreads), 0, stream, a);
-    else hipLaunchKernelGGL((pf_attention_kernel<64, false>), grid, dim3(kAttnThreads), 0, stream, a);
+    if (a.head_dim == 128) hipLaunchKernelGGL((pf_attention_kernel<128, 0>), grid, dim3(kAttnThreads), 0, stream, a);
+    else hipLaunchKernelGGL((pf_attention_kernel<64, 0>), grid, dim3(kAttnThreads), 0, stream, a);
   }
   CQ_HIP(hipGetLastError());
   return CQ_OK;

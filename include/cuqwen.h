@@ -119,11 +119,17 @@ int cq_state_destroy(cq_state* s);
  * the PV product. */
 #define CQ_KV_FP16 0
 #define CQ_KV_INT8 1
+/* CQ_KV_FP8 (the roadmap item's other format, "int8/fp8") stores OCP FP8
+ * E4M3 codes (bias 7, no infinities, largest finite 448) instead:
+ * s = max|x| / 448, q = e4m3(x / s) rounded to nearest with ties to an even
+ * mantissa; scores and P as for CQ_KV_INT8 with q read as its E4M3 value.
+ * Same storage as CQ_KV_INT8 (one byte per element plus the row scales). */
+#define CQ_KV_FP8 2
 
 /* malloc_qwen_state with a choice of KV cache element type (CQ_KV_*);
- * cq_state_create is cq_state_create_kv(..., CQ_KV_FP16, ...).  With an int8
- * cache, cq_state_kv_read returns half(q * s) and cq_state_kv_write
- * quantizes each position's row as above. */
+ * cq_state_create is cq_state_create_kv(..., CQ_KV_FP16, ...).  With a
+ * quantized cache, cq_state_kv_read returns half(value(q) * s) and
+ * cq_state_kv_write quantizes each position's row as above. */
 int cq_state_create_kv(const cq_config* cfg, const cq_weights* w, int32_t kv_dtype, cq_state** out);
 
 /* qwen_forward() (include/model.cuh:51-60, src/model.cu:183-223): one decode
@@ -314,6 +320,13 @@ size_t cq_attention_workspace_bytes(int32_t n_heads, int32_t n_kv_heads, int32_t
  * ([n_kv_heads][max_seq_len] fp32), then attn_out is computed over keys
  * [0, *d_pos].  `workspace` as for cq_gqa_attention_decode. */
 int cq_gqa_attention_decode_kv8(const void* q, const void* k_new, const void* v_new, void* k_cache8, void* v_cache8,
+                                float* k_scale, float* v_scale, void* attn_out, const int32_t* d_pos,
+                                int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, int32_t max_seq_len,
+                                void* workspace, void* stream);
+/* The same over an E4M3 layer cache (see CQ_KV_FP8; no counterpart in the
+ * reference): arguments as for cq_gqa_attention_decode_kv8, the caches
+ * holding E4M3 codes. */
+int cq_gqa_attention_decode_fp8(const void* q, const void* k_new, const void* v_new, void* k_cache8, void* v_cache8,
                                 float* k_scale, float* v_scale, void* attn_out, const int32_t* d_pos,
                                 int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, int32_t max_seq_len,
                                 void* workspace, void* stream);

@@ -324,14 +324,65 @@ void quant_row_i8(const uint16_t* x, int n, int8_t* q, float* s) {
   }
 }
 
-// Attention over an int8 cache Kq/Vq [n_kv][stride][hd] with row scales
-// Ks/Vs [n_kv][stride].  mode 1: softmax over q.(kq*ks)/sqrt(hd) of (vq*vs)
+// ------------------------------------------------------------- fp8 KV
+// The other format of the same roadmap item (README.md:147, "int8/fp8"):
+// OCP FP8 E4M3 ("e4m3fn": sign, 4 exponent bits with bias 7, 3 mantissa
+// bits, no infinities, 0x7F / 0xFF are NaN, largest finite 448).  A row is
+// stored as q = e4m3(x / s) with s = max|x| / 448 in fp32, rounding to
+// nearest with ties to an even mantissa; a zero row keeps s = 0, q = 0.
+float e4m3_decode(uint8_t b) {
+  const int e = (b >> 3) & 15, m = b & 7;
+  float v;
+  if (e == 15 && m == 7) v = NAN;
+  else if (e == 0) v = std::ldexp((float)m, -9);              // subnormal: m * 2^-9
+  else v = std::ldexp(1.0f + (float)m / 8.0f, e - 7);
+  return (b & 0x80) ? -v : v;
+}
+
+// Finite x to E4M3, round to nearest even, saturating at +-448.
+uint8_t e4m3_encode(float x) {
+  const uint8_t sign = std::signbit(x) ? 0x80 : 0;
+  const float a = std::fabs(x);
+  if (a < 0.015625f) {   // below 2^-6: the subnormal grid m * 2^-9 (m = 8 is 2^-6, code 0x08)
+    return sign | (uint8_t)std::nearbyint(a * 512.0f);   // exact scaling, round half to even
+  }
+  int k;
+  const float f = std::frexp(a, &k);   // a = f * 2^k, f in [0.5, 1)
+  int E = k - 1;                       // a = r * 2^E, r in [1, 2)
+  const float r = f * 2.0f;
+  int m = (int)std::nearbyint((r - 1.0f) * 8.0f);   // r - 1 and the * 8 are exact
+  if (m == 8) { m = 0; ++E; }
+  if (E > 8 || (E == 8 && m > 6)) return sign | 0x7E;   // beyond 448
+  return sign | (uint8_t)(((E + 7) << 3) | m);
+}
+
+void quant_row_f8(const uint16_t* x, int n, uint8_t* q, float* s) {
+  float amax = 0.f;
+  for (int i = 0; i < n; ++i) amax = std::max(amax, std::fabs(h2f(x[i])));
+  const float sc = amax / 448.0f;
+  *s = sc;
+  for (int i = 0; i < n; ++i) q[i] = sc == 0.f ? 0 : e4m3_encode(h2f(x[i]) / sc);
+}
+
+// Value of one stored byte of a quantized cache (before its row scale):
+// fmt 1 int8, 2 E4M3.
+inline float kv_code(int fmt, int8_t b) { return fmt == 2 ? e4m3_decode((uint8_t)b) : (float)b; }
+
+void quant_row_kv(int fmt, const uint16_t* x, int n, int8_t* q, float* s) {
+  if (fmt == 2) quant_row_f8(x, n, reinterpret_cast<uint8_t*>(q), s);
+  else quant_row_i8(x, n, q, s);
+}
+
+// Attention over a quantized cache Kq/Vq [n_kv][stride][hd] (bytes of
+// format fmt: 1 int8, 2 E4M3) with row scales Ks/Vs [n_kv][stride]; below,
+// kq / vq stand for the decoded byte values.  mode 1: softmax over q.(kq*ks)/sqrt(hd) of (vq*vs)
 // in double.  mode 0: the device's rounding points: score =
 // half((q.kq) * ks * 1/sqrt(hd)) with the dot in fp32, e = exp(s - m_part),
 // P = half(e * vs) for the PV product while the partition sum adds the
 // unrounded e, partitions merged like attention() above.
 void attention_i8(const uint16_t* q, const int8_t* Kq, const float* Ks, const int8_t* Vq, const float* Vs,
-                  uint16_t* out, int n_heads, int n_kv, int hd, int64_t stride, int T, int mode, int nparts) {
+                  uint16_t* out, int n_heads, int n_kv, int hd, int64_t stride, int T, int mode, int nparts,
+                  int fmt = 1) {
   const int g = n_heads / n_kv;
   const float scale = 1.0f / std::sqrt((float)hd);
 #pragma omp parallel for schedule(dynamic)
@@ -347,7 +398,7 @@ void attention_i8(const uint16_t* q, const int8_t* Kq, const float* Ks, const in
       double mx = -INFINITY;
       for (int t = 0; t < T; ++t) {
         double a = 0.0;
-        for (int d = 0; d < hd; ++d) a += (double)h2f(qh[d]) * ((double)Kh[(int64_t)t * hd + d] * ksh[t]);
+        for (int d = 0; d < hd; ++d) a += (double)h2f(qh[d]) * ((double)kv_code(fmt, Kh[(int64_t)t * hd + d]) * ksh[t]);
         s[t] = a / std::sqrt((double)hd);
         mx = std::max(mx, s[t]);
       }
@@ -356,7 +407,7 @@ void attention_i8(const uint16_t* q, const int8_t* Kq, const float* Ks, const in
       for (int t = 0; t < T; ++t) {
         const double e = std::exp(s[t] - mx);
         L += e;
-        for (int d = 0; d < hd; ++d) o[d] += e * ((double)Vh[(int64_t)t * hd + d] * vsh[t]);
+        for (int d = 0; d < hd; ++d) o[d] += e * ((double)kv_code(fmt, Vh[(int64_t)t * hd + d]) * vsh[t]);
       }
       for (int d = 0; d < hd; ++d) out[(int64_t)h * hd + d] = f2h((float)(o[d] / L));
       continue;
@@ -370,7 +421,7 @@ void attention_i8(const uint16_t* q, const int8_t* Kq, const float* Ks, const in
       float mx = -1e30f;
       for (int t = t0; t < t1; ++t) {
         float a = 0.f;
-        for (int d = 0; d < hd; ++d) a += h2f(qh[d]) * (float)Kh[(int64_t)t * hd + d];
+        for (int d = 0; d < hd; ++d) a += h2f(qh[d]) * kv_code(fmt, Kh[(int64_t)t * hd + d]);
         sc[t - t0] = rh(a * ksh[t] * scale);
         mx = std::max(mx, sc[t - t0]);
       }
@@ -380,7 +431,7 @@ void attention_i8(const uint16_t* q, const int8_t* Kq, const float* Ks, const in
         const float e = std::exp(sc[t - t0] - mx);
         sum += e;
         const float P = rh(e * vsh[t]);
-        for (int d = 0; d < hd; ++d) pv[d] += P * (float)Vh[(int64_t)t * hd + d];
+        for (int d = 0; d < hd; ++d) pv[d] += P * kv_code(fmt, Vh[(int64_t)t * hd + d]);
       }
       pm[p] = mx;
       ps[p] = sum;
@@ -454,7 +505,7 @@ struct Model {
   std::vector<Layer> L;
   int kv_slots = 0;
   std::vector<uint16_t> K, V;   // [layers][kv][kv_slots][hd]
-  int kv8 = 0;                  // int8 cache: Kq/Vq [layers][kv][kv_slots][hd], Ks/Vs [layers][kv][kv_slots]
+  int kv8 = 0;                  // 0 fp16; 1 int8 / 2 E4M3 cache: Kq/Vq [layers][kv][kv_slots][hd] bytes, Ks/Vs [layers][kv][kv_slots]
   std::vector<int8_t> Kq, Vq;
   std::vector<float> Ks, Vs;
   std::vector<uint16_t> logits;
@@ -523,8 +574,8 @@ void store_kv(Model& m, int l, int pos, const uint16_t* k, const uint16_t* v) {
   for (int h = 0; h < c.kv; ++h) {
     const size_t row = ((size_t)l * c.kv + h) * m.kv_slots + pos;
     if (m.kv8) {
-      quant_row_i8(k + h * c.hd, c.hd, m.Kq.data() + row * c.hd, m.Ks.data() + row);
-      quant_row_i8(v + h * c.hd, c.hd, m.Vq.data() + row * c.hd, m.Vs.data() + row);
+      quant_row_kv(m.kv8, k + h * c.hd, c.hd, m.Kq.data() + row * c.hd, m.Ks.data() + row);
+      quant_row_kv(m.kv8, v + h * c.hd, c.hd, m.Vq.data() + row * c.hd, m.Vs.data() + row);
     } else {
       std::memcpy(m.K.data() + row * c.hd, k + h * c.hd, c.hd * 2);
       std::memcpy(m.V.data() + row * c.hd, v + h * c.hd, c.hd * 2);
@@ -559,7 +610,7 @@ int forward(Model& m, int token, int pos, const int* hist, int hlen, int mode) {
     if (m.kv8) {
       const size_t ls = (size_t)l * c.kv * m.kv_slots;
       attention_i8(q.data(), m.Kq.data() + lo, m.Ks.data() + ls, m.Vq.data() + lo, m.Vs.data() + ls, att.data(),
-                   c.heads, c.kv, c.hd, m.kv_slots, pos + 1, mode, m.nparts);
+                   c.heads, c.kv, c.hd, m.kv_slots, pos + 1, mode, m.nparts, m.kv8);
     } else {
       attention(q.data(), m.K.data() + lo, m.V.data() + lo, att.data(), c.heads, c.kv, c.hd, m.kv_slots, pos + 1,
                 mode, m.nparts);
@@ -627,6 +678,18 @@ void or_quant_row_i8(const uint16_t* x, int n, int8_t* q, float* s) { quant_row_
 void or_attention_i8(const uint16_t* q, const int8_t* Kq, const float* Ks, const int8_t* Vq, const float* Vs,
                      uint16_t* out, int n_heads, int n_kv, int hd, int64_t stride, int T, int mode, int nparts) {
   attention_i8(q, Kq, Ks, Vq, Vs, out, n_heads, n_kv, hd, stride, T, mode, nparts);
+}
+void or_attention_kvq(const uint16_t* q, const int8_t* Kq, const float* Ks, const int8_t* Vq, const float* Vs,
+                      uint16_t* out, int n_heads, int n_kv, int hd, int64_t stride, int T, int mode, int nparts,
+                      int fmt) {
+  attention_i8(q, Kq, Ks, Vq, Vs, out, n_heads, n_kv, hd, stride, T, mode, nparts, fmt);
+}
+void or_quant_row_f8(const uint16_t* x, int n, uint8_t* q, float* s) { quant_row_f8(x, n, q, s); }
+void or_e4m3_encode(const float* x, int64_t n, uint8_t* out) {
+  for (int64_t i = 0; i < n; ++i) out[i] = e4m3_encode(x[i]);
+}
+void or_e4m3_decode(const uint8_t* b, int64_t n, float* out) {
+  for (int64_t i = 0; i < n; ++i) out[i] = e4m3_decode(b[i]);
 }
 int or_argmax(const uint16_t* logits, int vocab) { return argmax(logits, vocab); }
 void or_penalty(uint16_t* logits, const int* hist, int n, int vocab, float pen) { penalty(logits, hist, n, vocab, pen); }
@@ -724,8 +787,8 @@ void or_model_fill_kv(void* h, int n_pos, uint64_t seed) {
         }
         const size_t row = row0 + t;
         if (m.kv8) {
-          quant_row_i8(kr.data(), hd, m.Kq.data() + row * hd, m.Ks.data() + row);
-          quant_row_i8(vr.data(), hd, m.Vq.data() + row * hd, m.Vs.data() + row);
+          quant_row_kv(m.kv8, kr.data(), hd, m.Kq.data() + row * hd, m.Ks.data() + row);
+          quant_row_kv(m.kv8, vr.data(), hd, m.Vq.data() + row * hd, m.Vs.data() + row);
         } else {
           std::memcpy(m.K.data() + row * hd, kr.data(), hd * 2);
           std::memcpy(m.V.data() + row * hd, vr.data(), hd * 2);
@@ -734,7 +797,7 @@ void or_model_fill_kv(void* h, int n_pos, uint64_t seed) {
     }
 }
 
-// Switch the cache to int8 (1) or fp16 (0); clears it.
+// Switch the cache to fp16 (0), int8 (1) or E4M3 (2); clears it.
 void or_model_set_kv8(void* h, int on) {
   Model& m = *static_cast<Model*>(h);
   m.kv8 = on;
@@ -751,7 +814,7 @@ void or_model_logits(void* h, uint16_t* out) {
   std::memcpy(out, m.logits.data(), m.logits.size() * 2);
 }
 // Raw access for tests: kind 0/1 = K/V of (layer, kv_head) positions [0, n).
-// (int8 cache: the dequantized value half(q * s) of each element.)
+// (quantized cache: the dequantized value half(q * s) of each element.)
 void or_model_kv(void* h, int layer, int kv_head, int kind, int n, uint16_t* out) {
   Model& m = *static_cast<Model*>(h);
   const size_t row0 = ((size_t)layer * m.c.kv + kv_head) * m.kv_slots;
@@ -760,12 +823,12 @@ void or_model_kv(void* h, int layer, int kv_head, int kind, int n, uint16_t* out
     const std::vector<float>& S = kind ? m.Vs : m.Ks;
     for (int t = 0; t < n; ++t)
       for (int d = 0; d < m.c.hd; ++d)
-        out[(size_t)t * m.c.hd + d] = f2h((float)Q[(row0 + t) * m.c.hd + d] * S[row0 + t]);
+        out[(size_t)t * m.c.hd + d] = f2h(kv_code(m.kv8, Q[(row0 + t) * m.c.hd + d]) * S[row0 + t]);
     return;
   }
   std::memcpy(out, (kind ? m.V : m.K).data() + row0 * m.c.hd, (size_t)n * m.c.hd * 2);
 }
-// Raw int8 rows and scales (int8 cache only).
+// Raw quantized rows (bytes) and scales (int8 / E4M3 cache only).
 void or_model_kv8(void* h, int layer, int kv_head, int kind, int n, int8_t* q, float* sc) {
   Model& m = *static_cast<Model*>(h);
   const size_t row0 = ((size_t)layer * m.c.kv + kv_head) * m.kv_slots;

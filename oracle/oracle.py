@@ -41,6 +41,10 @@ def _load():
         "or_argmax": (I, [P, I]),
         "or_quant_row_i8": (None, [P, I, P, P]),
         "or_attention_i8": (None, [P, P, P, P, P, P, I, I, I, I64, I, I, I]),
+        "or_attention_kvq": (None, [P, P, P, P, P, P, I, I, I, I64, I, I, I, I]),
+        "or_quant_row_f8": (None, [P, I, P, P]),
+        "or_e4m3_encode": (None, [P, I64, P]),
+        "or_e4m3_decode": (None, [P, I64, P]),
         "or_model_set_kv8": (None, [P, I]),
         "or_model_kv8": (None, [P, I, I, I, I, P, P]),
         "or_penalty": (None, [P, P, I, I, F]),
@@ -135,15 +139,56 @@ def quant_rows_i8(x):
     return q, s
 
 
-def attention_i8(q, Kq, Ks, Vq, Vs, n_heads, n_kv, hd, T, mode=0, nparts=64):
-    """Attention over an int8 cache: Kq/Vq [n_kv][T][hd] int8, Ks/Vs [n_kv][T] fp32."""
-    Kq, Vq = np.ascontiguousarray(Kq, dtype=np.int8), np.ascontiguousarray(Vq, dtype=np.int8)
+def attention_i8(q, Kq, Ks, Vq, Vs, n_heads, n_kv, hd, T, mode=0, nparts=64, fmt=1):
+    """Attention over a quantized cache: Kq/Vq [n_kv][T][hd] bytes (fmt 1:
+    int8, 2: E4M3), Ks/Vs [n_kv][T] fp32."""
+    Kq = np.ascontiguousarray(Kq).view(np.int8)
+    Vq = np.ascontiguousarray(Vq).view(np.int8)
     Ks, Vs = np.ascontiguousarray(Ks, dtype=np.float32), np.ascontiguousarray(Vs, dtype=np.float32)
     out = np.zeros(n_heads * hd, dtype=np.uint16)
     qq = np.ascontiguousarray(q, dtype=np.float16)
-    lib.or_attention_i8(_p(qq), _p(Kq), _p(Ks), _p(Vq), _p(Vs), _p(out), n_heads, n_kv, hd, Kq.shape[1], T, mode,
-                        nparts)
+    lib.or_attention_kvq(_p(qq), _p(Kq), _p(Ks), _p(Vq), _p(Vs), _p(out), n_heads, n_kv, hd, Kq.shape[1], T, mode,
+                         nparts, fmt)
     return out.view(np.float16)
+
+
+def quant_rows_f8(x):
+    """E4M3 KV quantization of each row of x (fp16 [n][hd]): (q uint8 codes, s fp32)."""
+    x = np.ascontiguousarray(x, dtype=np.float16)
+    n, hd = x.shape
+    q = np.zeros((n, hd), dtype=np.uint8)
+    s = np.zeros(n, dtype=np.float32)
+    for i in range(n):
+        lib.or_quant_row_f8(_p(x[i]), hd, _p(q[i]), _p(s[i:i + 1]))
+    return q, s
+
+
+def quant_rows_kv(x, fmt):
+    """Rows quantized in KV format fmt (1 int8, 2 E4M3); codes as uint8."""
+    if fmt == 2:
+        return quant_rows_f8(x)
+    q, s = quant_rows_i8(x)
+    return q.view(np.uint8), s
+
+
+def e4m3_encode(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.zeros(x.shape, dtype=np.uint8)
+    lib.or_e4m3_encode(_p(x), x.size, _p(out))
+    return out
+
+
+def e4m3_decode(b):
+    b = np.ascontiguousarray(b, dtype=np.uint8)
+    out = np.zeros(b.shape, dtype=np.float32)
+    lib.or_e4m3_decode(_p(b), b.size, _p(out))
+    return out
+
+
+def kv_decode(codes, fmt):
+    """Values of stored cache bytes (before the row scale)."""
+    codes = np.ascontiguousarray(codes, dtype=np.uint8)
+    return e4m3_decode(codes) if fmt == 2 else codes.view(np.int8).astype(np.float32)
 
 
 def argmax(logits):
@@ -181,10 +226,11 @@ class Model:
         lib.or_model_set_nparts(self.h, n)
 
     def set_kv8(self, on=True):
-        """int8 KV cache (clears the cache)."""
-        lib.or_model_set_kv8(self.h, 1 if on else 0)
+        """Quantized KV cache (clears the cache): True / 1 int8, 2 E4M3, 0 fp16."""
+        lib.or_model_set_kv8(self.h, int(on))
 
     def kv8(self, layer, kv_head, kind, n):
+        """Raw rows (int8 array; E4M3 codes viewed as int8) and scales."""
         q = np.zeros((n, self.cfg.head_dim), dtype=np.int8)
         s = np.zeros(n, dtype=np.float32)
         lib.or_model_kv8(self.h, layer, kv_head, kind, n, _p(q), _p(s))

@@ -1,6 +1,7 @@
-"""GPU int8 KV cache (CQ_KV_INT8, the reference's roadmap item README.md:147)
-against the host oracle's int8 mode: per-(position, kv head) quantization
-bit-exact, attention within 1e-2, decode and prefill parity."""
+"""GPU quantized KV caches (CQ_KV_INT8 and CQ_KV_FP8 / E4M3, the reference's
+roadmap item README.md:147, "int8/fp8") against the host oracle's matching
+mode: per-(position, kv head) quantization bit-exact, attention within 1e-2,
+decode and prefill parity."""
 import numpy as np
 import pytest
 
@@ -11,6 +12,8 @@ from tests.gpu_util import Pool, rel_err, k_offsets, v_offsets
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-2
+FMTS = [cq.KV_INT8, cq.KV_FP8]
+ENTRY = {cq.KV_INT8: "cq_gqa_attention_decode_kv8", cq.KV_FP8: "cq_gqa_attention_decode_fp8"}
 
 
 @pytest.fixture
@@ -20,6 +23,17 @@ def g():
     p.close()
 
 
+def _kv_match(got, want, fmt):
+    """Dequantized cache rows of the device against the oracle's.  The rows
+    are quantized from k / v values that differ slightly (GEMV accumulation
+    order in layer 0, then the attention of earlier layers), which can move
+    an element to a neighbouring code.  For int8 a code step is 1/127 of the
+    row maximum, so rows stay within 1e-2 of it; the largest E4M3 code step
+    is 32 / 448 of the row maximum (448 -> 416), so for E4M3 rows the bound
+    is 0.08 of the row maximum (the logits are still held to 1e-2)."""
+    return rel_err(got, want) <= (TOL if fmt == cq.KV_INT8 else 0.08)
+
+
 def _gap(logits):
     l = np.sort(logits.astype(np.float64))
     return l[-1] - l[-2]
@@ -27,31 +41,46 @@ def _gap(logits):
 
 def _tile8(Kq, Vq, max_seq):
     n_kv, T, hd = Kq.shape
-    kc = np.zeros(n_kv * max_seq * hd, dtype=np.int8)
-    vc = np.zeros(n_kv * max_seq * hd, dtype=np.int8)
+    kc = np.zeros(n_kv * max_seq * hd, dtype=Kq.dtype)
+    vc = np.zeros(n_kv * max_seq * hd, dtype=Vq.dtype)
     kc[k_offsets(n_kv, T, hd, max_seq).ravel()] = Kq.ravel()
     vc[v_offsets(n_kv, T, hd, max_seq).ravel()] = Vq.ravel()
     return kc, vc
 
 
+def _e4m3_tie_rows(KV, hd):
+    """New k / v rows whose E4M3 codes exercise ties (to the even mantissa),
+    the subnormal grid and its tie with zero, the largest code and signs:
+    max|x| = 448 makes s = 1, so each code is e4m3(x) itself."""
+    base = np.float32([448, 1.0625, -1.1875, 2.0 ** -10, 3 * 2.0 ** -10, -2.0 ** -9, 0, 9.5, 232, -240, 0.01171875,
+                       2.0 ** -7 * 1.5, -448, 26, 1e-4, 3.0])
+    row = np.resize(base, hd)
+    return np.tile(row, (KV, 1)).astype(np.float16)
+
+
+@pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("H,KV,hd,T", [(28, 4, 128, 1), (28, 4, 128, 33), (14, 2, 64, 300), (12, 2, 128, 4100),
                                        (28, 4, 128, 32768), (40, 8, 128, 5000)])
-def test_attention_kv8_matches_oracle(g, H, KV, hd, T):
+def test_attention_kv8_matches_oracle(g, fmt, H, KV, hd, T):
     """Positions [0, T-1) come quantized in the cache; the new row (position
     T-1) arrives in fp16 and must be stored exactly as the oracle quantizes
-    it, scale included; the output matches the oracle's int8 attention."""
+    it, scale included; the output matches the oracle's attention over the
+    same format."""
     ms = ((T + 31) // 32) * 32
     rng = np.random.default_rng(T + H)
     q = rng.standard_normal(H * hd).astype(np.float16)
     K = rng.standard_normal((KV, T, hd)).astype(np.float16)
     V = rng.standard_normal((KV, T, hd)).astype(np.float16)
-    Kq, Ks = orc.quant_rows_i8(K.reshape(-1, hd))
-    Vq, Vs = orc.quant_rows_i8(V.reshape(-1, hd))
+    if fmt == cq.KV_FP8 and T in (33, 300):
+        K[:, T - 1] = _e4m3_tie_rows(KV, hd)
+        V[:, T - 1] = -_e4m3_tie_rows(KV, hd)
+    Kq, Ks = orc.quant_rows_kv(K.reshape(-1, hd), fmt)
+    Vq, Vs = orc.quant_rows_kv(V.reshape(-1, hd), fmt)
     Kq, Vq, Ks, Vs = Kq.reshape(KV, T, hd), Vq.reshape(KV, T, hd), Ks.reshape(KV, T), Vs.reshape(KV, T)
     # the device starts with positions [0, T-1) only; T-1 is garbage until the call
     Kd, Vd = Kq.copy(), Vq.copy()
-    Kd[:, T - 1] = 99
-    Vd[:, T - 1] = -99
+    Kd[:, T - 1] = 0x63
+    Vd[:, T - 1] = 0x9D
     kc, vc = _tile8(Kd, Vd, ms)
     ksd = np.zeros((KV, ms), np.float32)
     vsd = np.zeros((KV, ms), np.float32)
@@ -62,11 +91,11 @@ def test_attention_kv8_matches_oracle(g, H, KV, hd, T):
     vnew = np.ascontiguousarray(V[:, T - 1].reshape(-1))
     ws = g.empty(cq.lib.cq_attention_workspace_bytes(H, KV, hd), zero=True)
     out = g.empty(H * hd * 2)
-    cq.check(cq.lib.cq_gqa_attention_decode_kv8(g.put(q), g.put(knew), g.put(vnew), pk, pv, pks, pvs, out.ptr,
-                                                g.i32(T - 1), H, KV, hd, ms, ws.ptr, None))
+    cq.check(getattr(cq.lib, ENTRY[fmt])(g.put(q), g.put(knew), g.put(vnew), pk, pv, pks, pvs, out.ptr,
+                                         g.i32(T - 1), H, KV, hd, ms, ws.ptr, None))
     got = out.to_array(np.float16)
-    assert rel_err(got, orc.attention_i8(q, Kq, Ks, Vq, Vs, H, KV, hd, T, mode=1)) <= TOL
-    assert rel_err(got, orc.attention_i8(q, Kq, Ks, Vq, Vs, H, KV, hd, T, mode=0)) <= TOL
+    assert rel_err(got, orc.attention_i8(q, Kq, Ks, Vq, Vs, H, KV, hd, T, mode=1, fmt=fmt)) <= TOL
+    assert rel_err(got, orc.attention_i8(q, Kq, Ks, Vq, Vs, H, KV, hd, T, mode=0, fmt=fmt)) <= TOL
     # the new row and its scales, bit-exact
     kc2 = np.zeros_like(kc)
     vc2 = np.zeros_like(vc)
@@ -83,14 +112,15 @@ def test_attention_kv8_matches_oracle(g, H, KV, hd, T):
     np.testing.assert_array_equal(vs2[:, T - 1], Vs[:, T - 1])
 
 
-def test_state_kv8_fill_and_write_read():
-    """The int8 filler equals the oracle's (dequantized values bit-exact);
-    kv_write quantizes each row and kv_read returns half(q * s)."""
+@pytest.mark.parametrize("fmt", FMTS)
+def test_state_kv8_fill_and_write_read(fmt):
+    """The quantized filler equals the oracle's (dequantized values
+    bit-exact); kv_write quantizes each row and kv_read returns half(q * s)."""
     cfg = tiny_config(1)
     w = cq.synth_weights(cfg, 1)
-    st = cq.State(cfg, w, kv_dtype=cq.KV_INT8)
+    st = cq.State(cfg, w, kv_dtype=fmt)
     om = orc.Model.synth(cfg, 1, cfg.max_seq_len)
-    om.set_kv8(True)
+    om.set_kv8(fmt)
     st.fill_kv(100, 77)
     om.fill_kv(100, 77)
     for layer in range(cfg.n_layers):
@@ -100,23 +130,24 @@ def test_state_kv8_fill_and_write_read():
                                               om.kv(layer, h, kind, 100).view(np.uint16))
     rows = (np.random.default_rng(2).standard_normal((40, cfg.head_dim)) * 3).astype(np.float16)
     cq.check(cq.lib.cq_state_kv_write(st.handle, 1, 0, 1, 40, rows.view(np.uint16).ctypes.data))
-    q, s = orc.quant_rows_i8(rows)
-    want = (q.astype(np.float32) * s[:, None]).astype(np.float16)
+    q, s = orc.quant_rows_kv(rows, fmt)
+    want = (orc.kv_decode(q, fmt) * s[:, None]).astype(np.float16)
     np.testing.assert_array_equal(st.kv_read(1, 0, 1, 40).view(np.uint16), want.view(np.uint16))
     st.free()
     w.free()
 
 
+@pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("quant", [0, 1, 2])
-def test_decode_kv8_tiny_matches_oracle(quant):
-    """Teacher-forced decode with an int8 cache against the oracle's int8
-    mode: logits within 1e-2, top-1 where the gap exceeds 1e-2, the cache
-    rows bit-exact."""
+def test_decode_kv8_tiny_matches_oracle(quant, fmt):
+    """Teacher-forced decode with a quantized cache against the oracle's
+    matching mode: logits within 1e-2, top-1 where the gap exceeds 1e-2, the
+    cache rows within 1e-2."""
     cfg = tiny_config(quant)
     w = cq.synth_weights(cfg, 4)
     om = orc.Model.synth(cfg, 4, cfg.max_seq_len)
-    om.set_kv8(True)
-    st = cq.State(cfg, w, kv_dtype=cq.KV_INT8)
+    om.set_kv8(fmt)
+    st = cq.State(cfg, w, kv_dtype=fmt)
     tok, hist, checked = 5, [], 0
     for pos in range(40):
         ot = om.forward(tok, pos, hist)
@@ -132,21 +163,22 @@ def test_decode_kv8_tiny_matches_oracle(quant):
     for layer in range(cfg.n_layers):
         for h in range(cfg.n_kv_heads):
             for kind in (0, 1):
-                assert rel_err(st.kv_read(layer, h, kind, 40), om.kv(layer, h, kind, 40)) <= TOL
+                assert _kv_match(st.kv_read(layer, h, kind, 40), om.kv(layer, h, kind, 40), fmt)
     st.free()
     w.free()
 
 
-def test_decode_kv8_7b_int4_32k_matches_oracle():
-    """The bench workload's shapes (7B INT4, 28 layers, int8 lm_head) with an
-    int8 cache prefilled to just below 32768."""
+@pytest.mark.parametrize("fmt", FMTS)
+def test_decode_kv8_7b_int4_32k_matches_oracle(fmt):
+    """The bench workload's shapes (7B INT4, 28 layers, int8 lm_head) with a
+    quantized cache prefilled to just below 32768."""
     cfg = cq.preset("7B", "int4")
     n_ctx, steps = 32768 - 4, 4
     w = cq.synth_weights(cfg, 0x5157454E)
     om = orc.Model.synth(cfg, 0x5157454E, n_ctx + steps)
-    om.set_kv8(True)
+    om.set_kv8(fmt)
     om.fill_kv(n_ctx, 77)
-    st = cq.State(cfg, w, kv_dtype=cq.KV_INT8)
+    st = cq.State(cfg, w, kv_dtype=fmt)
     st.fill_kv(n_ctx, 77)
     tok = int(cq.lib.cq_synth_uniform(44, 0, 0, cfg.vocab_size))
     hist, checked = [], 0
@@ -165,16 +197,17 @@ def test_decode_kv8_7b_int4_32k_matches_oracle():
     w.free()
 
 
+@pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("quant,n", [(2, 70), (1, 600), (0, 17)])
-def test_prefill_kv8_matches_oracle(quant, n):
-    """Batched prefill into an int8 cache (GEMM epilogue quantization, both
-    the split-K and the single-pass epilogue) against the oracle's int8 mode
-    run token by token."""
+def test_prefill_kv8_matches_oracle(quant, n, fmt):
+    """Batched prefill into a quantized cache (GEMM epilogue quantization,
+    both the split-K and the single-pass epilogue) against the oracle's
+    matching mode run token by token."""
     cfg = tiny_config(quant, max_seq_len=1024)
     w = cq.synth_weights(cfg, 6)
     om = orc.Model.synth(cfg, 6, cfg.max_seq_len)
-    om.set_kv8(True)
-    st = cq.State(cfg, w, kv_dtype=cq.KV_INT8)
+    om.set_kv8(fmt)
+    st = cq.State(cfg, w, kv_dtype=fmt)
     prompt = [int(cq.lib.cq_synth_uniform(8, 0, i, cfg.vocab_size)) for i in range(n)]
     ot = None
     for i, t in enumerate(prompt):
@@ -186,19 +219,20 @@ def test_prefill_kv8_matches_oracle(quant, n):
     for layer in range(cfg.n_layers):
         for h in range(cfg.n_kv_heads):
             for kind in (0, 1):
-                assert rel_err(st.kv_read(layer, h, kind, n), om.kv(layer, h, kind, n)) <= TOL
+                assert _kv_match(st.kv_read(layer, h, kind, n), om.kv(layer, h, kind, n), fmt)
     st.free()
     w.free()
 
 
+@pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("model,quant,layers,n,n_ctx", [("7B", "int4", 2, 130, 2000), ("7B", "int4", 2, 2100, 0),
                                                         ("0.5B", "int8", 4, 300, 0)])
-def test_prefill_kv8_matches_decode_kv8_real_shapes(model, quant, layers, n, n_ctx):
+def test_prefill_kv8_matches_decode_kv8_real_shapes(model, quant, layers, n, n_ctx, fmt):
     cfg = cq.preset(model, quant).replace(n_layers=layers)
     w = cq.synth_weights(cfg, 0x5157454E)
     prompt = [int(cq.lib.cq_synth_uniform(31, 0, i, cfg.vocab_size)) for i in range(n)]
-    ref = cq.State(cfg, w, kv_dtype=cq.KV_INT8)
-    st = cq.State(cfg, w, kv_dtype=cq.KV_INT8)
+    ref = cq.State(cfg, w, kv_dtype=fmt)
+    st = cq.State(cfg, w, kv_dtype=fmt)
     if n_ctx:
         ref.fill_kv(n_ctx, 77)
         st.fill_kv(n_ctx, 77)
@@ -211,7 +245,7 @@ def test_prefill_kv8_matches_decode_kv8_real_shapes(model, quant, layers, n, n_c
         assert gt == rt
     for layer in (0, layers - 1):
         for kind in (0, 1):
-            assert rel_err(st.kv_read(layer, 0, kind, n_ctx + n), ref.kv_read(layer, 0, kind, n_ctx + n)) <= TOL
+            assert _kv_match(st.kv_read(layer, 0, kind, n_ctx + n), ref.kv_read(layer, 0, kind, n_ctx + n), fmt)
     st.free()
     ref.free()
     w.free()

@@ -291,6 +291,104 @@ def test_model_kv8_layer0_rows_are_quantized_fp16_rows():
             np.testing.assert_array_equal(s, ws)
 
 
+# ------------------------------------------------------------- fp8 KV
+def test_e4m3_decode_matches_torch_on_every_code():
+    """All 256 E4M3 codes against torch.float8_e4m3fn (OCP e4m3fn: bias 7,
+    subnormals m * 2^-9, 0x7F / 0xFF NaN, largest finite 448)."""
+    import torch
+    codes = np.arange(256, dtype=np.uint8)
+    ref = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy()
+    got = orc.e4m3_decode(codes)
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(ref))
+    np.testing.assert_array_equal(got[~np.isnan(ref)], ref[~np.isnan(ref)])
+    assert got[0x7E] == 448 and got[0x01] == 2.0 ** -9 and got[0x08] == 2.0 ** -6
+
+
+def test_e4m3_encode_matches_torch():
+    """Round to nearest, ties to even: every finite fp16 value within +-448,
+    every midpoint between adjacent codes (the ties) and their neighbours one
+    fp32 ulp away, and random values, against torch's conversion."""
+    import torch
+    fin = orc.e4m3_decode(np.arange(0x7F, dtype=np.uint8))
+    mids = ((fin[1:] + fin[:-1]) / 2).astype(np.float32)
+    h = np.arange(0, 0x7C00, dtype=np.uint16).view(np.float16).astype(np.float32)
+    h = h[h <= 448]
+    x = np.concatenate([h, mids, np.nextafter(mids, np.float32(0)), np.nextafter(mids, np.float32(1e9)),
+                        np.random.default_rng(0).uniform(0, 448, 20000).astype(np.float32)])
+    x = np.concatenate([x, -x]).astype(np.float32)
+    want = torch.from_numpy(x).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    np.testing.assert_array_equal(orc.e4m3_encode(x), want)
+    # ties go to the even mantissa: 1.0625 -> 1.0, 1.1875 -> 1.25, 2^-10 -> 0, 3 * 2^-10 -> 2^-8
+    np.testing.assert_array_equal(orc.e4m3_decode(orc.e4m3_encode(np.float32([1.0625, 1.1875, 2.0 ** -10, 3 * 2.0 ** -10]))),
+                                  np.float32([1.0, 1.25, 0.0, 2.0 ** -8]))
+
+
+def test_quant_row_f8_known_answers_and_error_bound():
+    """s = max|x| / 448 (the largest element maps to +-448, code 0x7E / 0xFE);
+    an all-zero row keeps s = 0; every element within half a code step of
+    x / s (relative 2^-4 for normals, 2^-10 absolute below 2^-6)."""
+    x = np.array([[448, 1.0625, -1.1875, 2.0 ** -10, 0, 3 * 2.0 ** -10], [0] * 6], dtype=np.float16)
+    q, s = orc.quant_rows_f8(x)
+    assert s[0] == 1.0 and s[1] == 0 and not q[1].any()
+    assert list(q[0]) == list(orc.e4m3_encode(np.float32([448, 1.0, -1.25, 0.0, 0.0, 2.0 ** -8])))
+    assert q[0][0] == 0x7E and q[0][2] & 0x80
+    rng = np.random.default_rng(4)
+    x = (rng.standard_normal((200, 128)) * rng.uniform(0.01, 30, (200, 1))).astype(np.float16)
+    q, s = orc.quant_rows_f8(x)
+    np.testing.assert_array_equal(s, np.abs(x.astype(np.float32)).max(1) / np.float32(448))
+    r = x.astype(np.float64) / s[:, None].astype(np.float64)
+    dq = orc.e4m3_decode(q).astype(np.float64)
+    assert np.all(np.abs(dq - r) <= np.maximum(np.abs(r) * 2.0 ** -4, 2.0 ** -10) * (1 + 1e-5))
+    assert np.all(np.abs(dq).max(1) == 448)
+
+
+@pytest.mark.parametrize("T", [1, 33, 300])
+def test_attention_f8_matches_textbook_on_dequantized_cache(T):
+    rng = np.random.default_rng(T + 6)
+    H, KV, hd = 14, 2, 64
+    q = rng.standard_normal(H * hd).astype(np.float16)
+    K = rng.standard_normal((KV, 320, hd)).astype(np.float16)
+    V = rng.standard_normal((KV, 320, hd)).astype(np.float16)
+    Kq, Ks = orc.quant_rows_f8(K.reshape(-1, hd))
+    Vq, Vs = orc.quant_rows_f8(V.reshape(-1, hd))
+    Kq, Vq, Ks, Vs = Kq.reshape(KV, 320, hd), Vq.reshape(KV, 320, hd), Ks.reshape(KV, 320), Vs.reshape(KV, 320)
+    kd = orc.e4m3_decode(Kq).astype(np.float64) * Ks[..., None]
+    vd = orc.e4m3_decode(Vq).astype(np.float64) * Vs[..., None]
+    want = _attn_np(q, kd, vd, H, KV, hd, T)
+    for mode in (0, 1):
+        got = orc.attention_i8(q, Kq, Ks, Vq, Vs, H, KV, hd, T, mode, fmt=2).astype(np.float64)
+        tol = 2e-3 if mode == 1 else 1e-2
+        assert np.max(np.abs(got - want)) <= tol * max(1.0, np.max(np.abs(want)))
+    # the fp8 cache attends to a different cache than the int8 one: not interchangeable
+    Kq8, Ks8 = orc.quant_rows_i8(K.reshape(-1, hd))
+    assert not np.array_equal(orc.e4m3_decode(Kq).ravel() * np.repeat(Ks, hd),
+                              Kq8.astype(np.float32).ravel() * np.repeat(Ks8, hd))
+
+
+def test_model_kv_f8_layer0_rows_are_quantized_fp16_rows():
+    """As for int8: layer 0 of the E4M3 model stores exactly the E4M3
+    quantization of the fp16 model's rows; logits stay close."""
+    from tests.conftest import tiny_config
+    cfg = tiny_config(1)
+    a = orc.Model.synth(cfg, 5, 64)
+    b = orc.Model.synth(cfg, 5, 64)
+    b.set_kv8(2)
+    toks = [3, 77, 1000, 5, 9, 2000, 31]
+    for i, t in enumerate(toks):
+        a.forward(t, i, [])
+        b.forward(t, i, [])
+        la, lb = a.logits().astype(np.float64), b.logits().astype(np.float64)
+        assert np.max(np.abs(la - lb)) <= 1e-1 * np.max(np.abs(la))
+    for kind in (0, 1):
+        for h in range(cfg.n_kv_heads):
+            q, s = b.kv8(0, h, kind, len(toks))
+            wq, ws = orc.quant_rows_f8(a.kv(0, h, kind, len(toks)))
+            np.testing.assert_array_equal(q.view(np.uint8), wq)
+            np.testing.assert_array_equal(s, ws)
+            np.testing.assert_array_equal(b.kv(0, h, kind, len(toks)),
+                                          (orc.e4m3_decode(wq) * ws[:, None]).astype(np.float16))
+
+
 # ---------------------------------------------------------------- argmax
 def test_argmax_ties_lowest_index_and_specials():
     """kernels.cu:907-961: ties -> lowest index; NaN sorts above +inf."""
