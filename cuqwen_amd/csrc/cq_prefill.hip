@@ -13,16 +13,15 @@
 //   pf_gemm<RESID>  O-proj + residual (kernels.cu:640-687)
 //   pf_norm_rows, pf_gemm<SWIGLU> (kernels.cu:523-585), pf_gemm<RESID> (down)
 // The GEMMs are M > 1, so they run on the matrix cores: each wave dequantizes
-// its weight rows in registers (int4 / int8 to exact small-integer fp16) as
-// the A operand of v_mfma_f32_16x16x32_f16 and takes 16-token slices of the
-// activation tile, staged in LDS, as the B operand.  Quantized rows are
-// summed per 128-wide group in fp32 and scaled by the group's fp16 scale, as
-// the decode path does per chunk.
+// its weight rows in registers (int4 / int8 to exact small-integer fp16,
+// times the group's fp16 scale) as the A operand of v_mfma_f32_16x16x32_f16
+// and takes 16-token slices of the activation tile, staged in LDS straight
+// from global memory, as the B operand.
 //
 // Activation layout: the inputs of the GEMMs (normed x, attention output,
-// SwiGLU output) are stored with each group of 8 consecutive elements in the
-// order [0,4,1,5,2,6,3,7] -- the order in which the int4 / int8 unpack yields
-// weight pairs -- so neither operand needs a shuffle in the main loop.
+// SwiGLU output) are stored in the order in which the weights' unpack yields
+// pairs (int4: each 8-group as [0,4,1,5,2,6,3,7] with the odd elements / 16;
+// int8 / fp16: natural), so neither operand needs a shuffle in the main loop.
 #include "cq_attention.h"
 #include "cq_gemv.h"
 
@@ -32,11 +31,7 @@
 namespace cq {
 
 constexpr int kPfThreads = 256;   // 4 waves
-constexpr int kPfBM = 64;         // tokens per GEMM block (4 slices of 16)
-constexpr int kPfRowsPerWave = 32;
-constexpr int kPfBN = 4 * kPfRowsPerWave;   // weight rows per GEMM block
 constexpr int kPfK = 128;         // K per main-loop step (one quantization group)
-constexpr int kPfLdsStride = kPfK + 8;     // halves per token row in LDS (16-byte skew)
 constexpr int kPfTargetBlocks = 512;       // split K below this many blocks (2 per CU)
 constexpr int kPfMaxSplit = 8;
 
@@ -172,30 +167,62 @@ __device__ __forceinline__ void pf_load_w(const PfGemmArgs& a, const char* rowp,
   for (int i = 0; i < L; ++i) w[i] = load_u4(p + i * 16);
 }
 
+// Tile shape per weight format: RT 16-row slices per wave and matrix (the
+// weight registers of two steps in flight bound it), 8 token slices of 16 per
+// wave; a block is 4 waves over the same 128 tokens.  SwiGLU waves hold RT/2
+// gate and RT/2 up slices of the same output rows.
+template <int Q> struct PfTile { static constexpr int RT = Q == CQ_QUANT_INT4 ? 4 : 2; };
+constexpr int kPfTT = 4;                         // token slices per wave
+constexpr int kPfTok = 16 * kPfTT;               // tokens per block
+template <int Q, int MODE> struct PfShape {
+  static constexpr int NMAT = MODE == GM_SWIGLU ? 2 : 1;
+  static constexpr int RT = PfTile<Q>::RT / NMAT;   // row slices per matrix
+  static constexpr int WROWS = RT * 16;              // output rows per wave
+  static constexpr int BN = 4 * WROWS;               // output rows per block
+};
+
+// The block's (row block, token block) from its dispatch index, so that all
+// token blocks of a row block run on one XCD and share its weight rows in
+// that XCD's L2: dispatch goes round-robin over the 8 XCDs, so XCD x runs
+// blocks x, x + 8, ...; those take a contiguous range of row-major tiles.
+__device__ __forceinline__ void pf_block_tile(int n_tb, int* rb, int* tb) {
+  const int id = blockIdx.x, n = gridDim.x;
+  const int xcd = id & 7, k = id >> 3, base = n >> 3, rem = n & 7;
+  const int L = xcd * base + min(xcd, rem) + k;
+  *rb = L / n_tb;
+  *tb = L % n_tb;
+}
+
 // C^T tile of a wave: NMAT matrices (SwiGLU: gate and up) x RT row slices of
-// 16 x 4 token slices of 16; lane holds rows 4*(lane/16)+v, token lane%16.
+// 16 x 8 token slices of 16; lane holds rows 4*(lane/16)+v, token lane%16.
+// The group scale multiplies the unpacked weights (half(q * s), one packed
+// multiply per pair), so the matrix cores accumulate the whole K range
+// directly into the tile.
 template <int Q, int MODE, bool SPLIT>
-__global__ __launch_bounds__(kPfThreads) void pf_gemm_kernel(const PfGemmArgs a) {
-  constexpr int NMAT = MODE == GM_SWIGLU ? 2 : 1;
-  constexpr int RT = MODE == GM_SWIGLU ? 1 : 2;   // SwiGLU: 16 gate + 16 up rows per wave
-  constexpr int WROWS = RT * 16;
-  constexpr int BN = 4 * WROWS;
+__global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs a) {
+  using SH = PfShape<Q, MODE>;
+  constexpr int NMAT = SH::NMAT, RT = SH::RT, WROWS = SH::WROWS, BN = SH::BN, TT = kPfTT;
   constexpr int L = PfW<Q>::LOADS;
-  __shared__ _Float16 xs[2][kPfBM * kPfLdsStride];   // double-buffered activation tile
-  __shared__ _Float16 ot[MODE == GM_QKV ? kPfBN * kPfBM : 1];   // QKV epilogue tile (rows x tokens)
+  constexpr int XS = kPfTok * kPfK;                         // halves of one activation stage
+  constexpr int OT = MODE == GM_QKV ? BN * kPfTok : 0;      // QKV epilogue tile (rows x tokens)
+  __shared__ __align__(16) _Float16 smem[3 * XS > OT ? 3 * XS : OT];
+  _Float16* xs0 = smem;
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
   const int r = lane & 15, j = lane >> 4;
-  const int m0 = blockIdx.y * kPfBM;
-  const int nb0 = blockIdx.x * BN;             // first output row of the block
+  const int n_tb = (a.M + kPfTok - 1) / kPfTok;
+  int rb, tb;
+  pf_block_tile(n_tb, &rb, &tb);
+  const int m0 = tb * kPfTok;
+  const int nb0 = rb * BN;                     // first output row of the block
   const int nw0 = nb0 + wave * WROWS;          // first output row of the wave
   const int K = a.K, nks = K / kPfK;
   // split-K: block z of gridDim.z sums K steps [kb, ke) into an fp32 partial
   const int kb = SPLIT ? (int)((int64_t)blockIdx.z * nks / gridDim.z) : 0;
   const int ke = SPLIT ? (int)((int64_t)(blockIdx.z + 1) * nks / gridDim.z) : nks;
 
-  // weight row pointers of the lane (A operand row r of each slice)
+  // weight row (A operand row r of each slice) and its scale row
   const char* rowp[NMAT][RT];
-  const _Float16* srow[NMAT][RT][4];   // scale rows of the lane's 4 output rows
+  const _Float16* srow[NMAT][RT];
 #pragma unroll
   for (int mt = 0; mt < NMAT; ++mt)
 #pragma unroll
@@ -204,123 +231,132 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm_kernel(const PfGemmArgs a)
       const int mat = MODE == GM_SWIGLU ? mt : pf_mat(a, row, &local);
       if (MODE == GM_SWIGLU) local = row;
       const int64_t rbytes = Q == CQ_QUANT_INT4 ? K / 2 : Q == CQ_QUANT_INT8 ? K : 2 * K;
-      rowp[mt][rt] = reinterpret_cast<const char*>(a.W[mat]) + (int64_t)local * rbytes;
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        int l2, row2 = min(nw0 + rt * 16 + 4 * j + v, a.N - 1);
-        const int mat2 = MODE == GM_SWIGLU ? mt : pf_mat(a, row2, &l2);
-        if (MODE == GM_SWIGLU) l2 = row2;
-        srow[mt][rt][v] = Q == CQ_QUANT_FP16 ? nullptr : a.S[mat2] + (int64_t)l2 * (K / kGroup);
-      }
+      rowp[mt][rt] = reinterpret_cast<const char*>(sel3(a.W, mat)) + (int64_t)local * rbytes;
+      srow[mt][rt] = Q == CQ_QUANT_FP16 ? nullptr : sel3(a.S, mat) + (int64_t)local * (K / kGroup);
     }
 
-  // activation tile loader: thread t moves 4 x 16 bytes of the 64 x 128 tile
-  auto x_load = [&](int ks, u4_t* v) {
+  // Activation tiles go global -> LDS directly (global_load_lds_dwordx4, no
+  // registers), three stages deep.  A stage holds 128 token rows of 256 bytes;
+  // 16-byte slot s of row t holds K chunk s ^ (t & 15), so the B-operand
+  // reads (16 rows at one chunk) hit 16 different bank groups.  Load q of a
+  // step (q = i * 4 + wave, i < 8) fills rows 4q .. 4q + 3: lane l writes
+  // row 4q + l / 16, slot l % 16.
+  auto x_issue = [&](int ks, int stg) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = threadIdx.x + i * kPfThreads;   // 16-byte chunk of the tile, 16 per token row
-      const int m = min(m0 + c / 16, a.M - 1);
-      v[i] = load_u4(a.A + (int64_t)m * K + ks * kPfK + (c % 16) * 8);
-    }
-  };
-  auto x_store = [&](int buf, const u4_t* v) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = threadIdx.x + i * kPfThreads;
-      *reinterpret_cast<u4_t*>(&xs[buf][(c / 16) * kPfLdsStride + (c % 16) * 8]) = v[i];
+    for (int i = 0; i < kPfTok / 16; ++i) {
+      const int q = i * 4 + wave, t = 4 * q + (lane >> 4), c = (lane & 15) ^ (t & 15);
+      const int m = min(m0 + t, a.M - 1);
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(a.A + (int64_t)m * K + ks * kPfK + c * 8),
+                                       (__attribute__((address_space(3))) void*)(
+                                           xs0 + stg * XS + q * 512),
+                                       16, 0, 0);
     }
   };
 
-  f4_t acc[NMAT][RT][4];
+  f4_t acc[NMAT][RT][TT];
 #pragma unroll
   for (int mt = 0; mt < NMAT; ++mt)
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt) acc[mt][rt][tt] = f4_t{0.f, 0.f, 0.f, 0.f};
+      for (int tt = 0; tt < TT; ++tt) acc[mt][rt][tt] = f4_t{0.f, 0.f, 0.f, 0.f};
 
-  // Two-step-ahead pipeline, unrolled by two so both register sets keep
-  // compile-time indices: at step k the weights of step k+2 are requested
-  // right after step k's weights are unpacked, the activations of step k+2
-  // at the start of step k (stored into LDS at the end of step k+1).
-  u4_t xv[2][4], wv[2][NMAT][RT][L];
-  auto load_w_step = [&](int ks, u4_t (&w)[NMAT][RT][L]) {
+  // Two-step-ahead pipeline: at step k (after its barrier) the weights and
+  // activations of step k+2 are requested; the K loop is unrolled by two so
+  // the two weight register sets keep compile-time indices.  Loads of the
+  // vector memory counter, per step and wave: WL weight / scale loads, 8
+  // activation loads.  Before step k's barrier a wave waits until at most
+  // one later step's loads are outstanding (its own step-k activation
+  // writes have landed in LDS); the barrier then makes all waves' visible.
+  constexpr int WL = NMAT * RT * (L + (Q != CQ_QUANT_FP16 ? 1 : 0));
+  constexpr int VMC = WL + kPfTok / 16;
+  static_assert(VMC < 64, "vmcnt range");
+  u4_t wv[2][NMAT][RT][L];
+  _Float16 sv[2][NMAT][RT];
+  auto load_w_step = [&](int ks, u4_t (&w)[NMAT][RT][L], _Float16 (&s)[NMAT][RT]) {
 #pragma unroll
     for (int mt = 0; mt < NMAT; ++mt)
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt) pf_load_w<Q>(a, rowp[mt][rt], ks, j, w[mt][rt]);
+      for (int rt = 0; rt < RT; ++rt) {
+        pf_load_w<Q>(a, rowp[mt][rt], ks, j, w[mt][rt]);
+        if constexpr (Q != CQ_QUANT_FP16) s[mt][rt] = srow[mt][rt][ks];
+      }
   };
-  x_load(kb, xv[0]);
-  x_load(min(kb + 1, ke - 1), xv[1]);
-  load_w_step(kb, wv[0]);
-  load_w_step(min(kb + 1, ke - 1), wv[1]);
-  x_store(0, xv[0]);
-  __syncthreads();
+  load_w_step(kb, wv[0], sv[0]);
+  x_issue(kb, 0);
+  if (kb + 1 < ke) {
+    load_w_step(kb + 1, wv[1], sv[1]);
+    x_issue(kb + 1, 1);
+  }
 
   const UnpackRegs uk = unpack_regs();
   auto step = [&](auto I, int ks) {
-    constexpr int S = decltype(I)::value;   // register set and LDS buffer of this step
-    x_load(min(ks + 2, ke - 1), xv[S]);
-    _Float16 sc[NMAT][RT][4];
-    if constexpr (Q != CQ_QUANT_FP16) {
+    constexpr int S = decltype(I)::value;   // weight register set of this step
+    const int stg = (ks - kb) % 3;
+    // simm16 of s_waitcnt on gfx9: vmcnt in bits [3:0] and [15:14], expcnt
+    // [6:4] and lgkmcnt [11:8] left at their maxima
+    if (ks + 1 < ke) __builtin_amdgcn_s_waitcnt(0x0F70 | (VMC & 15) | ((VMC >> 4) << 14));
+    else __builtin_amdgcn_s_waitcnt(0x0F70);
+    __builtin_amdgcn_s_barrier();
+    const _Float16* xb0 = xs0 + stg * XS;
+    h2_t s2[NMAT][RT];
+    u4_t w[NMAT][RT][L];
 #pragma unroll
-      for (int mt = 0; mt < NMAT; ++mt)
+    for (int mt = 0; mt < NMAT; ++mt)
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt)
+      for (int rt = 0; rt < RT; ++rt) {
+        s2[mt][rt] = h2_t{sv[S][mt][rt], sv[S][mt][rt]};
 #pragma unroll
-          for (int v = 0; v < 4; ++v) sc[mt][rt][v] = srow[mt][rt][v][ks];
+        for (int i = 0; i < L; ++i) w[mt][rt][i] = wv[S][mt][rt][i];
+      }
+    if (ks + 2 < ke) {
+      load_w_step(ks + 2, wv[S], sv[S]);
+      x_issue(ks + 2, (ks + 2 - kb) % 3);
     }
-    h8_t wa[NMAT][RT][4];
+    // B fragments of sub-step s4 + 1 are read while sub-step s4's weights
+    // are unpacked and multiplied: with one wave per SIMD nothing else would
+    // cover the LDS latency
+    auto read_b = [&](int s4, h8_t* xb) {
 #pragma unroll
-    for (int mt = 0; mt < NMAT; ++mt)
-#pragma unroll
-      for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-        for (int s4 = 0; s4 < 4; ++s4) wa[mt][rt][s4] = pf_unpack<Q>(wv[S][mt][rt], s4, uk.m_lo, uk.m_hi, uk.magic);
-    load_w_step(min(ks + 2, ke - 1), wv[S]);
-    f4_t part[NMAT][RT][4];
-#pragma unroll
-    for (int mt = 0; mt < NMAT; ++mt)
-#pragma unroll
-      for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-        for (int tt = 0; tt < 4; ++tt)
-          part[mt][rt][tt] = Q == CQ_QUANT_FP16 ? acc[mt][rt][tt] : f4_t{0.f, 0.f, 0.f, 0.f};
+      for (int tt = 0; tt < TT; ++tt)   // row tt*16 + r, K chunk 4j + s4 at slot (4j + s4) ^ r
+        xb[tt] = *reinterpret_cast<const h8_t*>(&xb0[(tt * 16 + r) * kPfK + (((4 * j + s4) ^ r) * 8)]);
+    };
 #pragma unroll
     for (int s4 = 0; s4 < 4; ++s4) {
-      h8_t xb[4];
-#pragma unroll
-      for (int tt = 0; tt < 4; ++tt)
-        xb[tt] = *reinterpret_cast<const h8_t*>(&xs[S][(tt * 16 + r) * kPfLdsStride + j * 32 + s4 * 8]);
+      h8_t xb[1][TT];
+      read_b(s4, xb[0]);
+      h8_t wa[NMAT][RT];
 #pragma unroll
       for (int mt = 0; mt < NMAT; ++mt)
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-          for (int tt = 0; tt < 4; ++tt)
-            part[mt][rt][tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[mt][rt][s4], xb[tt], part[mt][rt][tt], 0, 0, 0);
-    }
-#pragma unroll
-    for (int mt = 0; mt < NMAT; ++mt)
-#pragma unroll
-      for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-        for (int tt = 0; tt < 4; ++tt) {
-          if constexpr (Q == CQ_QUANT_FP16) {
-            acc[mt][rt][tt] = part[mt][rt][tt];
-          } else {
-#pragma unroll
-            for (int v = 0; v < 4; ++v) acc[mt][rt][tt][v] = fmaf((float)sc[mt][rt][v], part[mt][rt][tt][v], acc[mt][rt][tt][v]);
+        for (int rt = 0; rt < RT; ++rt) {
+          h8_t u = pf_unpack<Q>(w[mt][rt], s4, uk.m_lo, uk.m_hi, uk.magic);
+          if constexpr (Q != CQ_QUANT_FP16) {
+            u4_t uu = __builtin_bit_cast(u4_t, u);
+            uu.x = as_u32(as_h2(uu.x) * s2[mt][rt]);
+            uu.y = as_u32(as_h2(uu.y) * s2[mt][rt]);
+            uu.z = as_u32(as_h2(uu.z) * s2[mt][rt]);
+            uu.w = as_u32(as_h2(uu.w) * s2[mt][rt]);
+            u = __builtin_bit_cast(h8_t, uu);
           }
+          wa[mt][rt] = u;
         }
-    // the activations of step ks+1 (requested one step ago) into the other buffer
-    if (ks + 1 < ke) x_store(S ^ 1, xv[S ^ 1]);
-    __syncthreads();
+#pragma unroll
+      for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+        for (int mt = 0; mt < NMAT; ++mt)
+#pragma unroll
+          for (int rt = 0; rt < RT; ++rt)
+            acc[mt][rt][tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[mt][rt], xb[0][tt], acc[mt][rt][tt], 0, 0, 0);
+    }
   };
-  for (int ks = kb; ks < ke; ks += 2) {
+  int ks = kb;
+  for (; ks + 1 < ke; ks += 2) {
     step(std::integral_constant<int, 0>{}, ks);
-    if (ks + 1 < ke) step(std::integral_constant<int, 1>{}, ks + 1);
+    step(std::integral_constant<int, 1>{}, ks + 1);
   }
+  if (ks < ke) step(std::integral_constant<int, 0>{}, ks);
+  __syncthreads();   // every wave's last LDS reads are done before the QKV epilogue reuses the buffers
 
   if constexpr (SPLIT) {
     // fp32 partial [z][mat][M][N]; the split epilogue sums and finishes
@@ -329,13 +365,16 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm_kernel(const PfGemmArgs a)
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-        for (int tt = 0; tt < 4; ++tt)
+        for (int tt = 0; tt < TT; ++tt) {
+          const int n = nw0 + rt * 16 + 4 * j, m = m0 + tt * 16 + r;
+          if (m < a.M && n + 3 < a.N) {
+            *reinterpret_cast<f4_t*>(&a.part[(((int64_t)blockIdx.z * NMAT + mt) * a.M + m) * a.N + n]) = acc[mt][rt][tt];
+          } else if (m < a.M) {
 #pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            const int n = nw0 + rt * 16 + 4 * j + v, m = m0 + tt * 16 + r;
-            if (n < a.N && m < a.M)
-              a.part[(((int64_t)blockIdx.z * NMAT + mt) * a.M + m) * a.N + n] = acc[mt][rt][tt][v];
+            for (int v = 0; v < 4; ++v)
+              if (n + v < a.N) a.part[(((int64_t)blockIdx.z * NMAT + mt) * a.M + m) * a.N + n + v] = acc[mt][rt][tt][v];
           }
+        }
     return;
   }
 
@@ -345,7 +384,7 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm_kernel(const PfGemmArgs a)
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt)
+      for (int tt = 0; tt < TT; ++tt)
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const int n = nw0 + rt * 16 + 4 * j + v, m = m0 + tt * 16 + r;
@@ -356,24 +395,29 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm_kernel(const PfGemmArgs a)
         }
   } else if constexpr (MODE == GM_SWIGLU) {
 #pragma unroll
-    for (int tt = 0; tt < 4; ++tt)
+    for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int n = nw0 + 4 * j + v, m = m0 + tt * 16 + r;
-        if (n < a.N && m < a.M) {
-          const float s = a.inv[m];
-          const float g = acc[0][0][tt][v] * s, u = acc[1][0][tt][v] * s;
-          const float sig = 1.f / (1.f + expf(-g));   // kernels.cu:566
-          a.out[(int64_t)m * a.N + pf_pos(n, Q == CQ_QUANT_INT4)] = pf_val((float)(_Float16)((g * sig) * u), n, Q == CQ_QUANT_INT4);
+      for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int n = nw0 + rt * 16 + 4 * j + v, m = m0 + tt * 16 + r;
+          if (n < a.N && m < a.M) {
+            const float s = a.inv[m];
+            const float g = acc[0][rt][tt][v] * s, u = acc[1][rt][tt][v] * s;
+            const float sig = 1.f / (1.f + expf(-g));   // kernels.cu:566
+            a.out[(int64_t)m * a.N + pf_pos(n, Q == CQ_QUANT_INT4)] =
+                pf_val((float)(_Float16)((g * sig) * u), n, Q == CQ_QUANT_INT4);
+          }
         }
-      }
   } else {
-    // QKV: scale, bias, fp16 into LDS; then pairs (i, i + hd/2) of each head
-    // rotate (q, k) and go to Q or the KV cache
+    // QKV: norm scale, bias, fp16 into LDS (over the activation buffers, all
+    // reads of which finished at the loop's last barrier); then pairs
+    // (i, i + hd/2) of each head rotate (q, k) and go to Q or the KV cache
+    _Float16* ot = smem;
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt)
+      for (int tt = 0; tt < TT; ++tt)
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const int nl = wave * WROWS + rt * 16 + 4 * j + v, ml = tt * 16 + r;
@@ -382,42 +426,42 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm_kernel(const PfGemmArgs a)
           const int mat = pf_mat(a, min(n, a.N - 1), &local);
           const _Float16* b = a.bias[mat];
           const float y = acc[0][rt][tt][v] * a.inv[m] + (b ? (float)b[local] : 0.f);
-          ot[nl * kPfBM + ml] = (_Float16)y;   // q/k/v are fp16 before RoPE (kernels.cu:470)
+          ot[nl * kPfTok + ml] = (_Float16)y;   // q/k/v are fp16 before RoPE (kernels.cu:470)
         }
     __syncthreads();
     const int hd = a.head_dim, half = hd / 2;
-    for (int idx = threadIdx.x; idx < (kPfBN / 2) * kPfBM; idx += kPfThreads) {
-      const int ml = idx % kPfBM, pi = idx / kPfBM;   // pair pi of the block's 64 pairs
+    for (int idx = threadIdx.x; idx < (BN / 2) * kPfTok; idx += kPfThreads) {
+      const int ml = idx % kPfTok, pi = idx / kPfTok;   // pair pi of the block's BN/2 pairs
       const int nl0 = (pi / half) * hd + pi % half, nl1 = nl0 + half;
       const int n0 = nb0 + nl0, m = m0 + ml;
       if (n0 >= a.N || m >= a.M) continue;
       int local;
       const int mat = pf_mat(a, n0, &local);
-      float y0 = (float)ot[nl0 * kPfBM + ml], y1 = (float)ot[nl1 * kPfBM + ml];
+      float y0 = (float)ot[nl0 * kPfTok + ml], y1 = (float)ot[nl1 * kPfTok + ml];
       const int pos = a.pos0 + m, i = local % hd;
       if (mat < 2) rope_rotate(y0, y1, pos, a.inv_freq[i]);
       if (a.kcache8 && mat > 0) {
         // quantized cache: rotated values back into the tile, quantized per head below
-        ot[nl0 * kPfBM + ml] = (_Float16)y0;
-        ot[nl1 * kPfBM + ml] = (_Float16)y1;
+        ot[nl0 * kPfTok + ml] = (_Float16)y0;
+        ot[nl1 * kPfTok + ml] = (_Float16)y1;
       } else {
         pf_qkv_store(a, mat, local, m, (_Float16)y0, (_Float16)y1);
       }
     }
     if (a.kcache8) {
       __syncthreads();
-      const int heads = kPfBN / hd;
-      for (int idx = threadIdx.x; idx < heads * kPfBM; idx += kPfThreads) {
-        const int hb = idx / kPfBM, ml = idx % kPfBM;
+      const int heads = BN / hd;
+      for (int idx = threadIdx.x; idx < heads * kPfTok; idx += kPfThreads) {
+        const int hb = idx / kPfTok, ml = idx % kPfTok;
         const int n0 = nb0 + hb * hd, m = m0 + ml;
         if (n0 >= a.N || m >= a.M) continue;
         int local;
         const int mat = pf_mat(a, n0, &local);
         if (mat == 0) continue;
         float amax = 0.f;
-        for (int d = 0; d < hd; ++d) amax = fmaxf(amax, fabsf((float)ot[(hb * hd + d) * kPfBM + ml]));
+        for (int d = 0; d < hd; ++d) amax = fmaxf(amax, fabsf((float)ot[(hb * hd + d) * kPfTok + ml]));
         pf_kv8_store(a, mat, local / hd, a.pos0 + m, amax,
-                     [&](int d) { return (float)ot[(hb * hd + d) * kPfBM + ml]; });
+                     [&](int d) { return (float)ot[(hb * hd + d) * kPfTok + ml]; });
       }
     }
   }
@@ -647,24 +691,24 @@ int launch_pf_embed(const __half* embed, const int* tokens, int M, int dim, __ha
 
 template <int Q, int MODE>
 static int launch_pf_gemm_m(const PfGemmArgs& a, hipStream_t stream) {
-  const int bn = MODE == GM_SWIGLU ? 64 : kPfBN;
-  const int gx = (a.N + bn - 1) / bn, gy = (a.M + kPfBM - 1) / kPfBM;
+  const int bn = PfShape<Q, MODE>::BN;
+  const int gx = ((a.N + bn - 1) / bn) * ((a.M + kPfTok - 1) / kPfTok);   // row blocks x token blocks
   const int nks = a.K / kPfK, nmat = MODE == GM_SWIGLU ? 2 : 1;
   // split K until the grid holds ~2 blocks per CU (small M), within the workspace
   int S = 1;
-  const int blocks = gx * gy;
+  const int blocks = gx;
   if (blocks < kPfTargetBlocks && a.part) {
     S = std::min({kPfMaxSplit, (kPfTargetBlocks + blocks - 1) / blocks, nks});
     while (S > 1 && (size_t)S * nmat * a.M * a.N * sizeof(float) > a.part_bytes) --S;
   }
   if (S > 1) {
-    hipLaunchKernelGGL((pf_gemm_kernel<Q, MODE, true>), dim3(gx, gy, S), dim3(kPfThreads), 0, stream, a);
+    hipLaunchKernelGGL((pf_gemm_kernel<Q, MODE, true>), dim3(gx, 1, S), dim3(kPfThreads), 0, stream, a);
     CQ_HIP(hipGetLastError());
     const int64_t work = MODE == GM_QKV ? (int64_t)a.M * a.N / 2 : (int64_t)a.M * a.N;
     const int eb = (int)std::min<int64_t>((work + 255) / 256, 4096);
     hipLaunchKernelGGL((pf_split_epilogue<MODE>), dim3(eb), dim3(256), 0, stream, a, S);
   } else {
-    hipLaunchKernelGGL((pf_gemm_kernel<Q, MODE, false>), dim3(gx, gy), dim3(kPfThreads), 0, stream, a);
+    hipLaunchKernelGGL((pf_gemm_kernel<Q, MODE, false>), dim3(gx), dim3(kPfThreads), 0, stream, a);
   }
   CQ_HIP(hipGetLastError());
   return CQ_OK;
@@ -686,7 +730,7 @@ int launch_pf_gemm(const PfGemmArgs& a, hipStream_t stream) {
     if (!a.inv || !a.W[1] || !a.W[2] || !a.inv_freq) return fail(CQ_EINVAL, "prefill gemm: qkv operands");
     if (a.kcache8 ? (!a.vcache8 || !a.kscale || !a.vscale) : (!a.kcache || !a.vcache))
       return fail(CQ_EINVAL, "prefill gemm: qkv cache pointers");
-    if (kPfBN % a.head_dim || a.rows[0] % a.head_dim || a.rows[1] % a.head_dim || a.rows[0] + a.rows[1] + a.rows[2] != a.N)
+    if (PfShape<CQ_QUANT_FP16, GM_QKV>::BN % a.head_dim || a.rows[0] % a.head_dim || a.rows[1] % a.head_dim || a.rows[0] + a.rows[1] + a.rows[2] != a.N)
       return fail(CQ_EINVAL, "prefill gemm: qkv rows must be whole heads");
   }
   switch (a.quant) {

