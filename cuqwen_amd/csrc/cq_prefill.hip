@@ -30,7 +30,8 @@
 
 namespace cq {
 
-constexpr int kPfThreads = 256;   // 4 waves
+constexpr int kPfWaves = 8;
+constexpr int kPfThreads = kPfWaves * 64;
 constexpr int kPfK = 128;         // K per main-loop step (one quantization group)
 constexpr int kPfTargetBlocks = 512;       // split K below this many blocks (2 per CU)
 constexpr int kPfMaxSplit = 8;
@@ -167,18 +168,18 @@ __device__ __forceinline__ void pf_load_w(const PfGemmArgs& a, const char* rowp,
   for (int i = 0; i < L; ++i) w[i] = load_u4(p + i * 16);
 }
 
-// Tile shape per weight format: RT 16-row slices per wave and matrix (the
-// weight registers of two steps in flight bound it), 8 token slices of 16 per
-// wave; a block is 4 waves over the same 128 tokens.  SwiGLU waves hold RT/2
-// gate and RT/2 up slices of the same output rows.
-template <int Q> struct PfTile { static constexpr int RT = Q == CQ_QUANT_INT4 ? 4 : 2; };
-constexpr int kPfTT = 4;                         // token slices per wave
+// Tile shape: RT 16-row slices per wave (SwiGLU: RT/2 gate and RT/2 up
+// slices of the same output rows), 8 token slices of 16 per wave (the unpack
+// of a weight fragment is shared by 8 matrix instructions); a block is 8
+// waves over the same 128 tokens, two per SIMD.
+template <int Q> struct PfTile { static constexpr int RT = 2; };
+constexpr int kPfTT = 8;                         // token slices per wave
 constexpr int kPfTok = 16 * kPfTT;               // tokens per block
 template <int Q, int MODE> struct PfShape {
   static constexpr int NMAT = MODE == GM_SWIGLU ? 2 : 1;
   static constexpr int RT = PfTile<Q>::RT / NMAT;   // row slices per matrix
   static constexpr int WROWS = RT * 16;              // output rows per wave
-  static constexpr int BN = 4 * WROWS;               // output rows per block
+  static constexpr int BN = kPfWaves * WROWS;        // output rows per block
 };
 
 // The block's (row block, token block) from its dispatch index, so that all
@@ -239,12 +240,12 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
   // registers), three stages deep.  A stage holds 128 token rows of 256 bytes;
   // 16-byte slot s of row t holds K chunk s ^ (t & 15), so the B-operand
   // reads (16 rows at one chunk) hit 16 different bank groups.  Load q of a
-  // step (q = i * 4 + wave, i < 8) fills rows 4q .. 4q + 3: lane l writes
+  // step (q = i * waves + wave) fills rows 4q .. 4q + 3: lane l writes
   // row 4q + l / 16, slot l % 16.
   auto x_issue = [&](int ks, int stg) {
 #pragma unroll
-    for (int i = 0; i < kPfTok / 16; ++i) {
-      const int q = i * 4 + wave, t = 4 * q + (lane >> 4), c = (lane & 15) ^ (t & 15);
+    for (int i = 0; i < kPfTok / (4 * kPfWaves); ++i) {
+      const int q = i * kPfWaves + wave, t = 4 * q + (lane >> 4), c = (lane & 15) ^ (t & 15);
       const int m = min(m0 + t, a.M - 1);
       __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(a.A + (int64_t)m * K + ks * kPfK + c * 8),
                                        (__attribute__((address_space(3))) void*)(
@@ -269,7 +270,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
   // one later step's loads are outstanding (its own step-k activation
   // writes have landed in LDS); the barrier then makes all waves' visible.
   constexpr int WL = NMAT * RT * (L + (Q != CQ_QUANT_FP16 ? 1 : 0));
-  constexpr int VMC = WL + kPfTok / 16;
+  constexpr int VMC = WL + kPfTok / (4 * kPfWaves);
   static_assert(VMC < 64, "vmcnt range");
   u4_t wv[2][NMAT][RT][L];
   _Float16 sv[2][NMAT][RT];
