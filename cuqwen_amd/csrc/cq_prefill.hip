@@ -314,9 +314,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
       load_w_step(ks + 2, wv[S], sv[S]);
       x_issue(ks + 2, (ks + 2 - kb) % 3);
     }
-    // B fragments of sub-step s4 + 1 are read while sub-step s4's weights
-    // are unpacked and multiplied: with one wave per SIMD nothing else would
-    // cover the LDS latency
+    // B fragments of one sub-step (the other wave of the SIMD covers their
+    // LDS latency)
     auto read_b = [&](int s4, h8_t* xb) {
 #pragma unroll
       for (int tt = 0; tt < TT; ++tt)   // row tt*16 + r, K chunk 4j + s4 at slot (4j + s4) ^ r
@@ -324,8 +323,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
     };
 #pragma unroll
     for (int s4 = 0; s4 < 4; ++s4) {
-      h8_t xb[1][TT];
-      read_b(s4, xb[0]);
+      h8_t xb[TT];
+      read_b(s4, xb);
       h8_t wa[NMAT][RT];
 #pragma unroll
       for (int mt = 0; mt < NMAT; ++mt)
@@ -348,7 +347,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
         for (int mt = 0; mt < NMAT; ++mt)
 #pragma unroll
           for (int rt = 0; rt < RT; ++rt)
-            acc[mt][rt][tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[mt][rt], xb[0][tt], acc[mt][rt][tt], 0, 0, 0);
+            acc[mt][rt][tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[mt][rt], xb[tt], acc[mt][rt][tt], 0, 0, 0);
     }
   };
   int ks = kb;
