@@ -136,6 +136,14 @@ def _load():
                                ctypes.POINTER(ctypes.c_double)]),
         "cq_state_profile": (I32, [P, I32, I32, I32, ctypes.c_char_p, ctypes.POINTER(ctypes.c_double),
                                    ctypes.POINTER(ctypes.c_double), IP]),
+        "cq_tokenizer_load": (I32, [ctypes.c_char_p, ctypes.POINTER(P)]),
+        "cq_tokenizer_free": (I32, [P]),
+        "cq_tokenizer_encode": (I32, [P, ctypes.c_char_p, SZ, IP, I32, IP]),
+        "cq_tokenizer_decode": (I32, [P, IP, I32, ctypes.c_char_p, SZ, ctypes.POINTER(SZ)]),
+        "cq_tokenizer_token_id": (I32, [P, ctypes.c_char_p]),
+        "cq_tokenizer_vocab_size": (I32, [P]),
+        "cq_chat_template": (I32, [ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_char_p), I32, I32,
+                                   ctypes.c_char_p, SZ, ctypes.POINTER(SZ)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -157,7 +165,8 @@ EXPORTED = [
     "cq_fused_mlp_stage1", "cq_fused_mlp_stage2", "cq_compute_logits", "cq_apply_repetition_penalty",
     "cq_penalty_workspace_bytes", "cq_argmax", "cq_argmax_workspace_bytes", "cq_kv_k_offset", "cq_kv_v_offset",
     "cq_kv_cache_store", "cq_rope", "cq_gqa_attention_decode", "cq_attention_workspace_bytes", "cq_dequantize",
-    "cq_time_gemv", "cq_state_profile",
+    "cq_time_gemv", "cq_state_profile", "cq_tokenizer_load", "cq_tokenizer_free", "cq_tokenizer_encode",
+    "cq_tokenizer_decode", "cq_tokenizer_token_id", "cq_tokenizer_vocab_size", "cq_chat_template",
 ]
 
 
@@ -401,3 +410,113 @@ def free_qwen_state(state):
 def qwen_forward(token, pos, cfg, state, weights, history=None):
     """qwen_forward() (src/model.cu:183-223): one synchronous decode step -> sampled id."""
     return state.forward(token, pos, history)
+
+
+# ------------------------------------------------------------- tokenizer
+class Tokenizer:
+    """QwenTokenizer (include/tokenizer.h:18-41) over the C ABI: the
+    exporter's qwen25_bpe_ranks.json in, token ids out and back."""
+
+    def __init__(self, ranks_json_path):
+        self.handle = ctypes.c_void_p()
+        check(lib.cq_tokenizer_load(os.fsencode(ranks_json_path), ctypes.byref(self.handle)))
+
+    def encode(self, text):
+        data = text.encode("utf-8") if isinstance(text, str) else bytes(text)
+        cap = len(data) + 16
+        while True:
+            ids = np.zeros(cap, dtype=np.int32)
+            n = ctypes.c_int32()
+            rc = lib.cq_tokenizer_encode(self.handle, data, len(data),
+                                         ids.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), cap, ctypes.byref(n))
+            if rc == 6 and n.value > cap:   # CQ_ERANGE: grow to the reported size
+                cap = n.value
+                continue
+            check(rc)
+            return [int(i) for i in ids[:n.value]]
+
+    def decode_bytes(self, ids):
+        a = np.ascontiguousarray(ids, dtype=np.int32)
+        need = ctypes.c_size_t()
+        cap = max(16, 8 * int(a.size) + 16)
+        while True:
+            buf = ctypes.create_string_buffer(cap)
+            rc = lib.cq_tokenizer_decode(self.handle, a.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), int(a.size),
+                                         buf, cap, ctypes.byref(need))
+            if rc == 6 and need.value > cap:
+                cap = need.value
+                continue
+            check(rc)
+            return buf.raw[:need.value]
+
+    def decode(self, ids):
+        """decode() (src/tokenizer.cpp:203-209): text of the ids (invalid
+        UTF-8 from a partial multi-byte character is replaced)."""
+        return self.decode_bytes(ids).decode("utf-8", errors="replace")
+
+    def token_id(self, token):
+        return int(lib.cq_tokenizer_token_id(self.handle, token.encode("utf-8")))
+
+    def vocab_size(self):
+        return int(lib.cq_tokenizer_vocab_size(self.handle))
+
+    @staticmethod
+    def apply_chat_template(messages, add_generation_prompt=True):
+        """apply_chat_template (src/tokenizer.cpp:98-105); messages are
+        (role, content) pairs or {"role", "content"} dicts."""
+        pairs = [(m["role"], m["content"]) if isinstance(m, dict) else tuple(m) for m in messages]
+        n = len(pairs)
+        roles = (ctypes.c_char_p * max(n, 1))(*[r.encode("utf-8") for r, _ in pairs])
+        contents = (ctypes.c_char_p * max(n, 1))(*[c.encode("utf-8") for _, c in pairs])
+        need = ctypes.c_size_t()
+        rc = lib.cq_chat_template(roles, contents, n, int(bool(add_generation_prompt)), None, 0, ctypes.byref(need))
+        if rc not in (0, 6):
+            check(rc)
+        buf = ctypes.create_string_buffer(max(1, need.value))
+        check(lib.cq_chat_template(roles, contents, n, int(bool(add_generation_prompt)), buf, need.value,
+                                   ctypes.byref(need)))
+        return buf.raw[:need.value].decode("utf-8")
+
+    def free(self):
+        if self.handle:
+            check(lib.cq_tokenizer_free(self.handle))
+            self.handle = None
+
+
+class ChatSession:
+    """The turn logic of the reference's chat loop (src/main.cu:40-126) as a
+    library object: the first turn sends the whole templated conversation,
+    later turns only the new user turn; the prompt is prefilled (batched here,
+    one decode step per token there), then greedy decode with the turn's
+    generated ids as the repetition-penalty history until <|endoftext|> or
+    <|im_end|> (neither is fed back) or the context limit (max_seq_len - 2)."""
+
+    def __init__(self, state, tokenizer, eos_id=151643, im_end_id=151645):
+        self.state = state
+        self.tok = tokenizer
+        self.eos_id = eos_id
+        self.im_end_id = im_end_id
+        self.history = []
+        self.pos = 0
+
+    def reply(self, user_text, max_new_tokens=None, on_token=None):
+        limit = self.state.cfg.max_seq_len - 2
+        self.history.append(("user", user_text))
+        turn = self.history if len(self.history) == 1 else [("user", user_text)]
+        prompt = self.tok.encode(self.tok.apply_chat_template(turn, True))
+        if self.pos + len(prompt) >= limit:
+            raise CuQwenError(6, "prompt too long for the remaining context")
+        nxt = self.state.prefill(prompt, self.pos)
+        self.pos += len(prompt)
+        generated = []
+        while nxt not in (self.eos_id, self.im_end_id) and self.pos < limit:
+            if max_new_tokens is not None and len(generated) >= max_new_tokens:
+                break
+            generated.append(nxt)
+            if on_token:
+                on_token(nxt)
+            nxt = self.state.forward(nxt, self.pos, generated)
+            self.pos += 1
+        text = self.tok.decode(generated)
+        self.history.append(("assistant", text))
+        return text, generated

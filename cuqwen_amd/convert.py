@@ -26,6 +26,7 @@ large ones one row block) at a time, so memory stays bounded by the largest
 row block rather than the checkpoint size.
 
 Usage: python -m cuqwen_amd.convert HF_DIR --quant int4 --out model_int4_7b.bin
+       [--tokenizer-out qwen25_bpe_ranks.json]   (the tokenizer file, export_weights.py:328-365)
 """
 import argparse
 import ctypes
@@ -225,14 +226,52 @@ def _write_file(tmp, st, cfg, qt, lm_int8, has_lm, say):
             _write_matrix(f, st, "lm_head.weight", cfg["vocab_size"], d, 0)
 
 
+def export_tokenizer(hf_dir, out_path):
+    """The tokenizer ranks file the engine's tokenizer reads
+    (cq_tokenizer_load), as export_weights.py:328-365 writes it:
+    {"vocab": vocab.json, "special_tokens": {tokenizer_config key: token} for
+    string values (and list items) that are vocabulary tokens,
+    "added_tokens": {"id": content} from tokenizer.json}."""
+    vocab_path = os.path.join(hf_dir, "vocab.json")
+    if not os.path.exists(vocab_path):
+        raise ConvertError(f"{vocab_path} not found")
+    with open(vocab_path, encoding="utf-8") as f:
+        vocab = json.load(f)
+    added = {}
+    tok_path = os.path.join(hf_dir, "tokenizer.json")
+    if os.path.exists(tok_path):
+        with open(tok_path, encoding="utf-8") as f:
+            for entry in json.load(f).get("added_tokens", []):
+                added[int(entry["id"])] = entry["content"]
+    special = {}
+    tc_path = os.path.join(hf_dir, "tokenizer_config.json")
+    if os.path.exists(tc_path):
+        with open(tc_path, encoding="utf-8") as f:
+            tc = json.load(f)
+        for k, v in tc.items():
+            if isinstance(v, str) and v in vocab:
+                special[k] = v
+            elif isinstance(v, list):
+                for item in v:
+                    if isinstance(item, str) and item in vocab:
+                        special[item] = item
+    data = {"vocab": vocab, "special_tokens": special, "added_tokens": {str(k): v for k, v in added.items()}}
+    with open(out_path, "w", encoding="utf-8") as f:
+        json.dump(data, f, ensure_ascii=False, indent=2)
+    return len(vocab), len(added)
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("hf_dir", help="local HuggingFace model directory (config.json + *.safetensors)")
     ap.add_argument("--quant", default="int4", choices=sorted(QUANT_TYPES))
     ap.add_argument("--out", required=True, help="output .bin path")
+    ap.add_argument("--tokenizer-out", help="also write the tokenizer ranks file (qwen25_bpe_ranks.json) here")
     args = ap.parse_args(argv)
     try:
         cfg = convert(args.hf_dir, args.out, args.quant, log=lambda m: print(m, file=sys.stderr, flush=True))
+        if args.tokenizer_out:
+            export_tokenizer(args.hf_dir, args.tokenizer_out)
     except ConvertError as e:
         print(f"convert: {e}", file=sys.stderr)
         return 1

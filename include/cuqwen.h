@@ -357,6 +357,45 @@ int cq_time_gemv(int32_t quant_type, int32_t group_size, int32_t n_bufs, void* c
 int cq_state_profile(cq_state* s, int32_t pos, int32_t iters, int32_t max_kernels, char* names,
                      double* us_per_launch, double* bytes_per_launch, int32_t* n_kernels);
 
+/* ------------------------------------------------------------ tokenizer */
+/* Byte-level BPE tokenizer of the Qwen2.5 family (QwenTokenizer,
+ * include/tokenizer.h:18-41, src/tokenizer.cpp).  Host code only; no PCRE2
+ * or JSON library is needed. */
+typedef struct cq_tokenizer cq_tokenizer;
+
+/* QwenTokenizer(ranks_json_path) (src/tokenizer.cpp:44-96): reads the
+ * exporter's qwen25_bpe_ranks.json (export_weights.py:328-365: "vocab"
+ * {token: id}, "added_tokens" {"id": token}; other members are skipped).
+ * Errors: CQ_EIO (cannot open), CQ_EFORMAT (not that JSON layout) instead of
+ * the reference's exceptions. */
+int cq_tokenizer_load(const char* ranks_json_path, cq_tokenizer** out);
+int cq_tokenizer_free(cq_tokenizer* t);
+
+/* QwenTokenizer::encode (src/tokenizer.cpp:170-201): special tokens split
+ * the UTF-8 text first, the rest is pre-tokenized with the Qwen2 pattern and
+ * merged by byte-level BPE.  Writes *n_out ids; CQ_ERANGE (with *n_out set to
+ * the count needed) when `cap` is too small.  Bytes that are not valid UTF-8
+ * are kept as single characters (the reference stops at them). */
+int cq_tokenizer_encode(cq_tokenizer* t, const char* text, size_t len, int32_t* ids, int32_t cap,
+                        int32_t* n_out);
+
+/* QwenTokenizer::decode / decode_single (src/tokenizer.cpp:203-238): the
+ * bytes of the ids' tokens (special tokens as their text, unknown ids as
+ * nothing).  *len_out = bytes needed; CQ_ERANGE when `cap` is too small. */
+int cq_tokenizer_decode(cq_tokenizer* t, const int32_t* ids, int32_t n, char* buf, size_t cap, size_t* len_out);
+
+/* Id of a vocabulary or special token (e.g. "<|im_end|>"), -1 if absent. */
+int32_t cq_tokenizer_token_id(cq_tokenizer* t, const char* token);
+/* Largest id + 1. */
+int32_t cq_tokenizer_vocab_size(cq_tokenizer* t);
+
+/* QwenTokenizer::apply_chat_template (src/tokenizer.cpp:98-105):
+ * "<|im_start|>{role}\n{content}<|im_end|>\n" per message, then
+ * "<|im_start|>assistant\n" when add_generation_prompt.  *len_out = bytes
+ * needed; CQ_ERANGE when `cap` is too small. */
+int cq_chat_template(const char* const* roles, const char* const* contents, int32_t n_messages,
+                     int32_t add_generation_prompt, char* buf, size_t cap, size_t* len_out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,60 @@
+"""The chat turn logic (cuqwen_amd.ChatSession, the reference's chat loop
+src/main.cu:40-126) on the device against the host oracle: templated and
+tokenized turns, prefill, greedy decode with the turn's generated ids as the
+penalty history, stop ids, and the second turn continuing at the next
+position with only the new turn templated."""
+import numpy as np
+import pytest
+
+import cuqwen_amd as cq
+from oracle import oracle as orc
+from tests.conftest import tiny_config
+from tests.test_tokenizer import train_hf_tokenizer, write_ranks
+
+pytestmark = pytest.mark.gpu
+
+
+def _oracle_turn(om, prompt, pos, stop, max_new):
+    nxt = None
+    for i, t in enumerate(prompt):
+        nxt = om.forward(t, pos + i, [])
+    pos += len(prompt)
+    gen, near_tie = [], False
+    while nxt not in stop and len(gen) < max_new:
+        gen.append(nxt)
+        l = np.sort(om.logits().astype(np.float64))
+        near_tie |= l[-1] - l[-2] <= 1e-2
+        nxt = om.forward(nxt, pos, gen)
+        pos += 1
+    return gen, pos, near_tie
+
+
+def test_chat_session_two_turns_match_oracle(tmp_path):
+    hf = train_hf_tokenizer()
+    path = tmp_path / "ranks.json"
+    write_ranks(hf, path)
+    tok = cq.Tokenizer(str(path))
+    cfg = tiny_config(2)
+    w = cq.synth_weights(cfg, 11)
+    st = cq.State(cfg, w)
+    eos, im_end = tok.token_id("<|endoftext|>"), tok.token_id("<|im_end|>")
+    chat = cq.ChatSession(st, tok, eos_id=eos, im_end_id=im_end)
+    om = orc.Model.synth(cfg, 11, cfg.max_seq_len)
+    pos, compared = 0, 0
+    turns = ["Hello there! How's it going?", "Tell me about 日本語 and numbers 42."]
+    for k, user in enumerate(turns):
+        msgs = [("user", user)]
+        prompt = tok.encode(cq.Tokenizer.apply_chat_template(msgs, True))
+        assert prompt[0] == tok.token_id("<|im_start|>")
+        text, gen = chat.reply(user, max_new_tokens=12)
+        want, pos, near_tie = _oracle_turn(om, prompt, pos, (eos, im_end), 12)
+        if not near_tie:
+            assert gen == want, k
+            compared += 1
+        assert text == tok.decode(gen)
+        assert chat.pos == pos
+    assert compared >= 1
+    assert [r for r, _ in chat.history] == ["user", "assistant", "user", "assistant"]
+    st.free()
+    w.free()
+    tok.free()
