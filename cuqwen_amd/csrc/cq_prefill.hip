@@ -673,6 +673,97 @@ __global__ __launch_bounds__(kAttnThreads) void pf_attention_kernel(const PfAttn
   }
 }
 
+// Causal attention with the K / V tiles shared by the query heads of a GQA
+// group (fp16 cache): block = (16 consecutive tokens, one kv head), wave w
+// owns query head kvh * g + w and runs the online softmax over every key tile
+// up to the block's last token, so no cross-wave merge is needed.  The tiles
+// stream global -> LDS directly (global_load_lds_dwordx4; a tile's K and V
+// are each one contiguous 32-key block of the tiled cache), three stages
+// deep, and each head-wave reads its operands from LDS: the cache is read
+// once per kv head instead of once per query head.
+constexpr int kPfGqaStages = 3;
+template <int HD>
+__global__ __launch_bounds__(kAttnThreads) void pf_attention_gqa_kernel(const PfAttnArgs a) {
+  constexpr int KK = HD / 32, DT = HD / 16;
+  constexpr int TILE = kTileKeys * HD;               // halves of K (or V) per tile
+  constexpr int CHUNKS = 2 * TILE * 2 / 1024;        // 1 KB LDS-direct loads per tile (K and V)
+  static_assert(CHUNKS % kAttnWaves == 0, "tile loads split evenly over the waves");
+  constexpr int PER_WAVE = CHUNKS / kAttnWaves;
+  __shared__ __align__(16) _Float16 st[kPfGqaStages][2 * TILE];
+  const int t0 = blockIdx.x * 16, kvh = blockIdx.y;
+  const int g = a.n_heads / a.n_kv;
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int h = lane & 15, j = lane >> 4;   // h: token column
+  const int t_max = a.pos0 + min(t0 + 16, a.M);   // keys visible to the block
+  const int n_tiles = (t_max + kTileKeys - 1) / kTileKeys;
+  const _Float16* kbase = a.kcache + (int64_t)kvh * a.max_seq * HD;
+  const _Float16* vbase = a.vcache + (int64_t)kvh * a.max_seq * HD;
+  auto issue = [&](int ti) {
+    _Float16* dst = st[ti % kPfGqaStages];
+#pragma unroll
+    for (int i = 0; i < PER_WAVE; ++i) {
+      const int c = i * kAttnWaves + wave;            // 1 KB chunk: K chunks first, then V
+      const bool isv = c >= CHUNKS / 2;
+      const int cc = isv ? c - CHUNKS / 2 : c;
+      const _Float16* src = (isv ? vbase : kbase) + (int64_t)ti * TILE + cc * 512 + lane * 8;
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src),
+                                       (__attribute__((address_space(3))) void*)(dst + (isv ? TILE : 0) + cc * 512),
+                                       16, 0, 0);
+    }
+  };
+  const bool active = wave < g;
+  const int hq = kvh * g + min(wave, g - 1);
+  const int tcol = min(t0 + h, a.M - 1);
+  const int t_lane = a.pos0 + tcol + 1;                // keys visible to this column
+  h8_t qb[KK];
+  const _Float16* q = a.q + (int64_t)tcol * a.n_heads * HD + hq * HD;
+#pragma unroll
+  for (int kk = 0; kk < KK; ++kk) qb[kk] = __builtin_bit_cast(h8_t, load_u4(q + kk * 32 + j * 8));
+  issue(0);
+  if (n_tiles > 1) issue(1);
+  const float scale = 1.0f / sqrtf((float)HD);
+  float m = -INFINITY, l = 0.f;
+  f4_t o[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) o[dt] = f4_t{0.f, 0.f, 0.f, 0.f};
+  for (int ti = 0; ti < n_tiles; ++ti) {
+    // this tile's loads (issued two tiles ago) done, then visible to all waves
+    // (at most the next tile's PER_WAVE loads stay outstanding; the q loads
+    // went out before any of them)
+    if (ti + 1 < n_tiles) __builtin_amdgcn_s_waitcnt(0x0F70 | PER_WAVE);
+    else __builtin_amdgcn_s_waitcnt(0x0F70);
+    __builtin_amdgcn_s_barrier();
+    if (ti + 2 < n_tiles) issue(ti + 2);   // into the stage every wave finished reading at ti - 1
+    if (active) {
+      const _Float16* kt = st[ti % kPfGqaStages];
+      const _Float16* vt = kt + TILE;
+      KVTile<HD> A;
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk)
+          A.ka[s2][kk] = *reinterpret_cast<const h8_t*>(kt + s2 * 16 * HD + (kk * 64 + lane) * 8);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) A.va[dt] = *reinterpret_cast<const h8_t*>(vt + (dt * 64 + lane) * 8);
+      pf_attend_tile<HD>(A, qb, ti, t_lane, t_max, scale, j, m, l, o);
+    }
+  }
+  if (!active) return;
+  l += __shfl_xor(l, 16, kWave);
+  l += __shfl_xor(l, 32, kWave);
+  if (t0 + h >= a.M) return;
+  const int qd = a.n_heads * HD;
+  const float inv = 1.0f / (l + 1e-9f);
+  _Float16* orow = a.out + (int64_t)(t0 + h) * qd;
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int k = hq * HD + dt * 16 + 4 * j + i;
+      orow[pf_pos(k, a.int4_layout)] = pf_val((float)(_Float16)(o[dt][i] * inv), k, a.int4_layout);
+    }
+}
+
 // ------------------------------------------------------------------ host
 int launch_pf_norm(const __half* x, const __half* w, float eps, int M, int dim, __half* A, float* inv,
                    int quant, hipStream_t stream) {
@@ -753,6 +844,10 @@ int launch_pf_attention(const PfAttnArgs& a, hipStream_t stream) {
       if (a.head_dim == 128) hipLaunchKernelGGL((pf_attention_kernel<128, CQ_KV_INT8>), grid, dim3(kAttnThreads), 0, stream, a);
       else hipLaunchKernelGGL((pf_attention_kernel<64, CQ_KV_INT8>), grid, dim3(kAttnThreads), 0, stream, a);
     }
+  } else if (a.n_heads / a.n_kv <= kAttnWaves) {
+    const dim3 g2((a.M + 15) / 16, a.n_kv);
+    if (a.head_dim == 128) hipLaunchKernelGGL((pf_attention_gqa_kernel<128>), g2, dim3(kAttnThreads), 0, stream, a);
+    else hipLaunchKernelGGL((pf_attention_gqa_kernel<64>), g2, dim3(kAttnThreads), 0, stream, a);
   } else {
     if (a.head_dim == 128) hipLaunchKernelGGL((pf_attention_kernel<128, 0>), grid, dim3(kAttnThreads), 0, stream, a);
     else hipLaunchKernelGGL((pf_attention_kernel<64, 0>), grid, dim3(kAttnThreads), 0, stream, a);
