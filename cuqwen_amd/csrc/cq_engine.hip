@@ -759,8 +759,31 @@ int prefill_workspace(cq_state* s) {
   return CQ_OK;
 }
 
+// The last prompt token's tail: its row of the last layer continues through
+// the decode kernels (O-proj + residual, RMSNorm + gate/up + SwiGLU, down +
+// residual, final RMSNorm + lm_head, argmax into ctl->sampled); no
+// repetition penalty, as in the reference's prefill loop.
+int prefill_tail(cq_state* s, int M) {
+  const cq_config& c = s->cfg;
+  hipStream_t st = s->stream;
+  const int d = c.dim, qd = c.n_heads * c.head_dim;
+  CQ_HIP(hipMemcpyAsync(s->x, s->pf_x + (size_t)(M - 1) * d, (size_t)d * 2, hipMemcpyDeviceToDevice, st));
+  CQ_TRY(launch_pf_row_natural(s->pf_ao + (size_t)(M - 1) * qd, s->xb, qd, c.quant_type, st));
+  GemvArgs o, m1, m2;
+  layer_gemvs(s, c.n_layers - 1, nullptr, &o, &m1, &m2);
+  CQ_TRY(launch_gemv(o, st));
+  CQ_TRY(launch_gemv(m1, st));
+  CQ_TRY(launch_gemv(m2, st));
+  GemvArgs lm = lm_head_gemv(s);
+  lm.stamp = nullptr;   // no penalty history
+  lm.argmax_out = s->argmax_ws;
+  CQ_TRY(launch_gemv(lm, st));
+  return launch_argmax_reduce(s->argmax_ws, kArgmaxPartials, nullptr, &s->ctl->sampled, nullptr, nullptr, st);
+}
+
 // tokens[0..n) at positions pos0.. through every layer, M tokens at a time;
-// fills the KV cache (the residual stream of the last layer is not needed).
+// fills the KV cache.  The last layer's O-proj / MLP run only for the last
+// token, through prefill_tail (which also produces its logits and argmax).
 int prefill_batched(cq_state* s, const int32_t* tokens, int n, int pos0) {
   CQ_TRY(prefill_workspace(s));
   const cq_config& c = s->cfg;
@@ -804,7 +827,10 @@ int prefill_batched(cq_state* s, const int32_t* tokens, int n, int pos0) {
       at.kcache8 = kc8; at.vcache8 = vc8; at.kscale = ksc; at.vscale = vsc; at.kv_fmt = s->kv_dtype;
       at.int4_layout = c.quant_type == CQ_QUANT_INT4;
       CQ_TRY(launch_pf_attention(at, st));
-      if (l == c.n_layers - 1) break;   // the last layer's residual stream feeds nothing here
+      if (l == c.n_layers - 1) {   // only the last token's row goes on
+        if (c0 + M == n) CQ_TRY(prefill_tail(s, M));
+        break;
+      }
       PfGemmArgs o;
       o.mode = GM_RESID; o.quant = c.quant_type; o.A = (const _Float16*)s->pf_ao; o.M = M; o.N = d; o.K = qd;
       o.W[0] = L.wo; o.S[0] = (const _Float16*)L.so; o.rows[0] = d; o.out = (_Float16*)s->pf_x;
@@ -838,11 +864,16 @@ extern "C" int cq_prefill(cq_state* s, const int32_t* tokens, int32_t n_tokens, 
     if (tokens[i] < 0 || tokens[i] >= s->cfg.vocab_size) return fail(CQ_ERANGE, "prefill: token outside the vocabulary");
   CQ_TRY(ensure_graph(s));   // recorded before any prefill work is queued on the stream
   CQ_HIP(hipEventRecord(s->ev0, s->stream));
-  if (n_tokens > 1) CQ_TRY(prefill_batched(s, tokens, n_tokens - 1, pos0));
-  // the last prompt token is a normal decode step: logits, argmax (no
-  // penalty history, like the reference's prefill loop)
-  CQ_TRY(set_ctl(s, tokens[n_tokens - 1], pos0 + n_tokens - 1, nullptr, 0, 0));
-  CQ_HIP(hipGraphLaunch(s->exec, s->stream));
+  if (n_tokens > 1) {
+    // every token through the batched path; the last one's logits and
+    // argmax from its tail (no penalty history, like the reference's
+    // prefill loop)
+    CQ_TRY(prefill_batched(s, tokens, n_tokens, pos0));
+  } else {
+    // a one-token prompt is a normal decode step
+    CQ_TRY(set_ctl(s, tokens[0], pos0, nullptr, 0, 0));
+    CQ_HIP(hipGraphLaunch(s->exec, s->stream));
+  }
   CQ_HIP(hipEventRecord(s->ev1, s->stream));
   CQ_HIP(hipMemcpyAsync(s->host_pinned + 8, &s->ctl->sampled, sizeof(int), hipMemcpyDeviceToHost, s->stream));
   CQ_HIP(hipStreamSynchronize(s->stream));

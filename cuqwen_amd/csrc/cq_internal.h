@@ -123,6 +123,7 @@ struct PfAttnArgs {
 int launch_pf_norm(const __half* x, const __half* w, float eps, int M, int dim, __half* A, float* inv, int quant,
                    hipStream_t stream);
 int launch_pf_embed(const __half* embed, const int* tokens, int M, int dim, __half* x, hipStream_t stream);
+int launch_pf_row_natural(const __half* src, __half* dst, int n, int quant, hipStream_t stream);
 int launch_pf_gemm(const PfGemmArgs& a, hipStream_t stream);
 int launch_pf_attention(const PfAttnArgs& a, hipStream_t stream);
 

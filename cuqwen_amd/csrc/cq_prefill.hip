@@ -764,11 +764,26 @@ __global__ __launch_bounds__(kAttnThreads) void pf_attention_gqa_kernel(const Pf
     }
 }
 
+// One row of a GEMM input back to natural order (the int4 layout stores each
+// 8-group as [0,4,1,5,2,6,3,7] with the odd elements / 16; the scale is a
+// power of two, so the round trip is exact).
+__global__ __launch_bounds__(256) void pf_row_natural(const _Float16* src, _Float16* dst, int n, bool int4) {
+  for (int k = threadIdx.x; k < n; k += blockDim.x)
+    dst[k] = (_Float16)((float)src[pf_pos(k, int4)] * ((int4 && (k & 1)) ? 16.0f : 1.0f));
+}
+
 // ------------------------------------------------------------------ host
 int launch_pf_norm(const __half* x, const __half* w, float eps, int M, int dim, __half* A, float* inv,
                    int quant, hipStream_t stream) {
   hipLaunchKernelGGL(pf_norm_rows, dim3(M), dim3(256), 0, stream, (const _Float16*)x, (const _Float16*)w, eps, dim,
                      (_Float16*)A, inv, quant == CQ_QUANT_INT4);
+  CQ_HIP(hipGetLastError());
+  return CQ_OK;
+}
+
+int launch_pf_row_natural(const __half* src, __half* dst, int n, int quant, hipStream_t stream) {
+  hipLaunchKernelGGL(pf_row_natural, dim3(1), dim3(256), 0, stream, (const _Float16*)src, (_Float16*)dst, n,
+                     quant == CQ_QUANT_INT4);
   CQ_HIP(hipGetLastError());
   return CQ_OK;
 }

@@ -152,9 +152,10 @@ int cq_decode(cq_state* s, int32_t token, int32_t pos0, int32_t n_steps,
 
 /* Prompt processing.  The reference's prefill loop (src/main.cu:87-92) runs
  * one qwen_forward per prompt token with no penalty history; this entry
- * point gives the same result with tokens[0..n_tokens-1) pushed through the
- * layers in batches (matrix-core GEMMs and a causal attention kernel, up to
- * 2048 tokens per pass) and the last token run as a decode step.  Fills the
+ * point gives the same result with the tokens pushed through the layers in
+ * batches (matrix-core GEMMs and a causal attention kernel, up to 2048
+ * tokens per pass), the last layer's O-proj / MLP and the lm_head run for the
+ * last token only (a one-token prompt is a plain decode step).  Fills the
  * KV cache for positions [pos0, pos0 + n_tokens); *token_out receives the
  * greedy id after the last prompt token and cq_state_logits its logits.
  * Errors: CQ_ERANGE for positions past max_seq_len or ids outside the
