@@ -97,7 +97,7 @@ def prefill_leg(cq, cfg, st, n):
     reference's prefill-by-decode (one decode step per prompt token,
     src/main.cu:87-92) timed on the same state at the same positions.
     Matrix-core roofline: the GEMM flops of the batched tokens over the whole
-    prefill time (attention, norms and the last token's decode step included)."""
+    prefill time (attention, norms and the last token's lm_head included)."""
     prompt = [int(cq.lib.cq_synth_uniform(42, 0, i, cfg.vocab_size)) for i in range(n)]
     st.prefill(prompt, 0)   # workspace allocation, first-touch
     best = None
@@ -112,7 +112,9 @@ def prefill_leg(cq, cfg, st, n):
     by_decode_ms = (time.perf_counter() - t0) * 1e3 / steps * n
     d, I, L = cfg.dim, cfg.intermediate_size, cfg.n_layers
     qd, kvd = cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim
-    flops = 2.0 * (n - 1) * (L * (qd + 2 * kvd) * d + (L - 1) * (d * qd + 3 * I * d))
+    # every token through the batched QKV GEMMs and L-1 layers of O-proj / MLP GEMMs (the last
+    # layer's O-proj / MLP run for the last token only, as GEMVs)
+    flops = 2.0 * n * (L * (qd + 2 * kvd) * d + (L - 1) * (d * qd + 3 * I * d))
     tflops = flops / (best * 1e-6) / 1e12
     return {"prompt_tokens": n, "ms": round(best / 1e3, 3), "tok_per_s": round(n / (best * 1e-6), 1),
             "prefill_by_decode_ms": round(by_decode_ms, 2), "speedup": round(by_decode_ms / (best / 1e3), 2),
