@@ -674,45 +674,69 @@ __global__ __launch_bounds__(kAttnThreads) void pf_attention_kernel(const PfAttn
 }
 
 // Causal attention with the K / V tiles shared by the query heads of a GQA
-// group (fp16 cache): block = (16 consecutive tokens, one kv head), wave w
-// owns query head kvh * g + w and runs the online softmax over every key tile
-// up to the block's last token, so no cross-wave merge is needed.  The tiles
-// stream global -> LDS directly (global_load_lds_dwordx4; a tile's K and V
-// are each one contiguous 32-key block of the tiled cache), three stages
-// deep, and each head-wave reads its operands from LDS: the cache is read
-// once per kv head instead of once per query head.
+// group (fp16 cache): block = (16 consecutive tokens, one kv head), 16 waves:
+// wave w owns query head kvh * g + (w % 8) and, with its partner w ^ 8, runs
+// the online softmax over every key tile up to the block's last token (even
+// tiles in waves 0-7, odd tiles in waves 8-15); the two halves merge in LDS
+// at the end.  The tiles stream global -> LDS directly
+// (global_load_lds_dwordx4; a tile's K and V are each one contiguous 32-key
+// block of the tiled cache), a pair of tiles per stage, three stages deep,
+// and every head of the group reads them from LDS: the cache is read once
+// per kv head instead of once per query head.
 constexpr int kPfGqaStages = 3;
+constexpr int kPfGqaWaves = 16;
 template <int HD>
-__global__ __launch_bounds__(kAttnThreads) void pf_attention_gqa_kernel(const PfAttnArgs a) {
+__global__ __launch_bounds__(kPfGqaWaves * kWave) void pf_attention_gqa_kernel(const PfAttnArgs a) {
   constexpr int KK = HD / 32, DT = HD / 16;
   constexpr int TILE = kTileKeys * HD;               // halves of K (or V) per tile
-  constexpr int CHUNKS = 2 * TILE * 2 / 1024;        // 1 KB LDS-direct loads per tile (K and V)
-  static_assert(CHUNKS % kAttnWaves == 0, "tile loads split evenly over the waves");
-  constexpr int PER_WAVE = CHUNKS / kAttnWaves;
-  __shared__ __align__(16) _Float16 st[kPfGqaStages][2 * TILE];
+  constexpr int STAGE = 4 * TILE;                    // two tiles, K and V
+  constexpr int CHUNKS = STAGE * 2 / 1024;           // 1 KB LDS-direct loads per stage
+  constexpr int PER_WAVE = (CHUNKS + kPfGqaWaves - 1) / kPfGqaWaves;
+  constexpr int MERGE = 8 * kWave * (2 + 4 * DT);    // floats of one half's softmax state
+  static_assert(MERGE * 4 <= kPfGqaStages * STAGE * 2, "merge area fits in the stage buffers");
+  __shared__ __align__(16) _Float16 st[kPfGqaStages * STAGE];
   const int t0 = blockIdx.x * 16, kvh = blockIdx.y;
   const int g = a.n_heads / a.n_kv;
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int head = wave & 7, half = wave >> 3;
   const int h = lane & 15, j = lane >> 4;   // h: token column
   const int t_max = a.pos0 + min(t0 + 16, a.M);   // keys visible to the block
   const int n_tiles = (t_max + kTileKeys - 1) / kTileKeys;
+  const int n_steps = (n_tiles + 1) / 2;
   const _Float16* kbase = a.kcache + (int64_t)kvh * a.max_seq * HD;
   const _Float16* vbase = a.vcache + (int64_t)kvh * a.max_seq * HD;
-  auto issue = [&](int ti) {
-    _Float16* dst = st[ti % kPfGqaStages];
+  // stage layout: [tile 0: K, V][tile 1: K, V]; chunk c of a stage is 1 KB
+  // loads this wave issues for a step (the pair's second tile may be past the end)
+  auto n_loads = [&](int step) {
+    int n = 0;
 #pragma unroll
     for (int i = 0; i < PER_WAVE; ++i) {
-      const int c = i * kAttnWaves + wave;            // 1 KB chunk: K chunks first, then V
-      const bool isv = c >= CHUNKS / 2;
-      const int cc = isv ? c - CHUNKS / 2 : c;
-      const _Float16* src = (isv ? vbase : kbase) + (int64_t)ti * TILE + cc * 512 + lane * 8;
-      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src),
-                                       (__attribute__((address_space(3))) void*)(dst + (isv ? TILE : 0) + cc * 512),
-                                       16, 0, 0);
+      const int c = i * kPfGqaWaves + wave;
+      n += (c < CHUNKS && 2 * step + c / (CHUNKS / 2) < n_tiles) ? 1 : 0;
+    }
+    return n;
+  };
+  static_assert(PER_WAVE <= 2, "the waits below cover up to two loads per step");
+  auto issue = [&](int step) {
+    _Float16* dst = st + (step % kPfGqaStages) * STAGE;
+#pragma unroll
+    for (int i = 0; i < PER_WAVE; ++i) {
+      const int c = i * kPfGqaWaves + wave;
+      const int tt = c / (CHUNKS / 2), r = c % (CHUNKS / 2);   // tile of the pair, chunk within it
+      const int ti = 2 * step + tt;
+      if (c < CHUNKS && ti < n_tiles) {
+        const bool isv = r >= CHUNKS / 4;
+        const int cc = isv ? r - CHUNKS / 4 : r;
+        const _Float16* src = (isv ? vbase : kbase) + (int64_t)ti * TILE + cc * 512 + lane * 8;
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src),
+                                         (__attribute__((address_space(3))) void*)(dst + tt * 2 * TILE +
+                                                                                    (isv ? TILE : 0) + cc * 512),
+                                         16, 0, 0);
+      }
     }
   };
-  const bool active = wave < g;
-  const int hq = kvh * g + min(wave, g - 1);
+  const bool active = head < g;
+  const int hq = kvh * g + min(head, g - 1);
   const int tcol = min(t0 + h, a.M - 1);
   const int t_lane = a.pos0 + tcol + 1;                // keys visible to this column
   h8_t qb[KK];
@@ -720,22 +744,25 @@ __global__ __launch_bounds__(kAttnThreads) void pf_attention_gqa_kernel(const Pf
 #pragma unroll
   for (int kk = 0; kk < KK; ++kk) qb[kk] = __builtin_bit_cast(h8_t, load_u4(q + kk * 32 + j * 8));
   issue(0);
-  if (n_tiles > 1) issue(1);
+  if (n_steps > 1) issue(1);
   const float scale = 1.0f / sqrtf((float)HD);
   float m = -INFINITY, l = 0.f;
   f4_t o[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) o[dt] = f4_t{0.f, 0.f, 0.f, 0.f};
-  for (int ti = 0; ti < n_tiles; ++ti) {
-    // this tile's loads (issued two tiles ago) done, then visible to all waves
-    // (at most the next tile's PER_WAVE loads stay outstanding; the q loads
+  for (int sp = 0; sp < n_steps; ++sp) {
+    // this step's loads (issued two steps ago) done, then visible to all
+    // waves: at most the next step's loads stay outstanding (the q loads
     // went out before any of them)
-    if (ti + 1 < n_tiles) __builtin_amdgcn_s_waitcnt(0x0F70 | PER_WAVE);
+    const int later = sp + 1 < n_steps ? n_loads(sp + 1) : 0;
+    if (later >= 2) __builtin_amdgcn_s_waitcnt(0x0F70 | 2);
+    else if (later == 1) __builtin_amdgcn_s_waitcnt(0x0F70 | 1);
     else __builtin_amdgcn_s_waitcnt(0x0F70);
     __builtin_amdgcn_s_barrier();
-    if (ti + 2 < n_tiles) issue(ti + 2);   // into the stage every wave finished reading at ti - 1
-    if (active) {
-      const _Float16* kt = st[ti % kPfGqaStages];
+    if (sp + 2 < n_steps) issue(sp + 2);   // into the stage every wave finished reading at sp - 1
+    const int ti = 2 * sp + half;
+    if (active && ti < n_tiles) {
+      const _Float16* kt = st + (sp % kPfGqaStages) * STAGE + half * 2 * TILE;
       const _Float16* vt = kt + TILE;
       KVTile<HD> A;
 #pragma unroll
@@ -748,19 +775,34 @@ __global__ __launch_bounds__(kAttnThreads) void pf_attention_gqa_kernel(const Pf
       pf_attend_tile<HD>(A, qb, ti, t_lane, t_max, scale, j, m, l, o);
     }
   }
-  if (!active) return;
   l += __shfl_xor(l, 16, kWave);
   l += __shfl_xor(l, 32, kWave);
-  if (t0 + h >= a.M) return;
+  // merge the odd-tile half into the even one (over the stage buffers)
+  __syncthreads();
+  float* mg = reinterpret_cast<float*>(st) + head * kWave * (2 + 4 * DT);
+  if (half == 1 && active) {
+    mg[lane] = m;
+    mg[kWave + lane] = l;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) mg[(2 + 4 * dt + i) * kWave + lane] = o[dt][i];
+  }
+  __syncthreads();
+  if (half == 1 || !active || t0 + h >= a.M) return;
+  const float m1 = mg[lane], l1 = mg[kWave + lane];
+  const float M = fmaxf(m, m1);
+  const float f0 = m == -INFINITY ? 0.f : __expf(m - M), f1 = m1 == -INFINITY ? 0.f : __expf(m1 - M);
+  const float inv = 1.0f / (l * f0 + l1 * f1 + 1e-9f);
   const int qd = a.n_heads * HD;
-  const float inv = 1.0f / (l + 1e-9f);
   _Float16* orow = a.out + (int64_t)(t0 + h) * qd;
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int k = hq * HD + dt * 16 + 4 * j + i;
-      orow[pf_pos(k, a.int4_layout)] = pf_val((float)(_Float16)(o[dt][i] * inv), k, a.int4_layout);
+      const float v = (o[dt][i] * f0 + mg[(2 + 4 * dt + i) * kWave + lane] * f1) * inv;
+      orow[pf_pos(k, a.int4_layout)] = pf_val((float)(_Float16)v, k, a.int4_layout);
     }
 }
 
@@ -859,10 +901,10 @@ int launch_pf_attention(const PfAttnArgs& a, hipStream_t stream) {
       if (a.head_dim == 128) hipLaunchKernelGGL((pf_attention_kernel<128, CQ_KV_INT8>), grid, dim3(kAttnThreads), 0, stream, a);
       else hipLaunchKernelGGL((pf_attention_kernel<64, CQ_KV_INT8>), grid, dim3(kAttnThreads), 0, stream, a);
     }
-  } else if (a.n_heads / a.n_kv <= kAttnWaves) {
+  } else if (a.n_heads / a.n_kv <= 8) {
     const dim3 g2((a.M + 15) / 16, a.n_kv);
-    if (a.head_dim == 128) hipLaunchKernelGGL((pf_attention_gqa_kernel<128>), g2, dim3(kAttnThreads), 0, stream, a);
-    else hipLaunchKernelGGL((pf_attention_gqa_kernel<64>), g2, dim3(kAttnThreads), 0, stream, a);
+    if (a.head_dim == 128) hipLaunchKernelGGL((pf_attention_gqa_kernel<128>), g2, dim3(kPfGqaWaves * kWave), 0, stream, a);
+    else hipLaunchKernelGGL((pf_attention_gqa_kernel<64>), g2, dim3(kPfGqaWaves * kWave), 0, stream, a);
   } else {
     if (a.head_dim == 128) hipLaunchKernelGGL((pf_attention_kernel<128, 0>), grid, dim3(kAttnThreads), 0, stream, a);
     else hipLaunchKernelGGL((pf_attention_kernel<64, 0>), grid, dim3(kAttnThreads), 0, stream, a);
