@@ -73,19 +73,21 @@ def test_prefill_tiny_matches_oracle(quant, segments):
     w.free()
 
 
-def test_prefill_crosses_chunks():
-    """A 2100-token prompt is two passes of at most 2048 tokens."""
+@pytest.mark.parametrize("n", [2100, 2049])
+def test_prefill_crosses_chunks(n):
+    """A prompt longer than 2048 tokens is several passes of at most 2048
+    (2049: the last pass holds only the last token)."""
     cfg = tiny_config(2, max_seq_len=4096)
     w = cq.synth_weights(cfg, 5)
     om = orc.Model.synth(cfg, 5, cfg.max_seq_len)
     st = cq.State(cfg, w)
-    prompt = _prompt(cfg, 2100, 9)
+    prompt = _prompt(cfg, n, 9)
     ot = _oracle_prompt(om, prompt, 0)
     gt = st.prefill(prompt, 0)
     assert _rel(st.logits(), om.logits()) <= TOL
     if _gap(om.logits()) > 1e-2:
         assert gt == ot
-    _check_kv(cfg, st, om.kv, 2100)
+    _check_kv(cfg, st, om.kv, n)
     st.free()
     w.free()
 
