@@ -1,7 +1,7 @@
 // Device building blocks of the FlashDecoding GQA attention (gfx950): the
 // 32-key K/V tile of one wave, its loads, the online-softmax step with
 // v_mfma_f32_16x16x32_f16, and the run-time partitioning of the context.
-// Shared by the attention kernels and the fused QKV + attention kernel.
+// Shared by the decode and prefill attention kernels.
 #pragma once
 
 #include "cq_device.h"

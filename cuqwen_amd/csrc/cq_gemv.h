@@ -121,8 +121,8 @@ template <int Q> __device__ __forceinline__ float plane_order_packed(const u4_t&
 }
 
 // ---------------------------------------------------------------------------
-// Building blocks of the GEMV kernels (shared with the fused QKV + attention
-// kernel): input staging, weight steps, row mapping and epilogues.
+// Building blocks of the GEMV kernels: input staging, weight steps, row
+// mapping and epilogues.
 
 constexpr int kNumCUs = 256;   // MI355X
 
