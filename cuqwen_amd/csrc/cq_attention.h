@@ -249,11 +249,12 @@ __device__ __forceinline__ int8_t kv_encode(float v) {
   else return (int8_t)fminf(127.f, fmaxf(-127.f, rintf(v)));
 }
 
-// One 32-key tile of the online softmax over the int8 cache.  Keys at or past
-// t_lane (this lane's column limit) are masked; P of masked keys is exactly 0
-// (int8 data is always finite, stale scales are selected out).  Rounding as
-// the fp16 path: score = half(s * k_scale * 1/sqrt(hd)), P = half(p *
-// v_scale) for the product, the row sum over the unrounded p.
+// One 32-key tile of the online softmax over a one-byte cache (F: int8 codes
+// or FP8 E4M3 codes).  Keys at or past t_lane (this lane's column limit) are
+// masked; P of masked keys is exactly 0 (the encoders never write a NaN code,
+// stale scales are selected out).  Rounding as the fp16 path:
+// score = half(s * k_scale * 1/sqrt(hd)), P = half(p * v_scale) for the
+// product, the row sum over the unrounded p.
 template <int HD, int F = CQ_KV_INT8>
 __device__ __forceinline__ void attend_tile8(KVTile8<HD>& t, const h8_t* qb, int ti, int t_lane, float scale, int j,
                                              float& m, float& l, f4_t* o, uint32_t magic_v) {
