@@ -168,18 +168,31 @@ __device__ __forceinline__ void pf_load_w(const PfGemmArgs& a, const char* rowp,
   for (int i = 0; i < L; ++i) w[i] = load_u4(p + i * 16);
 }
 
-// Tile shape: RT 16-row slices per wave (SwiGLU: RT/2 gate and RT/2 up
+// Tile shape: RT 16-row slices per wave in all (SwiGLU: RT/2 gate and RT/2 up
 // slices of the same output rows), 8 token slices of 16 per wave (the unpack
 // of a weight fragment is shared by 8 matrix instructions); a block is 8
-// waves over the same 128 tokens, two per SIMD.
-template <int Q> struct PfTile { static constexpr int RT = 2; };
+// waves over the same 128 tokens, two per SIMD.  With KS = 2 the waves form
+// two sets over the same rows: set h takes every other K step (kb + 2i + h),
+// so each wave reads half of the activation tiles from LDS for the same
+// matrix work (LDS read bytes per flop fall with the rows per wave), and the
+// two sets add their accumulators through LDS at the end.
+template <int Q> struct PfTile;
+template <> struct PfTile<CQ_QUANT_INT4> { static constexpr int RT = 2, KS = 1; };
+template <> struct PfTile<CQ_QUANT_INT8> { static constexpr int RT = 2, KS = 1; };
+template <> struct PfTile<CQ_QUANT_FP16> { static constexpr int RT = 2, KS = 1; };
 constexpr int kPfTT = 8;                         // token slices per wave
 constexpr int kPfTok = 16 * kPfTT;               // tokens per block
 template <int Q, int MODE> struct PfShape {
   static constexpr int NMAT = MODE == GM_SWIGLU ? 2 : 1;
   static constexpr int RT = PfTile<Q>::RT / NMAT;   // row slices per matrix
+  static constexpr int KS = PfTile<Q>::KS;           // wave sets splitting the K steps
+  static constexpr int RG = kPfWaves / KS;           // waves per set (row groups)
   static constexpr int WROWS = RT * 16;              // output rows per wave
-  static constexpr int BN = kPfWaves * WROWS;        // output rows per block
+  static constexpr int BN = RG * WROWS;              // output rows per block
+  // LDS stages of KS activation tiles, and how many super-steps (KS K steps)
+  // ahead loads are issued: 3 stages / 2 ahead for one set, 2 / 1 for two
+  static constexpr int NST = KS == 2 ? 2 : 3;
+  static constexpr int AH = NST - 1;
 };
 
 // The block's (row block, token block) from its dispatch index, so that all
@@ -203,23 +216,29 @@ template <int Q, int MODE, bool SPLIT>
 __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs a) {
   using SH = PfShape<Q, MODE>;
   constexpr int NMAT = SH::NMAT, RT = SH::RT, WROWS = SH::WROWS, BN = SH::BN, TT = kPfTT;
+  constexpr int KS = SH::KS, NST = SH::NST, AH = SH::AH;
   constexpr int L = PfW<Q>::LOADS;
-  constexpr int XS = kPfTok * kPfK;                         // halves of one activation stage
+  constexpr int XS = kPfTok * kPfK;                         // halves of one activation tile
+  constexpr int SM = NST * KS * XS;
   constexpr int OT = MODE == GM_QKV ? BN * kPfTok : 0;      // QKV epilogue tile (rows x tokens)
-  __shared__ __align__(16) _Float16 smem[3 * XS > OT ? 3 * XS : OT];
+  static_assert(OT <= SM && (KS == 1 || kPfWaves * NMAT * RT * (TT / 2) * 64 * 8 <= SM), "LDS reuse");
+  __shared__ __align__(16) _Float16 smem[SM];
   _Float16* xs0 = smem;
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int rg = wave % SH::RG, kh = wave / SH::RG;   // row group, K set
   const int r = lane & 15, j = lane >> 4;
   const int n_tb = (a.M + kPfTok - 1) / kPfTok;
   int rb, tb;
   pf_block_tile(n_tb, &rb, &tb);
   const int m0 = tb * kPfTok;
   const int nb0 = rb * BN;                     // first output row of the block
-  const int nw0 = nb0 + wave * WROWS;          // first output row of the wave
+  const int nw0 = nb0 + rg * WROWS;            // first output row of the wave
   const int K = a.K, nks = K / kPfK;
   // split-K: block z of gridDim.z sums K steps [kb, ke) into an fp32 partial
   const int kb = SPLIT ? (int)((int64_t)blockIdx.z * nks / gridDim.z) : 0;
   const int ke = SPLIT ? (int)((int64_t)(blockIdx.z + 1) * nks / gridDim.z) : nks;
+  const int nss = (ke - kb + KS - 1) / KS;     // super-steps of KS K steps
+  auto my_step = [&](int ss) { return kb + ss * KS + kh; };   // this wave's K step (valid below ke)
 
   // weight row (A operand row r of each slice) and its scale row
   const char* rowp[NMAT][RT];
@@ -237,20 +256,25 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
     }
 
   // Activation tiles go global -> LDS directly (global_load_lds_dwordx4, no
-  // registers), three stages deep.  A stage holds 128 token rows of 256 bytes;
-  // 16-byte slot s of row t holds K chunk s ^ (t & 15), so the B-operand
-  // reads (16 rows at one chunk) hit 16 different bank groups.  Load q of a
-  // step (q = i * waves + wave) fills rows 4q .. 4q + 3: lane l writes
-  // row 4q + l / 16, slot l % 16.
-  auto x_issue = [&](int ks, int stg) {
+  // registers).  A tile holds 128 token rows of 256 bytes; 16-byte slot s of
+  // row t holds K chunk s ^ (t & 15), so the B-operand reads (16 rows at one
+  // chunk) hit 16 different bank groups.  Load q of a tile (q = i * waves +
+  // wave) fills rows 4q .. 4q + 3: lane l writes row 4q + l / 16, slot l % 16.
+  // Stage g holds the KS tiles of one super-step.
+  constexpr int XL = kPfTok / (4 * kPfWaves);   // loads per lane per tile
+  auto x_issue = [&](int ss) {
 #pragma unroll
-    for (int i = 0; i < kPfTok / (4 * kPfWaves); ++i) {
-      const int q = i * kPfWaves + wave, t = 4 * q + (lane >> 4), c = (lane & 15) ^ (t & 15);
-      const int m = min(m0 + t, a.M - 1);
-      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(a.A + (int64_t)m * K + ks * kPfK + c * 8),
-                                       (__attribute__((address_space(3))) void*)(
-                                           xs0 + stg * XS + q * 512),
-                                       16, 0, 0);
+    for (int t = 0; t < KS; ++t) {
+      const int ks = kb + ss * KS + t;
+      if (ks >= ke) break;
+      _Float16* tile = xs0 + ((ss % NST) * KS + t) * XS;
+#pragma unroll
+      for (int i = 0; i < XL; ++i) {
+        const int q = i * kPfWaves + wave, tr = 4 * q + (lane >> 4), c = (lane & 15) ^ (tr & 15);
+        const int m = min(m0 + tr, a.M - 1);
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(a.A + (int64_t)m * K + ks * kPfK + c * 8),
+                                         (__attribute__((address_space(3))) void*)(tile + q * 512), 16, 0, 0);
+      }
     }
   };
 
@@ -262,18 +286,20 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
 #pragma unroll
       for (int tt = 0; tt < TT; ++tt) acc[mt][rt][tt] = f4_t{0.f, 0.f, 0.f, 0.f};
 
-  // Two-step-ahead pipeline: at step k (after its barrier) the weights and
-  // activations of step k+2 are requested; the K loop is unrolled by two so
-  // the two weight register sets keep compile-time indices.  Loads of the
-  // vector memory counter, per step and wave: WL weight / scale loads, 8
-  // activation loads.  Before step k's barrier a wave waits until at most
-  // one later step's loads are outstanding (its own step-k activation
-  // writes have landed in LDS); the barrier then makes all waves' visible.
+  // Pipeline: at super-step ss (after its barrier) the weights and
+  // activations of super-step ss + AH are requested into register set
+  // ss % AH and LDS stage (ss + AH) % NST; the loop is unrolled by AH so the
+  // weight register sets keep compile-time indices.  Loads of the vector
+  // memory counter per super-step and wave: WL weight / scale loads (when
+  // the wave's step exists) and XL per activation tile.  Before a
+  // super-step's barrier a wave waits until only later super-steps' loads
+  // are outstanding (its own activation writes of this super-step have
+  // landed in LDS); the barrier then makes all waves' visible.
   constexpr int WL = NMAT * RT * (L + (Q != CQ_QUANT_FP16 ? 1 : 0));
-  constexpr int VMC = WL + kPfTok / (4 * kPfWaves);
+  constexpr int VMC = WL + XL;                  // one later super-step (KS = 1)
   static_assert(VMC < 64, "vmcnt range");
-  u4_t wv[2][NMAT][RT][L];
-  _Float16 sv[2][NMAT][RT];
+  u4_t wv[AH][NMAT][RT][L];
+  _Float16 sv[AH][NMAT][RT];
   auto load_w_step = [&](int ks, u4_t (&w)[NMAT][RT][L], _Float16 (&s)[NMAT][RT]) {
 #pragma unroll
     for (int mt = 0; mt < NMAT; ++mt)
@@ -283,23 +309,23 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
         if constexpr (Q != CQ_QUANT_FP16) s[mt][rt] = srow[mt][rt][ks];
       }
   };
-  load_w_step(kb, wv[0], sv[0]);
-  x_issue(kb, 0);
-  if (kb + 1 < ke) {
-    load_w_step(kb + 1, wv[1], sv[1]);
-    x_issue(kb + 1, 1);
-  }
+#pragma unroll
+  for (int p = 0; p < AH; ++p)
+    if (p < nss) {
+      if (my_step(p) < ke) load_w_step(my_step(p), wv[p], sv[p]);
+      x_issue(p);
+    }
 
   const UnpackRegs uk = unpack_regs();
-  auto step = [&](auto I, int ks) {
-    constexpr int S = decltype(I)::value;   // weight register set of this step
-    const int stg = (ks - kb) % 3;
+  auto step = [&](auto I, int ss) {
+    constexpr int S = decltype(I)::value;   // weight register set of this super-step
     // simm16 of s_waitcnt on gfx9: vmcnt in bits [3:0] and [15:14], expcnt
     // [6:4] and lgkmcnt [11:8] left at their maxima
-    if (ks + 1 < ke) __builtin_amdgcn_s_waitcnt(0x0F70 | (VMC & 15) | ((VMC >> 4) << 14));
+    if (AH == 2 && ss + 1 < nss) __builtin_amdgcn_s_waitcnt(0x0F70 | (VMC & 15) | ((VMC >> 4) << 14));
     else __builtin_amdgcn_s_waitcnt(0x0F70);
     __builtin_amdgcn_s_barrier();
-    const _Float16* xb0 = xs0 + stg * XS;
+    const bool active = my_step(ss) < ke;
+    const _Float16* xb0 = xs0 + ((ss % NST) * KS + kh) * XS;
     h2_t s2[NMAT][RT];
     u4_t w[NMAT][RT][L];
 #pragma unroll
@@ -310,22 +336,19 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
 #pragma unroll
         for (int i = 0; i < L; ++i) w[mt][rt][i] = wv[S][mt][rt][i];
       }
-    if (ks + 2 < ke) {
-      load_w_step(ks + 2, wv[S], sv[S]);
-      x_issue(ks + 2, (ks + 2 - kb) % 3);
+    if (ss + AH < nss) {
+      if (my_step(ss + AH) < ke) load_w_step(my_step(ss + AH), wv[S], sv[S]);
+      x_issue(ss + AH);
     }
-    // B fragments of one sub-step (the other wave of the SIMD covers their
-    // LDS latency)
+    if (!active) return;
+    // B fragments of one sub-step
     auto read_b = [&](int s4, h8_t* xb) {
 #pragma unroll
       for (int tt = 0; tt < TT; ++tt)   // row tt*16 + r, K chunk 4j + s4 at slot (4j + s4) ^ r
         xb[tt] = *reinterpret_cast<const h8_t*>(&xb0[(tt * 16 + r) * kPfK + (((4 * j + s4) ^ r) * 8)]);
     };
-#pragma unroll
-    for (int s4 = 0; s4 < 4; ++s4) {
-      h8_t xb[TT];
-      read_b(s4, xb);
-      h8_t wa[NMAT][RT];
+    // A fragments (dequantized weights) of sub-step s4
+    auto unpack_a = [&](int s4, h8_t (&wa)[NMAT][RT]) {
 #pragma unroll
       for (int mt = 0; mt < NMAT; ++mt)
 #pragma unroll
@@ -341,22 +364,82 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
           }
           wa[mt][rt] = u;
         }
+    };
+    // Software pipeline over the four sub-steps: the B fragments (LDS) and
+    // A fragments (unpack) of sub-step s4 + 1 are produced while the matrix
+    // instructions of s4 run; the scheduling groups interleave them (the
+    // LDS reads first, then one matrix instruction and two vector
+    // instructions at a time) so the unpack co-executes with the matrix
+    // cores instead of alternating with them.
+    constexpr int NMF = NMAT * RT * TT;   // matrix instructions per sub-step
+    h8_t xb[2][TT];
+    h8_t wa[2][NMAT][RT];
+    read_b(0, xb[0]);
+    unpack_a(0, wa[0]);
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4) {
+      __builtin_amdgcn_sched_barrier(0);
+      if (s4 < 3) {
+        read_b(s4 + 1, xb[(s4 + 1) & 1]);
+        unpack_a(s4 + 1, wa[(s4 + 1) & 1]);
+      }
 #pragma unroll
       for (int tt = 0; tt < TT; ++tt)
 #pragma unroll
         for (int mt = 0; mt < NMAT; ++mt)
 #pragma unroll
           for (int rt = 0; rt < RT; ++rt)
-            acc[mt][rt][tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[mt][rt], xb[tt], acc[mt][rt][tt], 0, 0, 0);
+            acc[mt][rt][tt] =
+                __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[s4 & 1][mt][rt], xb[s4 & 1][tt], acc[mt][rt][tt], 0, 0, 0);
+      if (s4 < 3) {
+        __builtin_amdgcn_sched_group_barrier(0x100, TT, 0);   // LDS reads
+#pragma unroll
+        for (int i = 0; i < NMF; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one matrix instruction
+          __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // two vector instructions
+        }
+      }
     }
+    __builtin_amdgcn_sched_barrier(0);
   };
-  int ks = kb;
-  for (; ks + 1 < ke; ks += 2) {
-    step(std::integral_constant<int, 0>{}, ks);
-    step(std::integral_constant<int, 1>{}, ks + 1);
+  int ss = 0;
+  if constexpr (AH == 2) {
+    for (; ss + 1 < nss; ss += 2) {
+      step(std::integral_constant<int, 0>{}, ss);
+      step(std::integral_constant<int, 1>{}, ss + 1);
+    }
+    if (ss < nss) step(std::integral_constant<int, 0>{}, ss);
+  } else {
+    for (; ss < nss; ++ss) step(std::integral_constant<int, 0>{}, ss);
   }
-  if (ks < ke) step(std::integral_constant<int, 0>{}, ks);
-  __syncthreads();   // every wave's last LDS reads are done before the QKV epilogue reuses the buffers
+  __syncthreads();   // every wave's last LDS reads are done before the buffers are reused
+
+  // Two K sets: wave (g, h) finishes token slices [h*TT/2, (h+1)*TT/2) of its
+  // rows; it hands the other half to its partner (g, 1-h) through LDS and
+  // adds the partner's half of its own.
+  auto owned = [&](int tt) { return KS == 1 || tt / (TT / 2) == kh; };
+  if constexpr (KS == 2) {
+    f4_t* xch = reinterpret_cast<f4_t*>(smem);
+    auto slot = [&](int w, int mt, int rt, int tt) {
+      return ((((w * NMAT + mt) * RT + rt) * (TT / 2) + tt % (TT / 2)) * 64) + lane;
+    };
+#pragma unroll
+    for (int mt = 0; mt < NMAT; ++mt)
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int tt = 0; tt < TT; ++tt)
+          if (!owned(tt)) xch[slot(wave ^ SH::RG, mt, rt, tt)] = acc[mt][rt][tt];
+    __syncthreads();
+#pragma unroll
+    for (int mt = 0; mt < NMAT; ++mt)
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int tt = 0; tt < TT; ++tt)
+          if (owned(tt)) acc[mt][rt][tt] += xch[slot(wave, mt, rt, tt)];
+    __syncthreads();   // exchange reads done before the QKV epilogue writes its tile
+  }
 
   if constexpr (SPLIT) {
     // fp32 partial [z][mat][M][N]; the split epilogue sums and finishes
@@ -366,6 +449,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
       for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
         for (int tt = 0; tt < TT; ++tt) {
+          if (!owned(tt)) continue;
           const int n = nw0 + rt * 16 + 4 * j, m = m0 + tt * 16 + r;
           if (m < a.M && n + 3 < a.N) {
             *reinterpret_cast<f4_t*>(&a.part[(((int64_t)blockIdx.z * NMAT + mt) * a.M + m) * a.N + n]) = acc[mt][rt][tt];
@@ -387,6 +471,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
       for (int tt = 0; tt < TT; ++tt)
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
+          if (!owned(tt)) continue;
           const int n = nw0 + rt * 16 + 4 * j + v, m = m0 + tt * 16 + r;
           if (n < a.N && m < a.M) {
             _Float16* p = y + (int64_t)m * a.N + n;
@@ -400,6 +485,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
       for (int tt = 0; tt < TT; ++tt)
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
+          if (!owned(tt)) continue;
           const int n = nw0 + rt * 16 + 4 * j + v, m = m0 + tt * 16 + r;
           if (n < a.N && m < a.M) {
             const float s = a.inv[m];
@@ -420,7 +506,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
       for (int tt = 0; tt < TT; ++tt)
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-          const int nl = wave * WROWS + rt * 16 + 4 * j + v, ml = tt * 16 + r;
+          if (!owned(tt)) continue;
+          const int nl = rg * WROWS + rt * 16 + 4 * j + v, ml = tt * 16 + r;
           const int n = nb0 + nl, m = min(m0 + ml, a.M - 1);
           int local;
           const int mat = pf_mat(a, min(n, a.N - 1), &local);
@@ -878,7 +965,10 @@ int launch_pf_gemm(const PfGemmArgs& a, hipStream_t stream) {
     if (!a.inv || !a.W[1] || !a.W[2] || !a.inv_freq) return fail(CQ_EINVAL, "prefill gemm: qkv operands");
     if (a.kcache8 ? (!a.vcache8 || !a.kscale || !a.vscale) : (!a.kcache || !a.vcache))
       return fail(CQ_EINVAL, "prefill gemm: qkv cache pointers");
-    if (PfShape<CQ_QUANT_FP16, GM_QKV>::BN % a.head_dim || a.rows[0] % a.head_dim || a.rows[1] % a.head_dim || a.rows[0] + a.rows[1] + a.rows[2] != a.N)
+    const int bn = a.quant == CQ_QUANT_INT4   ? PfShape<CQ_QUANT_INT4, GM_QKV>::BN
+                   : a.quant == CQ_QUANT_INT8 ? PfShape<CQ_QUANT_INT8, GM_QKV>::BN
+                                              : PfShape<CQ_QUANT_FP16, GM_QKV>::BN;
+    if (bn % a.head_dim || a.rows[0] % a.head_dim || a.rows[1] % a.head_dim || a.rows[0] + a.rows[1] + a.rows[2] != a.N)
       return fail(CQ_EINVAL, "prefill gemm: qkv rows must be whole heads");
   }
   switch (a.quant) {
