@@ -9,6 +9,7 @@ namespace cq {
 
 typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u4_t __attribute__((ext_vector_type(4)));
 
@@ -100,16 +101,22 @@ __device__ __forceinline__ float wave_max(float v) {
 // in double) is reduced modulo 2 pi in double (2 pi split in a high and a
 // low part) and its sine and cosine taken in fp32; the rotation is rounded
 // at the same points as the reference's fp32 expression.
-__device__ __forceinline__ void rope_rotate(float& y0, float& y1, int pos, double inv_freq) {
+__device__ __forceinline__ void rope_sincos(int pos, double inv_freq, float* s, float* c) {
   const double ang = (double)pos * inv_freq;
   const double k = rint(ang * 0.15915494309189535);                                        // 1 / (2 pi)
   const double rd = fma(-k, 6.283185307179586232e+00, ang) - k * 2.4492935982947064e-16;   // 2 pi hi + lo
-  float s, c;
-  sincosf((float)rd, &s, &c);
+  sincosf((float)rd, s, c);
+}
+__device__ __forceinline__ void rope_apply(float& y0, float& y1, float s, float c) {
   const float o0 = add_rn(mul_rn(y0, c), -mul_rn(y1, s));
   const float o1 = add_rn(mul_rn(y1, c), mul_rn(y0, s));
   y0 = o0;
   y1 = o1;
+}
+__device__ __forceinline__ void rope_rotate(float& y0, float& y1, int pos, double inv_freq) {
+  float s, c;
+  rope_sincos(pos, inv_freq, &s, &c);
+  rope_apply(y0, y1, s, c);
 }
 
 // Order-preserving argmax key (kernels.cu:907-911): a larger float gives a

@@ -807,7 +807,8 @@ int prefill_batched(cq_state* s, const int32_t* tokens, int n, int pos0) {
       const size_t ls = (size_t)l * c.n_kv_heads * c.max_seq_len;
       float* ksc = kv8 ? s->kscale + ls : nullptr;
       float* vsc = kv8 ? s->vscale + ls : nullptr;
-      CQ_TRY(launch_pf_norm(s->pf_x, L.in_norm, c.norm_eps, M, d, s->pf_a, s->pf_inv, c.quant_type, st));
+      // layer l > 0: the previous layer's down GEMM left this norm in pf_a / pf_inv
+      if (l == 0) CQ_TRY(launch_pf_norm(s->pf_x, L.in_norm, c.norm_eps, M, d, s->pf_a, s->pf_inv, c.quant_type, st));
       PfGemmArgs g;
       g.mode = GM_QKV; g.quant = c.quant_type; g.A = (const _Float16*)s->pf_a; g.inv = s->pf_inv;
       g.M = M; g.N = qd + 2 * kvd; g.K = d;
@@ -835,8 +836,9 @@ int prefill_batched(cq_state* s, const int32_t* tokens, int n, int pos0) {
       o.mode = GM_RESID; o.quant = c.quant_type; o.A = (const _Float16*)s->pf_ao; o.M = M; o.N = d; o.K = qd;
       o.W[0] = L.wo; o.S[0] = (const _Float16*)L.so; o.rows[0] = d; o.out = (_Float16*)s->pf_x;
       o.part = s->pf_part; o.part_bytes = kPrefillPartBytes;
+      o.norm_w = (const _Float16*)L.post_norm; o.norm_eps = c.norm_eps;
+      o.norm_out = (_Float16*)s->pf_a; o.norm_inv = s->pf_inv;
       CQ_TRY(launch_pf_gemm(o, st));
-      CQ_TRY(launch_pf_norm(s->pf_x, L.post_norm, c.norm_eps, M, d, s->pf_a, s->pf_inv, c.quant_type, st));
       PfGemmArgs m1;
       m1.mode = GM_SWIGLU; m1.quant = c.quant_type; m1.A = (const _Float16*)s->pf_a; m1.inv = s->pf_inv;
       m1.M = M; m1.N = I; m1.K = d; m1.W[0] = L.wg; m1.W[1] = L.wu;
@@ -848,6 +850,9 @@ int prefill_batched(cq_state* s, const int32_t* tokens, int n, int pos0) {
       m2.mode = GM_RESID; m2.quant = c.quant_type; m2.A = (const _Float16*)s->pf_inter; m2.M = M; m2.N = d; m2.K = I;
       m2.W[0] = L.wd; m2.S[0] = (const _Float16*)L.sd; m2.rows[0] = d; m2.out = (_Float16*)s->pf_x;
       m2.part = s->pf_part; m2.part_bytes = kPrefillPartBytes;
+      // the next layer's input norm (every layer after this one is still to run)
+      m2.norm_w = (const _Float16*)s->w->layers[l + 1].in_norm; m2.norm_eps = c.norm_eps;
+      m2.norm_out = (_Float16*)s->pf_a; m2.norm_inv = s->pf_inv;
       CQ_TRY(launch_pf_gemm(m2, st));
     }
   }

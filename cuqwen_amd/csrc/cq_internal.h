@@ -106,6 +106,12 @@ struct PfGemmArgs {
   float* kscale = nullptr;   // [n_kv][max_seq] of this layer
   float* vscale = nullptr;
   int kv_fmt = CQ_KV_INT8;   // CQ_KV_INT8 / CQ_KV_FP8 codes
+  // RESID only, optional: RMSNorm of the updated rows (as launch_pf_norm) into
+  // norm_out / norm_inv with weight norm_w
+  const _Float16* norm_w = nullptr;
+  float norm_eps = 0.f;
+  _Float16* norm_out = nullptr;
+  float* norm_inv = nullptr;
 };
 struct PfAttnArgs {
   const _Float16* q = nullptr;   // [M][n_heads * hd] natural

@@ -33,7 +33,6 @@ namespace cq {
 constexpr int kPfWaves = 8;
 constexpr int kPfThreads = kPfWaves * 64;
 constexpr int kPfK = 128;         // K per main-loop step (one quantization group)
-constexpr int kPfTargetBlocks = 512;       // split K below this many blocks (2 per CU)
 constexpr int kPfMaxSplit = 8;
 
 // Activation layout of the GEMM inputs, chosen by the weights' format so the
@@ -51,26 +50,41 @@ __device__ __forceinline__ _Float16 pf_val(float v, int k, bool int4) {
 }
 
 // ------------------------------------------------------------- row norm
-// One block per token row: A[m] = half(x * w) (permuted), inv[m] =
-// rsqrt(mean(x^2) + half(eps)).  Without w, A = x (permuted) and no inv.
+// RMSNorm of one token row by one block (dim a multiple of 8): A row =
+// half(x * w) in the layout of the weights' format, inv = rsqrt(mean(x^2) +
+// half(eps)).  Without w, A = x (in the layout) and no inv.  Thread t takes
+// the 8-element groups t, t + blockDim.x, ... (the layout permutes within a
+// group, so each group is one 16-byte load and one 16-byte store).
+__device__ __forceinline__ void pf_norm_row(const _Float16* xr, const _Float16* w, float eps, int dim, _Float16* ar,
+                                            float* inv_m, bool int4, float* red) {
+  float ss = 0.f;
+  for (int g = threadIdx.x; g < dim / 8; g += blockDim.x) {
+    const h8_t xv = __builtin_bit_cast(h8_t, load_u4(xr + 8 * g));
+    h8_t wv;
+    if (w) wv = __builtin_bit_cast(h8_t, load_u4(w + 8 * g));
+    h8_t o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float v = (float)xv[e];
+      ss = fmaf(v, v, ss);
+      // half(x * w) first (the decode GEMVs' staging), then the layout's scale
+      const float y = w ? (float)(_Float16)(v * (float)wv[e]) : v;
+      o[pf_pos(e, int4)] = pf_val(y, e, int4);
+    }
+    *reinterpret_cast<u4_t*>(ar + 8 * g) = __builtin_bit_cast(u4_t, o);
+  }
+  if (w) {
+    ss = block_sum(ss, red);
+    if (threadIdx.x == 0) *inv_m = rsqrtf(ss / (float)dim + (float)(_Float16)eps);
+  }
+}
+
+// One block per token row.
 __global__ __launch_bounds__(256) void pf_norm_rows(const _Float16* x, const _Float16* w, float eps, int dim,
                                                     _Float16* A, float* inv, bool int4) {
   __shared__ float red[16];
   const int m = blockIdx.x;
-  const _Float16* xr = x + (int64_t)m * dim;
-  _Float16* ar = A + (int64_t)m * dim;
-  float ss = 0.f;
-  for (int k = threadIdx.x; k < dim; k += blockDim.x) {
-    const float v = (float)xr[k];
-    ss = fmaf(v, v, ss);
-    // half(x * w) first (the decode GEMVs' staging), then the layout's scale
-    const float y = w ? (float)(_Float16)(v * (float)w[k]) : v;
-    ar[pf_pos(k, int4)] = pf_val(y, k, int4);
-  }
-  if (w) {
-    ss = block_sum(ss, red);
-    if (threadIdx.x == 0) inv[m] = rsqrtf(ss / (float)dim + (float)(_Float16)eps);
-  }
+  pf_norm_row(x + (int64_t)m * dim, w, eps, dim, A + (int64_t)m * dim, inv + m, int4, red);
 }
 
 // Embedding rows of the chunk's tokens (kernels.cu:85-103).
@@ -168,31 +182,18 @@ __device__ __forceinline__ void pf_load_w(const PfGemmArgs& a, const char* rowp,
   for (int i = 0; i < L; ++i) w[i] = load_u4(p + i * 16);
 }
 
-// Tile shape: RT 16-row slices per wave in all (SwiGLU: RT/2 gate and RT/2 up
+// Tile shape: RT 16-row slices per wave (SwiGLU: RT/2 gate and RT/2 up
 // slices of the same output rows), 8 token slices of 16 per wave (the unpack
 // of a weight fragment is shared by 8 matrix instructions); a block is 8
-// waves over the same 128 tokens, two per SIMD.  With KS = 2 the waves form
-// two sets over the same rows: set h takes every other K step (kb + 2i + h),
-// so each wave reads half of the activation tiles from LDS for the same
-// matrix work (LDS read bytes per flop fall with the rows per wave), and the
-// two sets add their accumulators through LDS at the end.
-template <int Q> struct PfTile;
-template <> struct PfTile<CQ_QUANT_INT4> { static constexpr int RT = 2, KS = 1; };
-template <> struct PfTile<CQ_QUANT_INT8> { static constexpr int RT = 2, KS = 1; };
-template <> struct PfTile<CQ_QUANT_FP16> { static constexpr int RT = 2, KS = 1; };
+// waves over the same 128 tokens, two per SIMD.
+template <int Q> struct PfTile { static constexpr int RT = 2; };
 constexpr int kPfTT = 8;                         // token slices per wave
 constexpr int kPfTok = 16 * kPfTT;               // tokens per block
 template <int Q, int MODE> struct PfShape {
   static constexpr int NMAT = MODE == GM_SWIGLU ? 2 : 1;
   static constexpr int RT = PfTile<Q>::RT / NMAT;   // row slices per matrix
-  static constexpr int KS = PfTile<Q>::KS;           // wave sets splitting the K steps
-  static constexpr int RG = kPfWaves / KS;           // waves per set (row groups)
   static constexpr int WROWS = RT * 16;              // output rows per wave
-  static constexpr int BN = RG * WROWS;              // output rows per block
-  // LDS stages of KS activation tiles, and how many super-steps (KS K steps)
-  // ahead loads are issued: 3 stages / 2 ahead for one set, 2 / 1 for two
-  static constexpr int NST = KS == 2 ? 2 : 3;
-  static constexpr int AH = NST - 1;
+  static constexpr int BN = kPfWaves * WROWS;        // output rows per block
 };
 
 // The block's (row block, token block) from its dispatch index, so that all
@@ -216,29 +217,23 @@ template <int Q, int MODE, bool SPLIT>
 __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs a) {
   using SH = PfShape<Q, MODE>;
   constexpr int NMAT = SH::NMAT, RT = SH::RT, WROWS = SH::WROWS, BN = SH::BN, TT = kPfTT;
-  constexpr int KS = SH::KS, NST = SH::NST, AH = SH::AH;
   constexpr int L = PfW<Q>::LOADS;
-  constexpr int XS = kPfTok * kPfK;                         // halves of one activation tile
-  constexpr int SM = NST * KS * XS;
+  constexpr int XS = kPfTok * kPfK;                         // halves of one activation stage
   constexpr int OT = MODE == GM_QKV ? BN * kPfTok : 0;      // QKV epilogue tile (rows x tokens)
-  static_assert(OT <= SM && (KS == 1 || kPfWaves * NMAT * RT * (TT / 2) * 64 * 8 <= SM), "LDS reuse");
-  __shared__ __align__(16) _Float16 smem[SM];
+  __shared__ __align__(16) _Float16 smem[3 * XS > OT ? 3 * XS : OT];
   _Float16* xs0 = smem;
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-  const int rg = wave % SH::RG, kh = wave / SH::RG;   // row group, K set
   const int r = lane & 15, j = lane >> 4;
   const int n_tb = (a.M + kPfTok - 1) / kPfTok;
   int rb, tb;
   pf_block_tile(n_tb, &rb, &tb);
   const int m0 = tb * kPfTok;
   const int nb0 = rb * BN;                     // first output row of the block
-  const int nw0 = nb0 + rg * WROWS;            // first output row of the wave
+  const int nw0 = nb0 + wave * WROWS;          // first output row of the wave
   const int K = a.K, nks = K / kPfK;
   // split-K: block z of gridDim.z sums K steps [kb, ke) into an fp32 partial
   const int kb = SPLIT ? (int)((int64_t)blockIdx.z * nks / gridDim.z) : 0;
   const int ke = SPLIT ? (int)((int64_t)(blockIdx.z + 1) * nks / gridDim.z) : nks;
-  const int nss = (ke - kb + KS - 1) / KS;     // super-steps of KS K steps
-  auto my_step = [&](int ss) { return kb + ss * KS + kh; };   // this wave's K step (valid below ke)
 
   // weight row (A operand row r of each slice) and its scale row
   const char* rowp[NMAT][RT];
@@ -256,25 +251,20 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
     }
 
   // Activation tiles go global -> LDS directly (global_load_lds_dwordx4, no
-  // registers).  A tile holds 128 token rows of 256 bytes; 16-byte slot s of
-  // row t holds K chunk s ^ (t & 15), so the B-operand reads (16 rows at one
-  // chunk) hit 16 different bank groups.  Load q of a tile (q = i * waves +
-  // wave) fills rows 4q .. 4q + 3: lane l writes row 4q + l / 16, slot l % 16.
-  // Stage g holds the KS tiles of one super-step.
-  constexpr int XL = kPfTok / (4 * kPfWaves);   // loads per lane per tile
-  auto x_issue = [&](int ss) {
+  // registers), three stages deep.  A stage holds 128 token rows of 256 bytes;
+  // 16-byte slot s of row t holds K chunk s ^ (t & 15), so the B-operand
+  // reads (16 rows at one chunk) hit 16 different bank groups.  Load q of a
+  // step (q = i * waves + wave) fills rows 4q .. 4q + 3: lane l writes
+  // row 4q + l / 16, slot l % 16.
+  auto x_issue = [&](int ks, int stg) {
 #pragma unroll
-    for (int t = 0; t < KS; ++t) {
-      const int ks = kb + ss * KS + t;
-      if (ks >= ke) break;
-      _Float16* tile = xs0 + ((ss % NST) * KS + t) * XS;
-#pragma unroll
-      for (int i = 0; i < XL; ++i) {
-        const int q = i * kPfWaves + wave, tr = 4 * q + (lane >> 4), c = (lane & 15) ^ (tr & 15);
-        const int m = min(m0 + tr, a.M - 1);
-        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(a.A + (int64_t)m * K + ks * kPfK + c * 8),
-                                         (__attribute__((address_space(3))) void*)(tile + q * 512), 16, 0, 0);
-      }
+    for (int i = 0; i < kPfTok / (4 * kPfWaves); ++i) {
+      const int q = i * kPfWaves + wave, t = 4 * q + (lane >> 4), c = (lane & 15) ^ (t & 15);
+      const int m = min(m0 + t, a.M - 1);
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(a.A + (int64_t)m * K + ks * kPfK + c * 8),
+                                       (__attribute__((address_space(3))) void*)(
+                                           xs0 + stg * XS + q * 512),
+                                       16, 0, 0);
     }
   };
 
@@ -286,20 +276,18 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
 #pragma unroll
       for (int tt = 0; tt < TT; ++tt) acc[mt][rt][tt] = f4_t{0.f, 0.f, 0.f, 0.f};
 
-  // Pipeline: at super-step ss (after its barrier) the weights and
-  // activations of super-step ss + AH are requested into register set
-  // ss % AH and LDS stage (ss + AH) % NST; the loop is unrolled by AH so the
-  // weight register sets keep compile-time indices.  Loads of the vector
-  // memory counter per super-step and wave: WL weight / scale loads (when
-  // the wave's step exists) and XL per activation tile.  Before a
-  // super-step's barrier a wave waits until only later super-steps' loads
-  // are outstanding (its own activation writes of this super-step have
-  // landed in LDS); the barrier then makes all waves' visible.
+  // Two-step-ahead pipeline: at step k (after its barrier) the weights and
+  // activations of step k+2 are requested; the K loop is unrolled by two so
+  // the two weight register sets keep compile-time indices.  Loads of the
+  // vector memory counter, per step and wave: WL weight / scale loads, 8
+  // activation loads.  Before step k's barrier a wave waits until at most
+  // one later step's loads are outstanding (its own step-k activation
+  // writes have landed in LDS); the barrier then makes all waves' visible.
   constexpr int WL = NMAT * RT * (L + (Q != CQ_QUANT_FP16 ? 1 : 0));
-  constexpr int VMC = WL + XL;                  // one later super-step (KS = 1)
+  constexpr int VMC = WL + kPfTok / (4 * kPfWaves);
   static_assert(VMC < 64, "vmcnt range");
-  u4_t wv[AH][NMAT][RT][L];
-  _Float16 sv[AH][NMAT][RT];
+  u4_t wv[2][NMAT][RT][L];
+  _Float16 sv[2][NMAT][RT];
   auto load_w_step = [&](int ks, u4_t (&w)[NMAT][RT][L], _Float16 (&s)[NMAT][RT]) {
 #pragma unroll
     for (int mt = 0; mt < NMAT; ++mt)
@@ -309,23 +297,23 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
         if constexpr (Q != CQ_QUANT_FP16) s[mt][rt] = srow[mt][rt][ks];
       }
   };
-#pragma unroll
-  for (int p = 0; p < AH; ++p)
-    if (p < nss) {
-      if (my_step(p) < ke) load_w_step(my_step(p), wv[p], sv[p]);
-      x_issue(p);
-    }
+  load_w_step(kb, wv[0], sv[0]);
+  x_issue(kb, 0);
+  if (kb + 1 < ke) {
+    load_w_step(kb + 1, wv[1], sv[1]);
+    x_issue(kb + 1, 1);
+  }
 
   const UnpackRegs uk = unpack_regs();
-  auto step = [&](auto I, int ss) {
-    constexpr int S = decltype(I)::value;   // weight register set of this super-step
+  auto step = [&](auto I, int ks) {
+    constexpr int S = decltype(I)::value;   // weight register set of this step
+    const int stg = (ks - kb) % 3;
     // simm16 of s_waitcnt on gfx9: vmcnt in bits [3:0] and [15:14], expcnt
     // [6:4] and lgkmcnt [11:8] left at their maxima
-    if (AH == 2 && ss + 1 < nss) __builtin_amdgcn_s_waitcnt(0x0F70 | (VMC & 15) | ((VMC >> 4) << 14));
+    if (ks + 1 < ke) __builtin_amdgcn_s_waitcnt(0x0F70 | (VMC & 15) | ((VMC >> 4) << 14));
     else __builtin_amdgcn_s_waitcnt(0x0F70);
     __builtin_amdgcn_s_barrier();
-    const bool active = my_step(ss) < ke;
-    const _Float16* xb0 = xs0 + ((ss % NST) * KS + kh) * XS;
+    const _Float16* xb0 = xs0 + stg * XS;
     h2_t s2[NMAT][RT];
     u4_t w[NMAT][RT][L];
 #pragma unroll
@@ -336,11 +324,10 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
 #pragma unroll
         for (int i = 0; i < L; ++i) w[mt][rt][i] = wv[S][mt][rt][i];
       }
-    if (ss + AH < nss) {
-      if (my_step(ss + AH) < ke) load_w_step(my_step(ss + AH), wv[S], sv[S]);
-      x_issue(ss + AH);
+    if (ks + 2 < ke) {
+      load_w_step(ks + 2, wv[S], sv[S]);
+      x_issue(ks + 2, (ks + 2 - kb) % 3);
     }
-    if (!active) return;
     // B fragments of one sub-step
     auto read_b = [&](int s4, h8_t* xb) {
 #pragma unroll
@@ -365,81 +352,64 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
           wa[mt][rt] = u;
         }
     };
-    // Software pipeline over the four sub-steps: the B fragments (LDS) and
-    // A fragments (unpack) of sub-step s4 + 1 are produced while the matrix
-    // instructions of s4 run; the scheduling groups interleave them (the
-    // LDS reads first, then one matrix instruction and two vector
-    // instructions at a time) so the unpack co-executes with the matrix
-    // cores instead of alternating with them.
     constexpr int NMF = NMAT * RT * TT;   // matrix instructions per sub-step
-    h8_t xb[2][TT];
-    h8_t wa[2][NMAT][RT];
-    read_b(0, xb[0]);
-    unpack_a(0, wa[0]);
-#pragma unroll
-    for (int s4 = 0; s4 < 4; ++s4) {
-      __builtin_amdgcn_sched_barrier(0);
-      if (s4 < 3) {
-        read_b(s4 + 1, xb[(s4 + 1) & 1]);
-        unpack_a(s4 + 1, wa[(s4 + 1) & 1]);
-      }
+    auto mfma_all = [&](const h8_t (&wa)[NMAT][RT], const h8_t* xb) {
 #pragma unroll
       for (int tt = 0; tt < TT; ++tt)
 #pragma unroll
         for (int mt = 0; mt < NMAT; ++mt)
 #pragma unroll
           for (int rt = 0; rt < RT; ++rt)
-            acc[mt][rt][tt] =
-                __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[s4 & 1][mt][rt], xb[s4 & 1][tt], acc[mt][rt][tt], 0, 0, 0);
-      if (s4 < 3) {
-        __builtin_amdgcn_sched_group_barrier(0x100, TT, 0);   // LDS reads
+            acc[mt][rt][tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[mt][rt], xb[tt], acc[mt][rt][tt], 0, 0, 0);
+    };
+    if constexpr (Q == CQ_QUANT_INT4) {
+      // Software pipeline over the four sub-steps: the B fragments (LDS) and
+      // A fragments (unpack) of sub-step s4 + 1 are produced while the
+      // matrix instructions of s4 run; the scheduling groups interleave them
+      // (the LDS reads first, then one matrix instruction and two vector
+      // instructions at a time) so the unpack co-executes with the matrix
+      // cores instead of alternating with them.  (The int8 / fp16 weight
+      // registers leave no room for the second fragment set.)
+      h8_t xb[2][TT];
+      h8_t wa[2][NMAT][RT];
+      read_b(0, xb[0]);
+      unpack_a(0, wa[0]);
 #pragma unroll
-        for (int i = 0; i < NMF; ++i) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one matrix instruction
-          __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // two vector instructions
+      for (int s4 = 0; s4 < 4; ++s4) {
+        __builtin_amdgcn_sched_barrier(0);
+        if (s4 < 3) {
+          read_b(s4 + 1, xb[(s4 + 1) & 1]);
+          unpack_a(s4 + 1, wa[(s4 + 1) & 1]);
+        }
+        mfma_all(wa[s4 & 1], xb[s4 & 1]);
+        if (s4 < 3) {
+          __builtin_amdgcn_sched_group_barrier(0x100, TT, 0);   // LDS reads
+#pragma unroll
+          for (int i = 0; i < NMF; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one matrix instruction
+            __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // two vector instructions
+          }
         }
       }
+      __builtin_amdgcn_sched_barrier(0);
+    } else {
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) {
+        h8_t xb[TT];
+        h8_t wa[NMAT][RT];
+        read_b(s4, xb);
+        unpack_a(s4, wa);
+        mfma_all(wa, xb);
+      }
     }
-    __builtin_amdgcn_sched_barrier(0);
   };
-  int ss = 0;
-  if constexpr (AH == 2) {
-    for (; ss + 1 < nss; ss += 2) {
-      step(std::integral_constant<int, 0>{}, ss);
-      step(std::integral_constant<int, 1>{}, ss + 1);
-    }
-    if (ss < nss) step(std::integral_constant<int, 0>{}, ss);
-  } else {
-    for (; ss < nss; ++ss) step(std::integral_constant<int, 0>{}, ss);
+  int ks = kb;
+  for (; ks + 1 < ke; ks += 2) {
+    step(std::integral_constant<int, 0>{}, ks);
+    step(std::integral_constant<int, 1>{}, ks + 1);
   }
-  __syncthreads();   // every wave's last LDS reads are done before the buffers are reused
-
-  // Two K sets: wave (g, h) finishes token slices [h*TT/2, (h+1)*TT/2) of its
-  // rows; it hands the other half to its partner (g, 1-h) through LDS and
-  // adds the partner's half of its own.
-  auto owned = [&](int tt) { return KS == 1 || tt / (TT / 2) == kh; };
-  if constexpr (KS == 2) {
-    f4_t* xch = reinterpret_cast<f4_t*>(smem);
-    auto slot = [&](int w, int mt, int rt, int tt) {
-      return ((((w * NMAT + mt) * RT + rt) * (TT / 2) + tt % (TT / 2)) * 64) + lane;
-    };
-#pragma unroll
-    for (int mt = 0; mt < NMAT; ++mt)
-#pragma unroll
-      for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-        for (int tt = 0; tt < TT; ++tt)
-          if (!owned(tt)) xch[slot(wave ^ SH::RG, mt, rt, tt)] = acc[mt][rt][tt];
-    __syncthreads();
-#pragma unroll
-    for (int mt = 0; mt < NMAT; ++mt)
-#pragma unroll
-      for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-        for (int tt = 0; tt < TT; ++tt)
-          if (owned(tt)) acc[mt][rt][tt] += xch[slot(wave, mt, rt, tt)];
-    __syncthreads();   // exchange reads done before the QKV epilogue writes its tile
-  }
+  if (ks < ke) step(std::integral_constant<int, 0>{}, ks);
+  __syncthreads();   // every wave's last LDS reads are done before the QKV epilogue reuses the buffers
 
   if constexpr (SPLIT) {
     // fp32 partial [z][mat][M][N]; the split epilogue sums and finishes
@@ -449,7 +419,6 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
       for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
         for (int tt = 0; tt < TT; ++tt) {
-          if (!owned(tt)) continue;
           const int n = nw0 + rt * 16 + 4 * j, m = m0 + tt * 16 + r;
           if (m < a.M && n + 3 < a.N) {
             *reinterpret_cast<f4_t*>(&a.part[(((int64_t)blockIdx.z * NMAT + mt) * a.M + m) * a.N + n]) = acc[mt][rt][tt];
@@ -471,7 +440,6 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
       for (int tt = 0; tt < TT; ++tt)
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-          if (!owned(tt)) continue;
           const int n = nw0 + rt * 16 + 4 * j + v, m = m0 + tt * 16 + r;
           if (n < a.N && m < a.M) {
             _Float16* p = y + (int64_t)m * a.N + n;
@@ -485,7 +453,6 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
       for (int tt = 0; tt < TT; ++tt)
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-          if (!owned(tt)) continue;
           const int n = nw0 + rt * 16 + 4 * j + v, m = m0 + tt * 16 + r;
           if (n < a.N && m < a.M) {
             const float s = a.inv[m];
@@ -506,8 +473,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
       for (int tt = 0; tt < TT; ++tt)
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-          if (!owned(tt)) continue;
-          const int nl = rg * WROWS + rt * 16 + 4 * j + v, ml = tt * 16 + r;
+          const int nl = wave * WROWS + rt * 16 + 4 * j + v, ml = tt * 16 + r;
           const int n = nb0 + nl, m = min(m0 + ml, a.M - 1);
           int local;
           const int mat = pf_mat(a, min(n, a.N - 1), &local);
@@ -554,68 +520,151 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
   }
 }
 
-// Split-K epilogue: sums the S partials of each output and applies the
-// mode's epilogue (the same arithmetic as the fused epilogues above).
-template <int MODE>
-__global__ __launch_bounds__(256) void pf_split_epilogue(const PfGemmArgs a, int S) {
+// Split-K epilogue of the SwiGLU GEMM: sums the S partials of each output
+// and applies the fused epilogue's arithmetic.
+__global__ __launch_bounds__(256) void pf_split_swiglu(const PfGemmArgs a, int S) {
   const int64_t MN = (int64_t)a.M * a.N;
-  const int NMAT = MODE == GM_SWIGLU ? 2 : 1;
-  auto sum = [&](int mt, int m, int n) {
+  auto sum = [&](int mt, int64_t i) {
     float v = 0.f;
-    for (int z = 0; z < S; ++z) v += a.part[((int64_t)z * NMAT + mt) * MN + (int64_t)m * a.N + n];
+    for (int z = 0; z < S; ++z) v += a.part[((int64_t)z * 2 + mt) * MN + i];
     return v;
   };
-  if constexpr (MODE == GM_QKV) {
-    const int hd = a.head_dim, half = hd / 2, np = a.N / 2;
-    // fp16 value of row n (bias added, before RoPE) of token m
-    auto raw = [&](int m, int n) {
-      int local;
-      const int mat = pf_mat(a, n, &local);
-      const _Float16* b = a.bias[mat];
-      return (float)(_Float16)(sum(0, m, n) * a.inv[m] + (b ? (float)b[local] : 0.f));
-    };
-    const int np_store = a.kcache8 ? a.rows[0] / 2 : np;   // quantized cache: k / v rows go per head below
-    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < (int64_t)a.M * np_store;
-         idx += (int64_t)gridDim.x * blockDim.x) {
-      const int m = (int)(idx / np_store), p = (int)(idx % np_store);
-      const int n0 = (p / half) * hd + p % half, n1 = n0 + half;
-      int local;
-      const int mat = pf_mat(a, n0, &local);
-      float y0 = raw(m, n0), y1 = raw(m, n1);
-      if (mat < 2) rope_rotate(y0, y1, a.pos0 + m, a.inv_freq[local % hd]);
-      pf_qkv_store(a, mat, local, m, (_Float16)y0, (_Float16)y1);
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < MN; idx += (int64_t)gridDim.x * blockDim.x) {
+    const int m = (int)(idx / a.N), n = (int)(idx % a.N);
+    const float g = sum(0, idx) * a.inv[m], u = sum(1, idx) * a.inv[m];
+    const float sig = 1.f / (1.f + expf(-g));
+    a.out[(int64_t)m * a.N + pf_pos(n, a.quant == CQ_QUANT_INT4)] =
+        pf_val((float)(_Float16)((g * sig) * u), n, a.quant == CQ_QUANT_INT4);
+  }
+}
+
+// Split-K epilogue of a residual GEMM, one block per token row (N a
+// multiple of 8): x = half(x + sum of the S partials), then, when asked, the
+// RMSNorm of the new row (the next GEMM's input) in the same pass.
+constexpr int kPfResidThreads = 512;   // one 8-element group per thread up to 4096-wide rows
+__global__ __launch_bounds__(kPfResidThreads) void pf_split_resid(const PfGemmArgs a, int S) {
+  __shared__ float red[16];
+  const int m = blockIdx.x;
+  const int64_t MN = (int64_t)a.M * a.N;
+  _Float16* xr = a.out + (int64_t)m * a.N;
+  for (int g = threadIdx.x; g < a.N / 8; g += blockDim.x) {
+    float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+    for (int z = 0; z < S; ++z) {
+      const f4_t* pz = reinterpret_cast<const f4_t*>(a.part + z * MN + (int64_t)m * a.N + 8 * g);
+      const f4_t p0 = pz[0], p1 = pz[1];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[e] += p0[e];
+        v[4 + e] += p1[e];
+      }
     }
-    if (a.kcache8) {
-      const int n_kv = a.rows[1] / hd;
-      for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < (int64_t)a.M * 2 * n_kv;
-           idx += (int64_t)gridDim.x * blockDim.x) {
-        const int m = (int)(idx / (2 * n_kv)), r = (int)(idx % (2 * n_kv));
-        const int mat = 1 + r / n_kv, kvh = r % n_kv;
-        const int nb = a.rows[0] + (mat == 2 ? a.rows[1] : 0) + kvh * hd;
-        // element d of the rotated (k) or plain (v) row, recomputed per use
-        auto value = [&](int d) {
-          const int i = d % half;
-          float y0 = raw(m, nb + i), y1 = raw(m, nb + i + half);
-          if (mat == 1) rope_rotate(y0, y1, a.pos0 + m, a.inv_freq[i]);
-          return (float)(_Float16)(d < half ? y0 : y1);
-        };
-        float amax = 0.f;
-        for (int d = 0; d < hd; ++d) amax = fmaxf(amax, fabsf(value(d)));
-        pf_kv8_store(a, mat, kvh, a.pos0 + m, amax, value);
+    h8_t x = __builtin_bit_cast(h8_t, load_u4(xr + 8 * g));
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = (_Float16)((float)x[e] + v[e]);   // residual stays fp16 (kernels.cu:621)
+    *reinterpret_cast<u4_t*>(xr + 8 * g) = __builtin_bit_cast(u4_t, x);
+  }
+  // the norm reads back the groups this thread has just written
+  if (a.norm_w)
+    pf_norm_row(xr, a.norm_w, a.norm_eps, a.N, a.norm_out + (int64_t)m * a.N, a.norm_inv + m,
+                a.quant == CQ_QUANT_INT4, red);
+}
+
+// Split-K epilogue of the QKV GEMM, blockIdx.x = token: sums the partials,
+// applies the norm scale and bias (q / k / v are fp16 before RoPE,
+// kernels.cu:470), rotates q and k with the token's sines and cosines
+// (computed once per block) and stores q, and k / v into the cache; block y
+// takes pairs [1024 y, 1024 y + 1024), four per thread.  A quantized cache takes each (k or v,
+// kv head) row through one wave of the blocks past the pairs.
+constexpr int kPfQkvThreads = 256;
+template <int HD>
+__global__ __launch_bounds__(kPfQkvThreads) void pf_split_qkv(const PfGemmArgs a, int S) {
+  constexpr int HALF = HD / 2;
+  __shared__ float sn[HALF], cs[HALF];
+  const int m = blockIdx.x, pos = a.pos0 + m;
+  const int64_t MN = (int64_t)a.M * a.N;
+  for (int i = threadIdx.x; i < HALF; i += blockDim.x) rope_sincos(pos, a.inv_freq[i], &sn[i], &cs[i]);
+  __syncthreads();
+  const float inv = a.inv[m];
+  const float* prow = a.part + (int64_t)m * a.N;
+  // fp16 value of row n (bias added, before RoPE)
+  auto raw = [&](int n) {
+    float v = 0.f;
+#pragma unroll 4
+    for (int z = 0; z < S; ++z) v += prow[z * MN + n];
+    int local;
+    const int mat = pf_mat(a, n, &local);
+    const _Float16* b = a.bias[mat];
+    return (float)(_Float16)(v * inv + (b ? (float)b[local] : 0.f));
+  };
+  const int np_store = (a.kcache8 ? a.rows[0] : a.N) / 2;   // quantized cache: k / v rows go per head below
+  const int pair_blocks = (np_store / 4 + kPfQkvThreads - 1) / kPfQkvThreads;
+  if ((int)blockIdx.y < pair_blocks) {
+    // four consecutive pairs (i .. i+3, i + HALF .. i + HALF + 3) per thread
+    const int p = 4 * (blockIdx.y * kPfQkvThreads + threadIdx.x);
+    if (p >= np_store) return;
+    const int i = p % HALF, n0 = (p / HALF) * HD + i;
+    int local;
+    const int mat = pf_mat(a, n0, &local);
+    f4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+    for (int z = 0; z < S; ++z) {
+      s0 += *reinterpret_cast<const f4_t*>(prow + z * MN + n0);
+      s1 += *reinterpret_cast<const f4_t*>(prow + z * MN + n0 + HALF);
+    }
+    const _Float16* b = a.bias[mat];
+    float y0[4], y1[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      y0[e] = (float)(_Float16)(s0[e] * inv + (b ? (float)b[local + e] : 0.f));
+      y1[e] = (float)(_Float16)(s1[e] * inv + (b ? (float)b[local + HALF + e] : 0.f));
+      if (mat < 2) rope_apply(y0[e], y1[e], sn[i + e], cs[i + e]);
+    }
+    h4_t h0, h1;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      h0[e] = (_Float16)y0[e];
+      h1[e] = (_Float16)y1[e];
+    }
+    if (mat == 0) {
+      *reinterpret_cast<h4_t*>(a.out + (int64_t)m * a.rows[0] + local) = h0;
+      *reinterpret_cast<h4_t*>(a.out + (int64_t)m * a.rows[0] + local + HALF) = h1;
+    } else if (mat == 1) {   // four consecutive elements of a K row are contiguous in the tiled cache
+      const int kvh = local / HD;
+      *reinterpret_cast<h4_t*>(a.kcache + kv_k_offset(kvh, pos, i, a.max_seq, HD)) = h0;
+      *reinterpret_cast<h4_t*>(a.kcache + kv_k_offset(kvh, pos, i + HALF, a.max_seq, HD)) = h1;
+    } else {
+      const int kvh = local / HD;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        a.vcache[kv_v_offset(kvh, pos, i + e, a.max_seq, HD)] = h0[e];
+        a.vcache[kv_v_offset(kvh, pos, i + HALF + e, a.max_seq, HD)] = h1[e];
       }
     }
   } else {
-    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < MN; idx += (int64_t)gridDim.x * blockDim.x) {
-      const int m = (int)(idx / a.N), n = (int)(idx % a.N);
-      if constexpr (MODE == GM_RESID) {
-        _Float16* p = a.out + idx;
-        *p = (_Float16)((float)*p + sum(0, m, n));
-      } else {
-        const float g = sum(0, m, n) * a.inv[m], u = sum(1, m, n) * a.inv[m];
-        const float sig = 1.f / (1.f + expf(-g));
-        a.out[(int64_t)m * a.N + pf_pos(n, a.quant == CQ_QUANT_INT4)] =
-            pf_val((float)(_Float16)((g * sig) * u), n, a.quant == CQ_QUANT_INT4);
+    constexpr int E = HD / kWave;   // consecutive elements per lane
+    const int lane = threadIdx.x & (kWave - 1), n_kv = a.rows[1] / HD;
+    const int r = (blockIdx.y - pair_blocks) * (kPfQkvThreads / kWave) + threadIdx.x / kWave;
+    if (r < 2 * n_kv) {
+      const int mat = 1 + r / n_kv, kvh = r % n_kv;
+      const int nb = a.rows[0] + (mat == 2 ? a.rows[1] : 0) + kvh * HD;
+      float x[E];
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const int d = lane * E + e, i = d % HALF;
+        float y0 = raw(nb + i), y1 = raw(nb + i + HALF);
+        if (mat == 1) rope_apply(y0, y1, sn[i], cs[i]);
+        x[e] = (float)(_Float16)(d < HALF ? y0 : y1);
       }
+      int8_t q[E];
+      const float sc = a.kv_fmt == CQ_KV_FP8 ? quant_row8_wave<HD, CQ_KV_FP8>(x, q) : quant_row8_wave<HD, CQ_KV_INT8>(x, q);
+      int8_t* c = mat == 1 ? a.kcache8 : a.vcache8;
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const int d = lane * E + e;
+        c[mat == 1 ? kv_k_offset(kvh, pos, d, a.max_seq, HD) : kv_v_offset(kvh, pos, d, a.max_seq, HD)] = q[e];
+      }
+      if (lane == 0) (mat == 1 ? a.kscale : a.vscale)[(int64_t)kvh * a.max_seq + pos] = sc;
     }
   }
 }
@@ -904,6 +953,7 @@ __global__ __launch_bounds__(256) void pf_row_natural(const _Float16* src, _Floa
 // ------------------------------------------------------------------ host
 int launch_pf_norm(const __half* x, const __half* w, float eps, int M, int dim, __half* A, float* inv,
                    int quant, hipStream_t stream) {
+  if (M <= 0 || dim <= 0 || dim % 8) return fail(CQ_EINVAL, "prefill norm: rows must be a multiple of 8 wide");
   hipLaunchKernelGGL(pf_norm_rows, dim3(M), dim3(256), 0, stream, (const _Float16*)x, (const _Float16*)w, eps, dim,
                      (_Float16*)A, inv, quant == CQ_QUANT_INT4);
   CQ_HIP(hipGetLastError());
@@ -929,21 +979,46 @@ static int launch_pf_gemm_m(const PfGemmArgs& a, hipStream_t stream) {
   const int bn = PfShape<Q, MODE>::BN;
   const int gx = ((a.N + bn - 1) / bn) * ((a.M + kPfTok - 1) / kPfTok);   // row blocks x token blocks
   const int nks = a.K / kPfK, nmat = MODE == GM_SWIGLU ? 2 : 1;
-  // split K until the grid holds ~2 blocks per CU (small M), within the workspace
+  // Split K when it shortens the GEMM plus its split epilogue.  Model: one
+  // block fits a CU (its LDS), so B blocks take ceil(B / CUs) rounds and S
+  // splits ceil(S B / CUs) rounds of 1/S the work; a full-K block runs at
+  // ~3.2 TFLOP/s per CU (measured, int4 gate/up); the split epilogue streams
+  // the S fp32 partials at ~5 TB/s after a launch of ~2 us.  Within the
+  // workspace.
   int S = 1;
-  const int blocks = gx;
-  if (blocks < kPfTargetBlocks && a.part) {
-    S = std::min({kPfMaxSplit, (kPfTargetBlocks + blocks - 1) / blocks, nks});
-    while (S > 1 && (size_t)S * nmat * a.M * a.N * sizeof(float) > a.part_bytes) --S;
+  if (a.part) {
+    auto rounds = [&](int s) { return (double)(((int64_t)gx * s + kNumCUs - 1) / kNumCUs); };
+    const double t1 = (double)bn * nmat * kPfTok * a.K * 2 / 3.2e6;     // us, one round of full-K blocks
+    const double part_us = (double)nmat * a.M * a.N * sizeof(float) / 5e6;   // us per split of partials
+    double best = rounds(1) * t1;
+    for (int s = 2; s <= std::min(kPfMaxSplit, nks); ++s) {
+      if ((size_t)s * nmat * a.M * a.N * sizeof(float) > a.part_bytes) break;
+      const double t = rounds(s) / s * t1 + s * part_us + 2.0;
+      if (t < best) { best = t; S = s; }
+    }
   }
   if (S > 1) {
     hipLaunchKernelGGL((pf_gemm_kernel<Q, MODE, true>), dim3(gx, 1, S), dim3(kPfThreads), 0, stream, a);
     CQ_HIP(hipGetLastError());
-    const int64_t work = MODE == GM_QKV ? (int64_t)a.M * a.N / 2 : (int64_t)a.M * a.N;
-    const int eb = (int)std::min<int64_t>((work + 255) / 256, 4096);
-    hipLaunchKernelGGL((pf_split_epilogue<MODE>), dim3(eb), dim3(256), 0, stream, a, S);
+    if constexpr (MODE == GM_QKV) {
+      const int np_store = (a.kcache8 ? a.rows[0] : a.N) / 2, waves = kPfQkvThreads / kWave;
+      const int ny = (np_store / 4 + kPfQkvThreads - 1) / kPfQkvThreads +
+                     (a.kcache8 ? (2 * (a.rows[1] / a.head_dim) + waves - 1) / waves : 0);
+      if (a.head_dim == 128) hipLaunchKernelGGL((pf_split_qkv<128>), dim3(a.M, ny), dim3(kPfQkvThreads), 0, stream, a, S);
+      else hipLaunchKernelGGL((pf_split_qkv<64>), dim3(a.M, ny), dim3(kPfQkvThreads), 0, stream, a, S);
+    } else if constexpr (MODE == GM_RESID) {
+      hipLaunchKernelGGL(pf_split_resid, dim3(a.M), dim3(kPfResidThreads), 0, stream, a, S);
+    } else {
+      const int eb = (int)std::min<int64_t>(((int64_t)a.M * a.N + 255) / 256, 4096);
+      hipLaunchKernelGGL(pf_split_swiglu, dim3(eb), dim3(256), 0, stream, a, S);
+    }
   } else {
     hipLaunchKernelGGL((pf_gemm_kernel<Q, MODE, false>), dim3(gx), dim3(kPfThreads), 0, stream, a);
+    if (MODE == GM_RESID && a.norm_w) {
+      CQ_HIP(hipGetLastError());
+      hipLaunchKernelGGL(pf_norm_rows, dim3(a.M), dim3(256), 0, stream, (const _Float16*)a.out, a.norm_w, a.norm_eps,
+                         a.N, a.norm_out, a.norm_inv, Q == CQ_QUANT_INT4);
+    }
   }
   CQ_HIP(hipGetLastError());
   return CQ_OK;
@@ -961,14 +1036,13 @@ int launch_pf_gemm(const PfGemmArgs& a, hipStream_t stream) {
   if (!a.A || !a.W[0] || !a.out) return fail(CQ_EINVAL, "prefill gemm: null operand");
   if (a.quant != CQ_QUANT_FP16 && !a.S[0]) return fail(CQ_EINVAL, "prefill gemm: quantized weights need scales");
   if (a.mode == GM_SWIGLU && (!a.W[1] || !a.inv)) return fail(CQ_EINVAL, "prefill gemm: swiglu needs gate, up and the norm");
+  if (a.mode == GM_RESID && (a.N % 8 || (a.norm_w && (!a.norm_out || !a.norm_inv))))
+    return fail(CQ_EINVAL, "prefill gemm: residual rows must be a multiple of 8 wide; the norm needs its outputs");
   if (a.mode == GM_QKV) {
     if (!a.inv || !a.W[1] || !a.W[2] || !a.inv_freq) return fail(CQ_EINVAL, "prefill gemm: qkv operands");
     if (a.kcache8 ? (!a.vcache8 || !a.kscale || !a.vscale) : (!a.kcache || !a.vcache))
       return fail(CQ_EINVAL, "prefill gemm: qkv cache pointers");
-    const int bn = a.quant == CQ_QUANT_INT4   ? PfShape<CQ_QUANT_INT4, GM_QKV>::BN
-                   : a.quant == CQ_QUANT_INT8 ? PfShape<CQ_QUANT_INT8, GM_QKV>::BN
-                                              : PfShape<CQ_QUANT_FP16, GM_QKV>::BN;
-    if (bn % a.head_dim || a.rows[0] % a.head_dim || a.rows[1] % a.head_dim || a.rows[0] + a.rows[1] + a.rows[2] != a.N)
+    if (PfShape<CQ_QUANT_FP16, GM_QKV>::BN % a.head_dim || a.rows[0] % a.head_dim || a.rows[1] % a.head_dim || a.rows[0] + a.rows[1] + a.rows[2] != a.N)
       return fail(CQ_EINVAL, "prefill gemm: qkv rows must be whole heads");
   }
   switch (a.quant) {
