@@ -431,37 +431,64 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
     return;
   }
 
-  // ---- epilogues: lane holds rows nw0 + rt*16 + 4j + v, token m0 + tt*16 + r
+  // ---- epilogues: lane holds rows nw0 + rt*16 + 4j + v, token m0 + tt*16 + r.
+  // The residual and SwiGLU outputs go through LDS (the activation buffers,
+  // free after the loop's last barrier) so that every token row is read and
+  // written in 16-byte pieces rather than 2 bytes per lane.
   if constexpr (MODE == GM_RESID) {
-    _Float16* y = a.out;
+    // fp32 sums, 64 tokens per pass: x = half(x + y), residual stays fp16 (kernels.cu:621)
+    constexpr int LDF = BN + 4;   // padded fp32 row
+    constexpr int HT = kPfTok / 2;
+    static_assert(HT * LDF * 2 <= 3 * XS, "residual staging fits");
+    float* ft = reinterpret_cast<float*>(smem);
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt)
+    for (int h = 0; h < 2; ++h) {
+      if (h) __syncthreads();
 #pragma unroll
-      for (int tt = 0; tt < TT; ++tt)
+      for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int n = nw0 + rt * 16 + 4 * j + v, m = m0 + tt * 16 + r;
-          if (n < a.N && m < a.M) {
-            _Float16* p = y + (int64_t)m * a.N + n;
-            *p = (_Float16)((float)*p + acc[0][rt][tt][v]);   // residual stays fp16 (kernels.cu:621)
-          }
-        }
+        for (int tt = h * TT / 2; tt < (h + 1) * TT / 2; ++tt)
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            ft[(tt * 16 + r - h * HT) * LDF + wave * WROWS + rt * 16 + 4 * j + v] = acc[0][rt][tt][v];
+      __syncthreads();
+      for (int idx = threadIdx.x; idx < HT * (BN / 4); idx += kPfThreads) {
+        const int ml = idx / (BN / 4), c = idx % (BN / 4);
+        const int m = m0 + h * HT + ml, n = nb0 + 4 * c;
+        if (m >= a.M || n >= a.N) continue;
+        _Float16* p = a.out + (int64_t)m * a.N + n;
+        h4_t x = *reinterpret_cast<const h4_t*>(p);
+        const f4_t y = *reinterpret_cast<const f4_t*>(&ft[ml * LDF + 4 * c]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[e] = (_Float16)((float)x[e] + y[e]);
+        *reinterpret_cast<h4_t*>(p) = x;
+      }
+    }
   } else if constexpr (MODE == GM_SWIGLU) {
+    constexpr int LD = BN + 8;   // padded fp16 row
+    static_assert(kPfTok * LD <= 3 * XS, "swiglu staging fits");
+    _Float16* ot = smem;
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
       for (int tt = 0; tt < TT; ++tt)
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-          const int n = nw0 + rt * 16 + 4 * j + v, m = m0 + tt * 16 + r;
-          if (n < a.N && m < a.M) {
-            const float s = a.inv[m];
-            const float g = acc[0][rt][tt][v] * s, u = acc[1][rt][tt][v] * s;
-            const float sig = 1.f / (1.f + expf(-g));   // kernels.cu:566
-            a.out[(int64_t)m * a.N + pf_pos(n, Q == CQ_QUANT_INT4)] =
-                pf_val((float)(_Float16)((g * sig) * u), n, Q == CQ_QUANT_INT4);
-          }
+          const int nl = wave * WROWS + rt * 16 + 4 * j + v, ml = tt * 16 + r;
+          const int m = min(m0 + ml, a.M - 1);
+          const float s = a.inv[m];
+          const float g = acc[0][rt][tt][v] * s, u = acc[1][rt][tt][v] * s;
+          const float sig = 1.f / (1.f + expf(-g));   // kernels.cu:566
+          // nb0 is a multiple of 8, so the layout's permutation stays inside the tile
+          ot[ml * LD + pf_pos(nl, Q == CQ_QUANT_INT4)] = pf_val((float)(_Float16)((g * sig) * u), nl, Q == CQ_QUANT_INT4);
         }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < kPfTok * (BN / 8); idx += kPfThreads) {
+      const int ml = idx / (BN / 8), c = idx % (BN / 8);
+      const int m = m0 + ml, n = nb0 + 8 * c;
+      if (m < a.M && n < a.N)
+        *reinterpret_cast<u4_t*>(a.out + (int64_t)m * a.N + n) = *reinterpret_cast<const u4_t*>(&ot[ml * LD + 8 * c]);
+    }
   } else {
     // QKV: norm scale, bias, fp16 into LDS (over the activation buffers, all
     // reads of which finished at the loop's last barrier); then pairs
@@ -1035,7 +1062,8 @@ int launch_pf_gemm(const PfGemmArgs& a, hipStream_t stream) {
   if (a.M <= 0 || a.N <= 0 || a.K <= 0 || a.K % kPfK) return fail(CQ_EINVAL, "prefill gemm: K must be a multiple of 128");
   if (!a.A || !a.W[0] || !a.out) return fail(CQ_EINVAL, "prefill gemm: null operand");
   if (a.quant != CQ_QUANT_FP16 && !a.S[0]) return fail(CQ_EINVAL, "prefill gemm: quantized weights need scales");
-  if (a.mode == GM_SWIGLU && (!a.W[1] || !a.inv)) return fail(CQ_EINVAL, "prefill gemm: swiglu needs gate, up and the norm");
+  if (a.mode == GM_SWIGLU && (!a.W[1] || !a.inv || a.N % 8))
+    return fail(CQ_EINVAL, "prefill gemm: swiglu needs gate, up, the norm and rows a multiple of 8");
   if (a.mode == GM_RESID && (a.N % 8 || (a.norm_w && (!a.norm_out || !a.norm_inv))))
     return fail(CQ_EINVAL, "prefill gemm: residual rows must be a multiple of 8 wide; the norm needs its outputs");
   if (a.mode == GM_QKV) {
