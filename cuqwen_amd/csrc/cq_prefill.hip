@@ -34,6 +34,7 @@ constexpr int kPfWaves = 8;
 constexpr int kPfThreads = kPfWaves * 64;
 constexpr int kPfK = 128;         // K per main-loop step (one quantization group)
 constexpr int kPfMaxSplit = 8;
+constexpr int kPfAhead = 2;       // K steps whose loads are in flight ahead of the one computed
 
 // Activation layout of the GEMM inputs, chosen by the weights' format so the
 // A operand needs no shuffle: int4 stores each 8-group in the order
@@ -220,7 +221,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
   constexpr int L = PfW<Q>::LOADS;
   constexpr int XS = kPfTok * kPfK;                         // halves of one activation stage
   constexpr int OT = MODE == GM_QKV ? BN * kPfTok : 0;      // QKV epilogue tile (rows x tokens)
-  __shared__ __align__(16) _Float16 smem[3 * XS > OT ? 3 * XS : OT];
+  constexpr int AH = kPfAhead, NS = AH + 1;                   // steps loaded ahead, LDS stages
+  __shared__ __align__(16) _Float16 smem[NS * XS > OT ? NS * XS : OT];
   _Float16* xs0 = smem;
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
   const int r = lane & 15, j = lane >> 4;
@@ -276,18 +278,19 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
 #pragma unroll
       for (int tt = 0; tt < TT; ++tt) acc[mt][rt][tt] = f4_t{0.f, 0.f, 0.f, 0.f};
 
-  // Two-step-ahead pipeline: at step k (after its barrier) the weights and
-  // activations of step k+2 are requested; the K loop is unrolled by two so
-  // the two weight register sets keep compile-time indices.  Loads of the
-  // vector memory counter, per step and wave: WL weight / scale loads, 8
-  // activation loads.  Before step k's barrier a wave waits until at most
-  // one later step's loads are outstanding (its own step-k activation
-  // writes have landed in LDS); the barrier then makes all waves' visible.
+  // AH-step-ahead pipeline: at step k (after its barrier) the weights and
+  // activations of step k+AH are requested into register set k % AH and LDS
+  // stage k+AH mod AH+1; the K loop is unrolled by AH so the weight register
+  // sets keep compile-time indices.  Loads of the vector memory counter, per
+  // step and wave: WL weight / scale loads, 4 activation loads.  Before step
+  // k's barrier a wave waits until only the later steps' loads (at most
+  // AH - 1 steps) are outstanding (its own step-k activation writes have
+  // landed in LDS); the barrier then makes all waves' visible.
   constexpr int WL = NMAT * RT * (L + (Q != CQ_QUANT_FP16 ? 1 : 0));
-  constexpr int VMC = WL + kPfTok / (4 * kPfWaves);
-  static_assert(VMC < 64, "vmcnt range");
-  u4_t wv[2][NMAT][RT][L];
-  _Float16 sv[2][NMAT][RT];
+  constexpr int VMC = WL + kPfTok / (4 * kPfWaves);          // loads of one step
+  static_assert(VMC * (AH - 1) < 64, "vmcnt range");
+  u4_t wv[AH][NMAT][RT][L];
+  _Float16 sv[AH][NMAT][RT];
   auto load_w_step = [&](int ks, u4_t (&w)[NMAT][RT][L], _Float16 (&s)[NMAT][RT]) {
 #pragma unroll
     for (int mt = 0; mt < NMAT; ++mt)
@@ -297,20 +300,23 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
         if constexpr (Q != CQ_QUANT_FP16) s[mt][rt] = srow[mt][rt][ks];
       }
   };
-  load_w_step(kb, wv[0], sv[0]);
-  x_issue(kb, 0);
-  if (kb + 1 < ke) {
-    load_w_step(kb + 1, wv[1], sv[1]);
-    x_issue(kb + 1, 1);
-  }
+#pragma unroll
+  for (int p = 0; p < AH; ++p)
+    if (kb + p < ke) {
+      load_w_step(kb + p, wv[p], sv[p]);
+      x_issue(kb + p, p);
+    }
 
   const UnpackRegs uk = unpack_regs();
   auto step = [&](auto I, int ks) {
     constexpr int S = decltype(I)::value;   // weight register set of this step
-    const int stg = (ks - kb) % 3;
+    const int stg = (ks - kb) % NS;
     // simm16 of s_waitcnt on gfx9: vmcnt in bits [3:0] and [15:14], expcnt
     // [6:4] and lgkmcnt [11:8] left at their maxima
-    if (ks + 1 < ke) __builtin_amdgcn_s_waitcnt(0x0F70 | (VMC & 15) | ((VMC >> 4) << 14));
+    // loads of the later steps already issued (up to AH - 1) may stay outstanding
+    constexpr int V1 = VMC, V2 = 2 * VMC;
+    if (AH >= 3 && ks + 2 < ke) __builtin_amdgcn_s_waitcnt(0x0F70 | (V2 & 15) | ((V2 >> 4) << 14));
+    else if (ks + 1 < ke) __builtin_amdgcn_s_waitcnt(0x0F70 | (V1 & 15) | ((V1 >> 4) << 14));
     else __builtin_amdgcn_s_waitcnt(0x0F70);
     __builtin_amdgcn_s_barrier();
     const _Float16* xb0 = xs0 + stg * XS;
@@ -324,9 +330,9 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
 #pragma unroll
         for (int i = 0; i < L; ++i) w[mt][rt][i] = wv[S][mt][rt][i];
       }
-    if (ks + 2 < ke) {
-      load_w_step(ks + 2, wv[S], sv[S]);
-      x_issue(ks + 2, (ks + 2 - kb) % 3);
+    if (ks + AH < ke) {
+      load_w_step(ks + AH, wv[S], sv[S]);
+      x_issue(ks + AH, (ks + AH - kb) % NS);
     }
     // B fragments of one sub-step
     auto read_b = [&](int s4, h8_t* xb) {
@@ -404,11 +410,13 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
     }
   };
   int ks = kb;
-  for (; ks + 1 < ke; ks += 2) {
+  for (; ks + AH - 1 < ke; ks += AH) {
     step(std::integral_constant<int, 0>{}, ks);
     step(std::integral_constant<int, 1>{}, ks + 1);
+    if constexpr (AH >= 3) step(std::integral_constant<int, 2 % AH>{}, ks + 2);
   }
   if (ks < ke) step(std::integral_constant<int, 0>{}, ks);
+  if (AH >= 3 && ks + 1 < ke) step(std::integral_constant<int, 1>{}, ks + 1);
   __syncthreads();   // every wave's last LDS reads are done before the QKV epilogue reuses the buffers
 
   if constexpr (SPLIT) {
@@ -439,7 +447,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
     // fp32 sums, 64 tokens per pass: x = half(x + y), residual stays fp16 (kernels.cu:621)
     constexpr int LDF = BN + 4;   // padded fp32 row
     constexpr int HT = kPfTok / 2;
-    static_assert(HT * LDF * 2 <= 3 * XS, "residual staging fits");
+    static_assert(HT * LDF * 2 <= NS * XS, "residual staging fits");
     float* ft = reinterpret_cast<float*>(smem);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -466,7 +474,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
     }
   } else if constexpr (MODE == GM_SWIGLU) {
     constexpr int LD = BN + 8;   // padded fp16 row
-    static_assert(kPfTok * LD <= 3 * XS, "swiglu staging fits");
+    static_assert(kPfTok * LD <= NS * XS, "swiglu staging fits");
     _Float16* ot = smem;
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
