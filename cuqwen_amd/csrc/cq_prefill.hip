@@ -34,7 +34,6 @@ constexpr int kPfWaves = 8;
 constexpr int kPfThreads = kPfWaves * 64;
 constexpr int kPfK = 128;         // K per main-loop step (one quantization group)
 constexpr int kPfMaxSplit = 8;
-constexpr int kPfAhead = 2;       // K steps whose loads are in flight ahead of the one computed
 
 // Activation layout of the GEMM inputs, chosen by the weights' format so the
 // A operand needs no shuffle: int4 stores each 8-group in the order
@@ -221,8 +220,10 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
   constexpr int L = PfW<Q>::LOADS;
   constexpr int XS = kPfTok * kPfK;                         // halves of one activation stage
   constexpr int OT = MODE == GM_QKV ? BN * kPfTok : 0;      // QKV epilogue tile (rows x tokens)
-  constexpr int AH = kPfAhead, NS = AH + 1;                   // steps loaded ahead, LDS stages
-  __shared__ __align__(16) _Float16 smem[NS * XS > OT ? NS * XS : OT];
+  constexpr int NS = 2;                                     // LDS stages
+  // the epilogues reuse the stages: QKV tile, residual fp32 half tile
+  constexpr int SM = std::max({NS * XS, OT, kPfTok / 2 * (BN + 4) * 2});
+  __shared__ __align__(16) _Float16 smem[SM];
   _Float16* xs0 = smem;
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
   const int r = lane & 15, j = lane >> 4;
@@ -252,24 +253,30 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
       srow[mt][rt] = Q == CQ_QUANT_FP16 ? nullptr : sel3(a.S, mat) + (int64_t)local * (K / kGroup);
     }
 
-  // Activation tiles go global -> LDS directly (global_load_lds_dwordx4, no
-  // registers), three stages deep.  A stage holds 128 token rows of 256 bytes;
-  // 16-byte slot s of row t holds K chunk s ^ (t & 15), so the B-operand
-  // reads (16 rows at one chunk) hit 16 different bank groups.  Load q of a
-  // step (q = i * waves + wave) fills rows 4q .. 4q + 3: lane l writes
-  // row 4q + l / 16, slot l % 16.
-  auto x_issue = [&](int ks, int stg) {
+  // Activation tiles: global -> registers one step ahead, then 16-byte LDS
+  // stores into one of two stages at the start of the step that reads them
+  // (measured faster than global_load_lds straight into LDS).  A stage holds
+  // 128 token rows of 256 bytes; 16-byte slot s of row t holds K chunk
+  // s ^ (t & 15), so the B-operand reads (16 rows at one chunk) hit 16
+  // different bank groups.  Piece q of a step (q = i * waves + wave) is rows
+  // 4q .. 4q + 3: lane l holds row 4q + l / 16, slot l % 16.
+  constexpr int XL = kPfTok / (4 * kPfWaves);
+  u4_t xr[XL];
+  auto x_load = [&](int ks) {
 #pragma unroll
-    for (int i = 0; i < kPfTok / (4 * kPfWaves); ++i) {
+    for (int i = 0; i < XL; ++i) {
       const int q = i * kPfWaves + wave, t = 4 * q + (lane >> 4), c = (lane & 15) ^ (t & 15);
       const int m = min(m0 + t, a.M - 1);
-      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(a.A + (int64_t)m * K + ks * kPfK + c * 8),
-                                       (__attribute__((address_space(3))) void*)(
-                                           xs0 + stg * XS + q * 512),
-                                       16, 0, 0);
+      xr[i] = load_u4(a.A + (int64_t)m * K + ks * kPfK + c * 8);
     }
   };
-
+  auto x_store = [&](int stg) {
+#pragma unroll
+    for (int i = 0; i < XL; ++i) {
+      const int q = i * kPfWaves + wave;
+      *reinterpret_cast<u4_t*>(xs0 + stg * XS + q * 512 + lane * 8) = xr[i];
+    }
+  };
   f4_t acc[NMAT][RT][TT];
 #pragma unroll
   for (int mt = 0; mt < NMAT; ++mt)
@@ -278,19 +285,19 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
 #pragma unroll
       for (int tt = 0; tt < TT; ++tt) acc[mt][rt][tt] = f4_t{0.f, 0.f, 0.f, 0.f};
 
-  // AH-step-ahead pipeline: at step k (after its barrier) the weights and
-  // activations of step k+AH are requested into register set k % AH and LDS
-  // stage k+AH mod AH+1; the K loop is unrolled by AH so the weight register
-  // sets keep compile-time indices.  Loads of the vector memory counter, per
-  // step and wave: WL weight / scale loads, 4 activation loads.  Before step
-  // k's barrier a wave waits until only the later steps' loads (at most
-  // AH - 1 steps) are outstanding (its own step-k activation writes have
-  // landed in LDS); the barrier then makes all waves' visible.
+  // Pipeline: at step k (after its barrier) the activations of step k+1
+  // (into registers) and then the weights of step k+2 (into register set
+  // k % 2) are requested; the K loop is unrolled by two so the weight
+  // register sets keep compile-time indices.  At the start of step k a wave
+  // waits until only the WL weight / scale loads of step k+1 are
+  // outstanding, stores its piece of step k's activations into LDS stage
+  // k % 2 (last read in step k-2, which every wave finished before step
+  // k-1's barrier) and waits for the stores; the barrier then makes all
+  // pieces visible.
   constexpr int WL = NMAT * RT * (L + (Q != CQ_QUANT_FP16 ? 1 : 0));
-  constexpr int VMC = WL + kPfTok / (4 * kPfWaves);          // loads of one step
-  static_assert(VMC * (AH - 1) < 64, "vmcnt range");
-  u4_t wv[AH][NMAT][RT][L];
-  _Float16 sv[AH][NMAT][RT];
+  static_assert(WL < 64, "vmcnt range");
+  u4_t wv[2][NMAT][RT][L];
+  _Float16 sv[2][NMAT][RT];
   auto load_w_step = [&](int ks, u4_t (&w)[NMAT][RT][L], _Float16 (&s)[NMAT][RT]) {
 #pragma unroll
     for (int mt = 0; mt < NMAT; ++mt)
@@ -300,24 +307,20 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
         if constexpr (Q != CQ_QUANT_FP16) s[mt][rt] = srow[mt][rt][ks];
       }
   };
-#pragma unroll
-  for (int p = 0; p < AH; ++p)
-    if (kb + p < ke) {
-      load_w_step(kb + p, wv[p], sv[p]);
-      x_issue(kb + p, p);
-    }
+  load_w_step(kb, wv[0], sv[0]);
+  x_load(kb);
+  if (kb + 1 < ke) load_w_step(kb + 1, wv[1], sv[1]);
 
   const UnpackRegs uk = unpack_regs();
   auto step = [&](auto I, int ks) {
     constexpr int S = decltype(I)::value;   // weight register set of this step
-    const int stg = (ks - kb) % NS;
+    const int stg = (ks - kb) & 1;
     // simm16 of s_waitcnt on gfx9: vmcnt in bits [3:0] and [15:14], expcnt
-    // [6:4] and lgkmcnt [11:8] left at their maxima
-    // loads of the later steps already issued (up to AH - 1) may stay outstanding
-    constexpr int V1 = VMC, V2 = 2 * VMC;
-    if (AH >= 3 && ks + 2 < ke) __builtin_amdgcn_s_waitcnt(0x0F70 | (V2 & 15) | ((V2 >> 4) << 14));
-    else if (ks + 1 < ke) __builtin_amdgcn_s_waitcnt(0x0F70 | (V1 & 15) | ((V1 >> 4) << 14));
+    // [6:4], lgkmcnt [11:8]; the fields not waited on are left at their maxima
+    if (ks + 1 < ke) __builtin_amdgcn_s_waitcnt(0x0F70 | (WL & 15) | ((WL >> 4) << 14));
     else __builtin_amdgcn_s_waitcnt(0x0F70);
+    x_store(stg);
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): the LDS stores are done
     __builtin_amdgcn_s_barrier();
     const _Float16* xb0 = xs0 + stg * XS;
     h2_t s2[NMAT][RT];
@@ -330,10 +333,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
 #pragma unroll
         for (int i = 0; i < L; ++i) w[mt][rt][i] = wv[S][mt][rt][i];
       }
-    if (ks + AH < ke) {
-      load_w_step(ks + AH, wv[S], sv[S]);
-      x_issue(ks + AH, (ks + AH - kb) % NS);
-    }
+    if (ks + 1 < ke) x_load(ks + 1);
+    if (ks + 2 < ke) load_w_step(ks + 2, wv[S], sv[S]);
     // B fragments of one sub-step
     auto read_b = [&](int s4, h8_t* xb) {
 #pragma unroll
@@ -410,13 +411,11 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
     }
   };
   int ks = kb;
-  for (; ks + AH - 1 < ke; ks += AH) {
+  for (; ks + 1 < ke; ks += 2) {
     step(std::integral_constant<int, 0>{}, ks);
     step(std::integral_constant<int, 1>{}, ks + 1);
-    if constexpr (AH >= 3) step(std::integral_constant<int, 2 % AH>{}, ks + 2);
   }
   if (ks < ke) step(std::integral_constant<int, 0>{}, ks);
-  if (AH >= 3 && ks + 1 < ke) step(std::integral_constant<int, 1>{}, ks + 1);
   __syncthreads();   // every wave's last LDS reads are done before the QKV epilogue reuses the buffers
 
   if constexpr (SPLIT) {
@@ -447,7 +446,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
     // fp32 sums, 64 tokens per pass: x = half(x + y), residual stays fp16 (kernels.cu:621)
     constexpr int LDF = BN + 4;   // padded fp32 row
     constexpr int HT = kPfTok / 2;
-    static_assert(HT * LDF * 2 <= NS * XS, "residual staging fits");
+    static_assert(HT * LDF * 2 <= SM, "residual staging fits");
     float* ft = reinterpret_cast<float*>(smem);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -474,7 +473,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
     }
   } else if constexpr (MODE == GM_SWIGLU) {
     constexpr int LD = BN + 8;   // padded fp16 row
-    static_assert(kPfTok * LD <= NS * XS, "swiglu staging fits");
+    static_assert(kPfTok * LD <= SM, "swiglu staging fits");
     _Float16* ot = smem;
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
