@@ -848,23 +848,21 @@ __global__ __launch_bounds__(kAttnThreads) void pf_attention_kernel(const PfAttn
 // wave w owns query head kvh * g + (w % 8) and, with its partner w ^ 8, runs
 // the online softmax over every key tile up to the block's last token (even
 // tiles in waves 0-7, odd tiles in waves 8-15); the two halves merge in LDS
-// at the end.  The tiles stream global -> LDS directly
-// (global_load_lds_dwordx4; a tile's K and V are each one contiguous 32-key
-// block of the tiled cache), a pair of tiles per stage, three stages deep,
-// and every head of the group reads them from LDS: the cache is read once
-// per kv head instead of once per query head.
-constexpr int kPfGqaStages = 3;
+// at the end.  The tiles stream global -> registers -> LDS (a tile's K and V
+// are each one contiguous 32-key block of the tiled cache), a pair of tiles
+// per stage, two stages, and every head of the group reads them from LDS:
+// the cache is read once per kv head instead of once per query head.
 constexpr int kPfGqaWaves = 16;
 template <int HD>
 __global__ __launch_bounds__(kPfGqaWaves * kWave) void pf_attention_gqa_kernel(const PfAttnArgs a) {
   constexpr int KK = HD / 32, DT = HD / 16;
   constexpr int TILE = kTileKeys * HD;               // halves of K (or V) per tile
   constexpr int STAGE = 4 * TILE;                    // two tiles, K and V
-  constexpr int CHUNKS = STAGE * 2 / 1024;           // 1 KB LDS-direct loads per stage
+  constexpr int CHUNKS = STAGE * 2 / 1024;           // 1 KB pieces per stage
   constexpr int PER_WAVE = (CHUNKS + kPfGqaWaves - 1) / kPfGqaWaves;
   constexpr int MERGE = 8 * kWave * (2 + 4 * DT);    // floats of one half's softmax state
-  static_assert(MERGE * 4 <= kPfGqaStages * STAGE * 2, "merge area fits in the stage buffers");
-  __shared__ __align__(16) _Float16 st[kPfGqaStages * STAGE];
+  constexpr int SM = 2 * STAGE > 2 * MERGE ? 2 * STAGE : 2 * MERGE;
+  __shared__ __align__(16) _Float16 st[SM];
   const int t0 = blockIdx.x * 16, kvh = blockIdx.y;
   const int g = a.n_heads / a.n_kv;
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
@@ -875,34 +873,36 @@ __global__ __launch_bounds__(kPfGqaWaves * kWave) void pf_attention_gqa_kernel(c
   const int n_steps = (n_tiles + 1) / 2;
   const _Float16* kbase = a.kcache + (int64_t)kvh * a.max_seq * HD;
   const _Float16* vbase = a.vcache + (int64_t)kvh * a.max_seq * HD;
-  // stage layout: [tile 0: K, V][tile 1: K, V]; chunk c of a stage is 1 KB
-  // loads this wave issues for a step (the pair's second tile may be past the end)
-  auto n_loads = [&](int step) {
-    int n = 0;
-#pragma unroll
-    for (int i = 0; i < PER_WAVE; ++i) {
-      const int c = i * kPfGqaWaves + wave;
-      n += (c < CHUNKS && 2 * step + c / (CHUNKS / 2) < n_tiles) ? 1 : 0;
-    }
-    return n;
+  // A step's tile pair goes global -> registers one step ahead, then into
+  // one of two LDS stages at the start of the step that reads it.  Stage
+  // layout: [tile 0: K, V][tile 1: K, V]; piece c of a stage is 1 KB (the
+  // pair's second tile may be past the end).
+  u4_t kv[PER_WAVE];
+  auto piece = [&](int i, int step, int* tt, bool* isv, int* cc) {
+    const int c = i * kPfGqaWaves + wave;
+    *tt = c / (CHUNKS / 2);
+    const int r = c % (CHUNKS / 2);
+    *isv = r >= CHUNKS / 4;
+    *cc = *isv ? r - CHUNKS / 4 : r;
+    return c < CHUNKS && 2 * step + *tt < n_tiles;
   };
-  static_assert(PER_WAVE <= 2, "the waits below cover up to two loads per step");
-  auto issue = [&](int step) {
-    _Float16* dst = st + (step % kPfGqaStages) * STAGE;
+  auto load = [&](int step) {
 #pragma unroll
     for (int i = 0; i < PER_WAVE; ++i) {
-      const int c = i * kPfGqaWaves + wave;
-      const int tt = c / (CHUNKS / 2), r = c % (CHUNKS / 2);   // tile of the pair, chunk within it
-      const int ti = 2 * step + tt;
-      if (c < CHUNKS && ti < n_tiles) {
-        const bool isv = r >= CHUNKS / 4;
-        const int cc = isv ? r - CHUNKS / 4 : r;
-        const _Float16* src = (isv ? vbase : kbase) + (int64_t)ti * TILE + cc * 512 + lane * 8;
-        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src),
-                                         (__attribute__((address_space(3))) void*)(dst + tt * 2 * TILE +
-                                                                                    (isv ? TILE : 0) + cc * 512),
-                                         16, 0, 0);
-      }
+      int tt, cc;
+      bool isv;
+      if (piece(i, step, &tt, &isv, &cc))
+        kv[i] = load_u4((isv ? vbase : kbase) + (int64_t)(2 * step + tt) * TILE + cc * 512 + lane * 8);
+    }
+  };
+  auto store = [&](int step) {
+    _Float16* dst = st + (step & 1) * STAGE;
+#pragma unroll
+    for (int i = 0; i < PER_WAVE; ++i) {
+      int tt, cc;
+      bool isv;
+      if (piece(i, step, &tt, &isv, &cc))
+        *reinterpret_cast<u4_t*>(dst + tt * 2 * TILE + (isv ? TILE : 0) + cc * 512 + lane * 8) = kv[i];
     }
   };
   const bool active = head < g;
@@ -913,26 +913,24 @@ __global__ __launch_bounds__(kPfGqaWaves * kWave) void pf_attention_gqa_kernel(c
   const _Float16* q = a.q + (int64_t)tcol * a.n_heads * HD + hq * HD;
 #pragma unroll
   for (int kk = 0; kk < KK; ++kk) qb[kk] = __builtin_bit_cast(h8_t, load_u4(q + kk * 32 + j * 8));
-  issue(0);
-  if (n_steps > 1) issue(1);
+  load(0);
   const float scale = 1.0f / sqrtf((float)HD);
   float m = -INFINITY, l = 0.f;
   f4_t o[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) o[dt] = f4_t{0.f, 0.f, 0.f, 0.f};
   for (int sp = 0; sp < n_steps; ++sp) {
-    // this step's loads (issued two steps ago) done, then visible to all
-    // waves: at most the next step's loads stay outstanding (the q loads
-    // went out before any of them)
-    const int later = sp + 1 < n_steps ? n_loads(sp + 1) : 0;
-    if (later >= 2) __builtin_amdgcn_s_waitcnt(0x0F70 | 2);
-    else if (later == 1) __builtin_amdgcn_s_waitcnt(0x0F70 | 1);
-    else __builtin_amdgcn_s_waitcnt(0x0F70);
+    // this step's pieces (loaded during the previous step) into LDS stage
+    // sp % 2, last read at step sp - 2, which every wave finished before the
+    // previous barrier; then visible to all waves
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    store(sp);
+    __builtin_amdgcn_s_waitcnt(0xC07F);
     __builtin_amdgcn_s_barrier();
-    if (sp + 2 < n_steps) issue(sp + 2);   // into the stage every wave finished reading at sp - 1
+    if (sp + 1 < n_steps) load(sp + 1);
     const int ti = 2 * sp + half;
     if (active && ti < n_tiles) {
-      const _Float16* kt = st + (sp % kPfGqaStages) * STAGE + half * 2 * TILE;
+      const _Float16* kt = st + (sp & 1) * STAGE + half * 2 * TILE;
       const _Float16* vt = kt + TILE;
       KVTile<HD> A;
 #pragma unroll
@@ -959,21 +957,41 @@ __global__ __launch_bounds__(kPfGqaWaves * kWave) void pf_attention_gqa_kernel(c
       for (int i = 0; i < 4; ++i) mg[(2 + 4 * dt + i) * kWave + lane] = o[dt][i];
   }
   __syncthreads();
-  if (half == 1 || !active || t0 + h >= a.M) return;
-  const float m1 = mg[lane], l1 = mg[kWave + lane];
-  const float M = fmaxf(m, m1);
-  const float f0 = m == -INFINITY ? 0.f : __expf(m - M), f1 = m1 == -INFINITY ? 0.f : __expf(m1 - M);
-  const float inv = 1.0f / (l * f0 + l1 * f1 + 1e-9f);
+  // the merged rows go through LDS (over the merge area, once every wave
+  // has read it) so each token's g heads are written as one contiguous run
+  // of 16-byte pieces
+  const bool writer = half == 0 && active;
+  float ov[DT][4];
+  if (writer) {
+    const float m1 = mg[lane], l1 = mg[kWave + lane];
+    const float M = fmaxf(m, m1);
+    const float f0 = m == -INFINITY ? 0.f : __expf(m - M), f1 = m1 == -INFINITY ? 0.f : __expf(m1 - M);
+    const float inv = 1.0f / (l * f0 + l1 * f1 + 1e-9f);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ov[dt][i] = (o[dt][i] * f0 + mg[(2 + 4 * dt + i) * kWave + lane] * f1) * inv;
+  }
+  __syncthreads();
+  const int GW = g * HD;   // output halves per token of this kv head
+  _Float16* ot = st;       // [16 tokens][GW]
+  if (writer) {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int k = head * HD + dt * 16 + 4 * j + i;   // head * HD is a multiple of 8: the layout stays in the tile
+        ot[h * GW + pf_pos(k, a.int4_layout)] = pf_val((float)(_Float16)ov[dt][i], k, a.int4_layout);
+      }
+  }
+  __syncthreads();
   const int qd = a.n_heads * HD;
-  _Float16* orow = a.out + (int64_t)(t0 + h) * qd;
-#pragma unroll
-  for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int k = hq * HD + dt * 16 + 4 * j + i;
-      const float v = (o[dt][i] * f0 + mg[(2 + 4 * dt + i) * kWave + lane] * f1) * inv;
-      orow[pf_pos(k, a.int4_layout)] = pf_val((float)(_Float16)v, k, a.int4_layout);
-    }
+  for (int idx = threadIdx.x; idx < 16 * (GW / 8); idx += kPfGqaWaves * kWave) {
+    const int c = idx / (GW / 8), p8 = idx % (GW / 8);
+    if (t0 + c < a.M)
+      *reinterpret_cast<u4_t*>(a.out + (int64_t)(t0 + c) * qd + kvh * GW + 8 * p8) =
+          *reinterpret_cast<const u4_t*>(ot + c * GW + 8 * p8);
+  }
 }
 
 // One row of a GEMM input back to natural order (the int4 layout stores each
