@@ -369,14 +369,14 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
           for (int rt = 0; rt < RT; ++rt)
             acc[mt][rt][tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[mt][rt], xb[tt], acc[mt][rt][tt], 0, 0, 0);
     };
-    if constexpr (Q == CQ_QUANT_INT4) {
+    if constexpr (Q != CQ_QUANT_FP16) {
       // Software pipeline over the four sub-steps: the B fragments (LDS) and
       // A fragments (unpack) of sub-step s4 + 1 are produced while the
       // matrix instructions of s4 run; the scheduling groups interleave them
       // (the LDS reads first, then one matrix instruction and two vector
       // instructions at a time) so the unpack co-executes with the matrix
-      // cores instead of alternating with them.  (The int8 / fp16 weight
-      // registers leave no room for the second fragment set.)
+      // cores instead of alternating with them.  (The fp16 weight registers
+      // leave no room for the second fragment set.)
       h8_t xb[2][TT];
       h8_t wa[2][NMAT][RT];
       read_b(0, xb[0]);
