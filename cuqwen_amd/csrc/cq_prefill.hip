@@ -4,19 +4,21 @@
 // prefill is its roadmap item, README.md:145).
 //
 // Per layer and chunk of M tokens:
-//   pf_norm_rows    x -> half(x * w) and rsqrt(mean(x^2) + eps) per token
-//                   (the decode GEMVs' fused RMSNorm, kernels.cu:689-751)
+//   RMSNorm         x -> half(x * w) and rsqrt(mean(x^2) + eps) per token
+//                   (the decode GEMVs' fused RMSNorm, kernels.cu:689-751):
+//                   pf_norm_rows for layer 0, later in the epilogue of the
+//                   residual GEMM that produces x
 //   pf_gemm<QKV>    Q / K / V rows, bias, RoPE at each token's position, K / V
 //                   into the cache (kernels.cu:402-474, :370-398, :326-347)
 //   pf_attention    causal FlashDecoding over the cache (kernels.cu:105-288
 //                   with a per-token key limit)
-//   pf_gemm<RESID>  O-proj + residual (kernels.cu:640-687)
-//   pf_norm_rows, pf_gemm<SWIGLU> (kernels.cu:523-585), pf_gemm<RESID> (down)
+//   pf_gemm<RESID>  O-proj + residual (kernels.cu:640-687), + RMSNorm
+//   pf_gemm<SWIGLU> (kernels.cu:523-585), pf_gemm<RESID> (down), + RMSNorm
 // The GEMMs are M > 1, so they run on the matrix cores: each wave dequantizes
 // its weight rows in registers (int4 / int8 to exact small-integer fp16,
 // times the group's fp16 scale) as the A operand of v_mfma_f32_16x16x32_f16
-// and takes 16-token slices of the activation tile, staged in LDS straight
-// from global memory, as the B operand.
+// and takes 16-token slices of the activation tile, staged in LDS, as the B
+// operand.
 //
 // Activation layout: the inputs of the GEMMs (normed x, attention output,
 // SwiGLU output) are stored in the order in which the weights' unpack yields
