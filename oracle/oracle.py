@@ -264,6 +264,6 @@ class Model:
         return out
 
     def __del__(self):
-        if getattr(self, "h", None):
+        if getattr(self, "h", None) and lib is not None:
             lib.or_model_free(self.h)
             self.h = None
