@@ -8,7 +8,6 @@ exporter's conversion (BF16 bits << 16 -> fp32 -> fp16 round to nearest
 even), projections must equal the oracle's quantizer (pinned against the
 exporter's formulas in test_oracle.py) applied to those fp16 values, and the
 header / lm_head rules must follow export_weights.py:243-322."""
-import json
 import os
 import struct
 
@@ -19,84 +18,7 @@ import cuqwen_amd as cq
 from cuqwen_amd import convert as cv
 from oracle import oracle as orc
 
-CFG = dict(vocab_size=1000, hidden_size=256, intermediate_size=384, num_hidden_layers=2,
-           num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=512)
-
-
-def _bf16_bits(a, rng):
-    # arbitrary bf16 bit patterns around the values (the converter must take any)
-    u = np.asarray(a, dtype=np.float32).view(np.uint32)
-    return ((u >> 16) ^ rng.integers(0, 2, u.shape, dtype=np.uint32)).astype(np.uint16)
-
-
-def _write_safetensors(path, tensors):
-    """tensors: name -> (dtype string, shape, raw bytes)."""
-    header, blobs, off = {}, [], 0
-    for name, (dt, shape, raw) in tensors.items():
-        header[name] = {"dtype": dt, "shape": list(shape), "data_offsets": [off, off + len(raw)]}
-        blobs.append(raw)
-        off += len(raw)
-    header["__metadata__"] = {"format": "pt"}
-    h = json.dumps(header).encode()
-    h += b" " * (-len(h) % 8)
-    with open(path, "wb") as f:
-        f.write(struct.pack("<Q", len(h)))
-        f.write(h)
-        for b in blobs:
-            f.write(b)
-
-
-def _make_checkpoint(d, tied=False, with_lm_head=True, seed=3):
-    rng = np.random.default_rng(seed)
-    cfg = dict(CFG, tie_word_embeddings=tied)
-    V, D, I, L = cfg["vocab_size"], cfg["hidden_size"], cfg["intermediate_size"], cfg["num_hidden_layers"]
-    hd = D // cfg["num_attention_heads"]
-    qd, kvd = cfg["num_attention_heads"] * hd, cfg["num_key_value_heads"] * hd
-    src = {}   # name -> fp16 array the converter must produce from it
-
-    def add(name, shape, dtype, scale=0.05):
-        v = (rng.standard_normal(shape) * scale).astype(np.float32)
-        if dtype == "BF16":
-            bits = _bf16_bits(v, rng)
-            raw = bits.tobytes()
-            f16 = (bits.astype(np.uint32) << 16).view(np.float32).astype(np.float16)
-        elif dtype == "F16":
-            f16 = v.astype(np.float16)
-            raw = f16.tobytes()
-        else:
-            raw = v.tobytes()
-            f16 = v.astype(np.float16)
-        src[name] = f16.reshape(shape)
-        return name, (dtype, shape, raw)
-
-    shard1, shard2 = {}, {}
-    shard1.update([add("model.embed_tokens.weight", (V, D), "BF16")])
-    for l in range(L):
-        p = f"model.layers.{l}"
-        tgt = shard1 if l == 0 else shard2
-        tgt.update([
-            add(f"{p}.input_layernorm.weight", (D,), "F32", 1.0),
-            add(f"{p}.self_attn.q_proj.weight", (qd, D), "BF16"),
-            add(f"{p}.self_attn.q_proj.bias", (qd,), "F16"),
-            add(f"{p}.self_attn.k_proj.weight", (kvd, D), "BF16"),
-            add(f"{p}.self_attn.k_proj.bias", (kvd,), "BF16"),
-            add(f"{p}.self_attn.v_proj.weight", (kvd, D), "F32"),
-            add(f"{p}.self_attn.v_proj.bias", (kvd,), "BF16"),
-            add(f"{p}.self_attn.o_proj.weight", (D, qd), "BF16"),
-            add(f"{p}.post_attention_layernorm.weight", (D,), "BF16", 1.0),
-            add(f"{p}.mlp.gate_proj.weight", (I, D), "BF16"),
-            add(f"{p}.mlp.up_proj.weight", (I, D), "F16"),
-            add(f"{p}.mlp.down_proj.weight", (D, I), "BF16"),
-        ])
-    shard2.update([add("model.norm.weight", (D,), "BF16", 1.0)])
-    if with_lm_head:
-        shard2.update([add("lm_head.weight", (V, D), "BF16")])
-    os.makedirs(d, exist_ok=True)
-    with open(os.path.join(d, "config.json"), "w") as f:
-        json.dump(cfg, f)
-    _write_safetensors(os.path.join(d, "model-00001-of-00002.safetensors"), shard1)
-    _write_safetensors(os.path.join(d, "model-00002-of-00002.safetensors"), shard2)
-    return cfg, src
+from tests.hfckpt import CFG, make_checkpoint as _make_checkpoint, write_safetensors as _write_safetensors
 
 
 def _expected_file(cfg, src, quant, lm):
@@ -209,3 +131,61 @@ def test_convert_cli(tmp_path):
     out = str(tmp_path / "cli.bin")
     assert cv.main([d, "--quant", "int4", "--out", out]) == 0
     assert cq.read_header(out).quant_type == 2
+
+
+# ------------------------------------------- the reference exporter's bytes
+# tests/golden/export_golden.json holds what export_weights.py:208-365 itself
+# wrote (run by tests/golden/make_export_golden.py in the build container) for
+# the same seeded checkpoints: SHA-256 and size of each weight file, and the
+# tokenizer ranks file in full.
+import hashlib  # noqa: E402
+import json  # noqa: E402
+
+from tests import hfckpt  # noqa: E402
+
+_GOLD = json.load(open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "export_golden.json"),
+                       encoding="utf-8"))
+
+
+def _sha(path):
+    return hashlib.sha256(open(path, "rb").read()).hexdigest()
+
+
+@pytest.mark.parametrize("name,quant,tied,with_lm", hfckpt.GOLDEN_CASES)
+def test_convert_equals_reference_exporter_bytes(tmp_path, name, quant, tied, with_lm):
+    g = _GOLD["cases"][name]
+    d = str(tmp_path / "hf")
+    hfckpt.make_checkpoint(d, tied=tied, with_lm_head=with_lm, base=hfckpt.GOLDEN_CFG)
+    for shard, h in g["shards"].items():   # the checkpoint generator is unchanged
+        assert _sha(os.path.join(d, shard)) == h, shard
+    out = str(tmp_path / "model.bin")
+    cv.convert(d, out, quant)
+    assert os.path.getsize(out) == g["size"]
+    assert _sha(out) == g["sha256"]
+
+
+@pytest.mark.parametrize("name", [n for n in _GOLD["cases"] if n.startswith("synth_")])
+def test_synthetic_file_equals_reference_export_of_generator_tensors(tmp_path, name):
+    """cq_write_synthetic_file (host) writes exactly what the exporter writes
+    for a checkpoint holding the generator's fp16 tensors."""
+    g = _GOLD["cases"][name]
+    c = _GOLD["config"]
+    qt = {"fp16": 0, "int8": 1, "int4": 2}[g["quant"]]
+    cfg = cq.Config(vocab_size=c["vocab_size"], dim=c["hidden_size"], intermediate_size=c["intermediate_size"],
+                    n_layers=c["num_hidden_layers"], n_heads=c["num_attention_heads"],
+                    n_kv_heads=c["num_key_value_heads"], head_dim=c["hidden_size"] // c["num_attention_heads"],
+                    max_seq_len=c["max_position_embeddings"], quant_type=qt,
+                    lm_head_fmt=1 if (qt and not g["tied"]) else 0, tied=int(g["tied"]),
+                    norm_eps=1e-6, rope_theta=1e6, repetition_penalty=1.1)
+    out = str(tmp_path / "synth.bin")
+    cq.write_synthetic_file(out, cfg, g["synthetic_seed"])
+    assert os.path.getsize(out) == g["size"]
+    assert _sha(out) == g["sha256"]
+
+
+def test_tokenizer_export_equals_reference_exporter(tmp_path):
+    d = str(tmp_path / "tok")
+    hfckpt.make_tokenizer_files(d)
+    out = str(tmp_path / "ranks.json")
+    cv.export_tokenizer(d, out)
+    assert open(out, encoding="utf-8").read() == _GOLD["tokenizer_ranks_file"]
