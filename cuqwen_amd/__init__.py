@@ -90,6 +90,7 @@ def _load():
         "cq_state_create_kv": (I32, [CP, P, I32, ctypes.POINTER(P)]),
         "cq_state_destroy": (I32, [P]),
         "cq_forward": (I32, [P, I32, I32, IP, I32, IP]),
+        "cq_forward_ex": (I32, [P, P, I32, I32, IP, I32, P, IP]),
         "cq_decode": (I32, [P, I32, I32, I32, IP, I32, IP]),
         "cq_state_logits": (I32, [P, P]),
         "cq_state_fill_kv": (I32, [P, I32, U64]),
@@ -129,6 +130,8 @@ def _load():
         "cq_rope": (I32, [P, P, I32, I32, I32, P, ctypes.c_float, P]),
         "cq_gqa_attention_decode": (I32, [P, P, P, P, P, I32, I32, I32, I32, P, P]),
         "cq_attention_workspace_bytes": (SZ, [I32, I32, I32]),
+        "cq_kv_cache_store_hm": (I32, [P, P, P, P, P, I32, I32, I32, P]),
+        "cq_gqa_attention_decode_hm": (I32, [P, P, P, P, P, I32, I32, I32, I32, P, P, P, P]),
         "cq_gqa_attention_decode_kv8": (I32, [P, P, P, P, P, P, P, P, P, I32, I32, I32, I32, P, P]),
         "cq_gqa_attention_decode_fp8": (I32, [P, P, P, P, P, P, P, P, P, I32, I32, I32, I32, P, P]),
         "cq_dequantize": (I32, [I32, I32, P, P, P, I32, I32, P]),
@@ -156,7 +159,7 @@ lib = _load()
 EXPORTED = [
     "cq_last_error", "cq_config_preset", "cq_read_header", "cq_write_synthetic_file", "cq_load_weights",
     "cq_synth_weights", "cq_free_weights", "cq_weights_tensor", "cq_state_create", "cq_state_destroy",
-    "cq_forward", "cq_decode", "cq_state_logits", "cq_state_fill_kv", "cq_state_kv_read", "cq_state_kv_write",
+    "cq_forward", "cq_forward_ex", "cq_decode", "cq_state_logits", "cq_state_fill_kv", "cq_state_kv_read", "cq_state_kv_write",
     "cq_prefill", "cq_state_last_prefill_us", "cq_state_create_kv", "cq_gqa_attention_decode_kv8",
     "cq_gqa_attention_decode_fp8",
     "cq_state_last_decode_us", "cq_synth_normal", "cq_synth_uniform", "cq_tensor_stream_id", "cq_kv_stream_id",
@@ -165,6 +168,7 @@ EXPORTED = [
     "cq_fused_mlp_stage1", "cq_fused_mlp_stage2", "cq_compute_logits", "cq_apply_repetition_penalty",
     "cq_penalty_workspace_bytes", "cq_argmax", "cq_argmax_workspace_bytes", "cq_kv_k_offset", "cq_kv_v_offset",
     "cq_kv_cache_store", "cq_rope", "cq_gqa_attention_decode", "cq_attention_workspace_bytes", "cq_dequantize",
+    "cq_kv_cache_store_hm", "cq_gqa_attention_decode_hm",
     "cq_time_gemv", "cq_state_profile", "cq_tokenizer_load", "cq_tokenizer_free", "cq_tokenizer_encode",
     "cq_tokenizer_decode", "cq_tokenizer_token_id", "cq_tokenizer_vocab_size", "cq_chat_template",
 ]
@@ -321,20 +325,27 @@ def free_weights(weights, cfg=None):
 class State:
     """Decode state (QwenState, include/model.cuh:9-46)."""
 
-    def __init__(self, cfg, weights, kv_dtype=0):
-        """kv_dtype: KV_FP16 (the reference's cache), KV_INT8 or KV_FP8 (E4M3)."""
+    def __init__(self, cfg, weights=None, kv_dtype=0):
+        """kv_dtype: KV_FP16 (the reference's cache), KV_INT8 or KV_FP8 (E4M3).
+        weights may be None (the reference's two-argument malloc_qwen_state):
+        the first forward() that passes weights binds them."""
         self.cfg = cfg
         self.weights = weights
         self.kv_dtype = kv_dtype
         self.handle = ctypes.c_void_p()
-        check(lib.cq_state_create_kv(ctypes.byref(cfg), weights.handle, int(kv_dtype), ctypes.byref(self.handle)))
+        check(lib.cq_state_create_kv(ctypes.byref(cfg), weights.handle if weights is not None else None,
+                                     int(kv_dtype), ctypes.byref(self.handle)))
 
-    def forward(self, token, pos, history=None):
+    def forward(self, token, pos, history=None, weights=None, stream=None):
+        """One synchronous step; `weights` binds (or switches) the weight set,
+        `stream` (a hipStream_t as int / c_void_p) runs the step there."""
         hist = np.ascontiguousarray(history if history is not None else [], dtype=np.int32)
         out = ctypes.c_int32(-1)
-        check(lib.cq_forward(self.handle, int(token), int(pos),
-                             hist.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)) if hist.size else None,
-                             int(hist.size), ctypes.byref(out)))
+        check(lib.cq_forward_ex(self.handle, weights.handle if weights is not None else None, int(token), int(pos),
+                                hist.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)) if hist.size else None,
+                                int(hist.size), stream, ctypes.byref(out)))
+        if weights is not None:
+            self.weights = weights
         return out.value
 
     def decode(self, token, pos0, n_steps, history=None):
@@ -399,7 +410,9 @@ class State:
             self.handle = None
 
 
-def malloc_qwen_state(cfg, weights):
+def malloc_qwen_state(cfg, weights=None):
+    """malloc_qwen_state(config, state) (include/model.cuh:48): weights are
+    optional here and bound by the first qwen_forward."""
     return State(cfg, weights)
 
 
@@ -407,9 +420,9 @@ def free_qwen_state(state):
     state.free()
 
 
-def qwen_forward(token, pos, cfg, state, weights, history=None):
+def qwen_forward(token, pos, cfg, state, weights, history=None, stream=None):
     """qwen_forward() (src/model.cu:183-223): one synchronous decode step -> sampled id."""
-    return state.forward(token, pos, history)
+    return state.forward(token, pos, history, weights=weights, stream=stream)
 
 
 # ------------------------------------------------------------- tokenizer

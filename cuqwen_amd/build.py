@@ -13,7 +13,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libcuqwen.so")
-SOURCES = ["cq_format.cpp", "cq_tokenizer.cpp", "cq_gemv.hip", "cq_attention.hip", "cq_prefill.hip", "cq_ops.hip", "cq_engine.hip", "cq_capi.hip"]
+SOURCES = ["cq_format.cpp", "cq_tokenizer.cpp", "cq_gemv.hip", "cq_attention.hip", "cq_attention_hm.hip", "cq_prefill.hip", "cq_ops.hip", "cq_engine.hip", "cq_capi.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = os.environ.get("CQ_OFFLOAD_ARCH", "gfx950")
@@ -43,9 +43,28 @@ def build(verbose=False):
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
     os.replace(LIB + ".tmp", LIB)
+    build_compat_caller()
     if verbose:
         print("built", LIB)
     return LIB
+
+
+ROOT = os.path.dirname(HERE)
+COMPAT_SRC = os.path.join(ROOT, "tests", "compat", "compat_caller.cpp")
+COMPAT_BIN = os.path.join(ROOT, "tests", "compat", "compat_caller")
+
+
+def build_compat_caller():
+    """The C++ caller that uses include/cuqwen_compat.hpp the way the
+    reference's benchmark and chat loop use its API (a 0.5B INT8 build, as
+    with -Dmodel=0.5b -Dquant=int8); linked against the library with an
+    rpath relative to itself."""
+    cmd = [HIPCC, "-O2", "-std=c++17", "-DQWEN_MODEL_0_5B", "-DQUANT_INT8", "-I", os.path.join(ROOT, "include"),
+           COMPAT_SRC, "-L", HERE, "-lcuqwen", "-Wl,-rpath,$ORIGIN/../../cuqwen_amd", "-o", COMPAT_BIN + ".tmp"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"compat caller build failed:\n{r.stdout}\n{r.stderr}")
+    os.replace(COMPAT_BIN + ".tmp", COMPAT_BIN)
 
 
 if __name__ == "__main__":

@@ -168,6 +168,21 @@ extern "C" int cq_gqa_attention_decode(const void* q, const void* kc, const void
   return launch_attention(a, as_stream(stream));
 }
 
+extern "C" int cq_kv_cache_store_hm(const void* k, const void* v, void* kc, void* vc, const int32_t* d_pos,
+                                    int32_t n_kv_heads, int32_t max_seq_len, int32_t head_dim, void* stream) {
+  return launch_kv_store_hm((const __half*)k, (const __half*)v, (__half*)kc, (__half*)vc, d_pos, n_kv_heads,
+                            max_seq_len, head_dim, as_stream(stream));
+}
+
+extern "C" int cq_gqa_attention_decode_hm(const void* q, const void* kc, const void* vc, void* out,
+                                          const int32_t* d_pos, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
+                                          int32_t max_seq_len, float* partial_out, float* partial_max,
+                                          float* partial_sum, void* stream) {
+  return launch_attention_hm((const __half*)q, (const __half*)kc, (const __half*)vc, (__half*)out, d_pos, n_heads,
+                             n_kv_heads, head_dim, max_seq_len, partial_out, partial_max, partial_sum,
+                             as_stream(stream));
+}
+
 static int attention_decode_q(int fmt, const void* q, const void* k_new, const void* v_new, void* k_cache8,
                               void* v_cache8, float* k_scale, float* v_scale, void* out, const int32_t* d_pos,
                               int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, int32_t max_seq_len,

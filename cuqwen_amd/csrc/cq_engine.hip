@@ -289,6 +289,7 @@ int step_body(cq_state* s) {
 
 int ensure_graph(cq_state* s) {
   if (s->exec) return CQ_OK;
+  if (!s->w) return fail(CQ_EINVAL, "no weights bound to the state (pass them to cq_forward_ex)");
   CQ_HIP(hipStreamBeginCapture(s->stream, hipStreamCaptureModeThreadLocal));
   const int rc = step_body(s);
   hipGraph_t g = nullptr;
@@ -304,13 +305,36 @@ int ensure_graph(cq_state* s) {
 }
 
 // Writes the host-owned control words (token, pos, history_len, chain, step).
-int set_ctl(cq_state* s, int token, int pos, const int32_t* history, int history_len, int chain) {
+int set_ctl(cq_state* s, int token, int pos, const int32_t* history, int history_len, int chain,
+            hipStream_t st = nullptr) {
+  if (!st) st = s->stream;
   int* h = s->host_pinned;
   h[0] = token; h[1] = pos; h[2] = history_len; h[3] = chain; h[4] = 0;
-  CQ_HIP(hipMemcpyAsync(s->ctl, h, 5 * sizeof(int), hipMemcpyHostToDevice, s->stream));
+  CQ_HIP(hipMemcpyAsync(s->ctl, h, 5 * sizeof(int), hipMemcpyHostToDevice, st));
   if (history_len > 0) {
-    CQ_HIP(hipMemcpyAsync(s->history, history, (size_t)history_len * sizeof(int), hipMemcpyHostToDevice, s->stream));
+    CQ_HIP(hipMemcpyAsync(s->history, history, (size_t)history_len * sizeof(int), hipMemcpyHostToDevice, st));
   }
+  return CQ_OK;
+}
+
+// Binds `w` to the state (deferred binding of a state made without weights,
+// or a switch to another weight set of the same shape).  The recorded step
+// graph holds the old weight pointers, so it is dropped and recorded again
+// on the next step.
+int bind_weights(cq_state* s, const cq_weights* w) {
+  if (!w || w == s->w) return CQ_OK;
+  if (std::memcmp(&s->cfg, &w->cfg, offsetof(cq_config, norm_eps)) != 0)
+    return fail(CQ_EINVAL, "forward: the weights do not match the state's config");
+  if (s->exec) {
+    CQ_HIP(hipStreamSynchronize(s->stream));
+    hipGraphExecDestroy(s->exec);
+    s->exec = nullptr;
+  }
+  if (s->graph) {
+    hipGraphDestroy(s->graph);
+    s->graph = nullptr;
+  }
+  s->w = w;
   return CQ_OK;
 }
 
@@ -504,11 +528,11 @@ extern "C" int cq_state_create(const cq_config* cfg, const cq_weights* w, cq_sta
 }
 
 extern "C" int cq_state_create_kv(const cq_config* cfg, const cq_weights* w, int32_t kv_dtype, cq_state** out) {
-  if (!cfg || !w || !out) return fail(CQ_EINVAL, "state_create: null argument");
+  if (!cfg || !out) return fail(CQ_EINVAL, "state_create: null argument");
   if (kv_dtype != CQ_KV_FP16 && kv_dtype != CQ_KV_INT8 && kv_dtype != CQ_KV_FP8)
     return fail(CQ_EINVAL, "state_create: unknown KV cache type");
   CQ_TRY(validate_config(*cfg));
-  if (std::memcmp(cfg, &w->cfg, offsetof(cq_config, norm_eps)) != 0)
+  if (w && std::memcmp(cfg, &w->cfg, offsetof(cq_config, norm_eps)) != 0)
     return fail(CQ_EINVAL, "state_create: config does not match the weights");
   std::unique_ptr<cq_state> s(new cq_state);
   s->cfg = *cfg;
@@ -590,13 +614,24 @@ extern "C" int cq_state_destroy(cq_state* s) {
 
 extern "C" int cq_forward(cq_state* s, int32_t token, int32_t pos, const int32_t* history, int32_t history_len,
                           int32_t* token_out) {
+  return cq_forward_ex(s, nullptr, token, pos, history, history_len, nullptr, token_out);
+}
+
+// qwen_forward (src/model.cu:183-223): the step runs on `stream` when it is
+// non-NULL, else on the state's own stream (model.cu:193); weights passed
+// here are bound on first use, where the reference records its graph
+// (model.cu:203-213).
+extern "C" int cq_forward_ex(cq_state* s, const cq_weights* w, int32_t token, int32_t pos, const int32_t* history,
+                             int32_t history_len, void* stream, int32_t* token_out) {
   if (!s) return fail(CQ_EINVAL, "forward: null state");
   CQ_TRY(check_step_args(s, token, pos, history, history_len));
+  CQ_TRY(bind_weights(s, w));
   CQ_TRY(ensure_graph(s));
-  CQ_TRY(set_ctl(s, token, pos, history, history_len, 0));
-  CQ_HIP(hipGraphLaunch(s->exec, s->stream));
-  CQ_HIP(hipMemcpyAsync(s->host_pinned + 8, &s->ctl->sampled, sizeof(int), hipMemcpyDeviceToHost, s->stream));
-  CQ_HIP(hipStreamSynchronize(s->stream));
+  hipStream_t st = stream ? static_cast<hipStream_t>(stream) : s->stream;
+  CQ_TRY(set_ctl(s, token, pos, history, history_len, 0, st));
+  CQ_HIP(hipGraphLaunch(s->exec, st));
+  CQ_HIP(hipMemcpyAsync(s->host_pinned + 8, &s->ctl->sampled, sizeof(int), hipMemcpyDeviceToHost, st));
+  CQ_HIP(hipStreamSynchronize(st));
   if (token_out) *token_out = s->host_pinned[8];
   return CQ_OK;
 }
@@ -747,15 +782,28 @@ int prefill_workspace(cq_state* s) {
   auto take = [&](size_t bytes) { size_t o = off; off = align_up(off + bytes); return o; };
   const size_t o_x = take(C * d * 2), o_a = take(C * d * 2), o_q = take(C * qd * 2), o_ao = take(C * qd * 2),
                o_i = take(C * I * 2), o_inv = take(C * 4), o_t = take(C * 4), o_p = take(kPrefillPartBytes);
-  if (hipMalloc(&s->pf_arena, off) != hipSuccess) return fail(CQ_ENOMEM, "prefill: workspace allocation failed");
-  char* a = s->pf_arena;
+  // the three parts are committed to the state together, or not at all
+  char* a = nullptr;
+  int* staging = nullptr;
+  hipEvent_t copied = nullptr;
+  if (hipMalloc(&a, off) != hipSuccess) return fail(CQ_ENOMEM, "prefill: workspace allocation failed");
+  if (hipHostMalloc((void**)&staging, C * 4, hipHostMallocDefault) != hipSuccess) {
+    hipFree(a);
+    return fail(CQ_ENOMEM, "prefill: pinned staging allocation failed");
+  }
+  const hipError_t e = hipEventCreateWithFlags(&copied, hipEventDisableTiming);
+  if (e != hipSuccess) {
+    hipHostFree(staging);
+    hipFree(a);
+    return fail(CQ_EHIP, std::string("prefill: hipEventCreate: ") + hipGetErrorString(e));
+  }
+  s->pf_arena = a;
+  s->pf_tokens_host = staging;
+  s->pf_copied = copied;
   s->pf_x = (__half*)(a + o_x); s->pf_a = (__half*)(a + o_a); s->pf_q = (__half*)(a + o_q);
   s->pf_ao = (__half*)(a + o_ao); s->pf_inter = (__half*)(a + o_i); s->pf_inv = (float*)(a + o_inv);
   s->pf_tokens = (int*)(a + o_t);
   s->pf_part = (float*)(a + o_p);
-  if (hipHostMalloc((void**)&s->pf_tokens_host, C * 4, hipHostMallocDefault) != hipSuccess)
-    return fail(CQ_ENOMEM, "prefill: pinned staging allocation failed");
-  CQ_HIP(hipEventCreateWithFlags(&s->pf_copied, hipEventDisableTiming));
   return CQ_OK;
 }
 
@@ -864,6 +912,7 @@ int prefill_batched(cq_state* s, const int32_t* tokens, int n, int pos0) {
 extern "C" int cq_prefill(cq_state* s, const int32_t* tokens, int32_t n_tokens, int32_t pos0, int32_t* token_out) {
   if (!s || !tokens) return fail(CQ_EINVAL, "prefill: null argument");
   if (n_tokens <= 0) return fail(CQ_EINVAL, "prefill: no tokens");
+  if (!s->w) return fail(CQ_EINVAL, "prefill: no weights bound to the state");
   if (pos0 < 0 || (int64_t)pos0 + n_tokens > s->cfg.max_seq_len) return fail(CQ_ERANGE, "prefill: positions exceed max_seq_len");
   for (int i = 0; i < n_tokens; ++i)
     if (tokens[i] < 0 || tokens[i] >= s->cfg.vocab_size) return fail(CQ_ERANGE, "prefill: token outside the vocabulary");
@@ -898,6 +947,7 @@ extern "C" int cq_state_last_prefill_us(cq_state* s, double* us) {
 // ------------------------------------------------------------ profiling
 extern "C" int cq_state_profile(cq_state* s, int32_t pos, int32_t iters, int32_t max_kernels, char* names,
                                 double* us_per_launch, double* bytes_per_launch, int32_t* n_kernels) {
+  if (s && !s->w) return fail(CQ_EINVAL, "profile: no weights bound to the state");
   if (!s || !names || !us_per_launch || !bytes_per_launch || !n_kernels || iters <= 0)
     return fail(CQ_EINVAL, "profile: bad arguments");
   if (pos < 0 || pos >= s->cfg.max_seq_len) return fail(CQ_ERANGE, "profile: pos outside [0, max_seq_len)");

@@ -75,6 +75,13 @@ struct AttnArgs {
 size_t attention_workspace_bytes(int n_heads, int n_kv, int head_dim);
 int launch_attention(const AttnArgs& a, hipStream_t stream);
 int attention_max_parts(int n_kv);
+// Head-major cache path (cq_attention_hm.hip): the reference's layout and
+// partial buffers (partial index (kv_head * 16 + head) * 64 + partition).
+int launch_attention_hm(const __half* q, const __half* kc, const __half* vc, __half* out, const int* d_pos,
+                        int n_heads, int n_kv, int head_dim, int max_seq, float* part_out, float* part_max,
+                        float* part_sum, hipStream_t stream);
+int launch_kv_store_hm(const __half* k, const __half* v, __half* kc, __half* vc, const int* d_pos, int n_kv,
+                       int max_seq, int hd, hipStream_t stream);
 
 // ---------------------------------------------------------------- prefill
 // M-token GEMM on the matrix cores (cq_prefill.hip).  A: [M][K] activations

@@ -105,7 +105,13 @@ int cq_weights_tensor(const cq_weights* w, const char* name, int32_t layer, void
 typedef struct cq_state cq_state;       /* opaque: QwenState (include/model.cuh:9-46) */
 
 /* malloc_qwen_state() (include/model.cuh:48, src/model.cu:5-44).  The KV
- * cache is zeroed.  The state keeps a pointer to `w`, which must outlive it. */
+ * cache is zeroed.  The state keeps a pointer to `w`, which must outlive it.
+ * `w` may be NULL, as in the reference's two-argument
+ * malloc_qwen_state(config, state): the weights are then bound by the first
+ * cq_forward_ex that passes them (the reference's qwen_forward takes the
+ * weights on every call and records its graph on the first,
+ * src/model.cu:203-213); until then every step entry point returns
+ * CQ_EINVAL. */
 int cq_state_create(const cq_config* cfg, const cq_weights* w, cq_state** out);
 /* free_qwen_state() (include/model.cuh:49). */
 int cq_state_destroy(cq_state* s);
@@ -140,6 +146,15 @@ int cq_state_create_kv(const cq_config* cfg, const cq_weights* w, int32_t kv_dty
  * token outside the vocabulary. */
 int cq_forward(cq_state* s, int32_t token, int32_t pos, const int32_t* history,
                int32_t history_len, int32_t* token_out);
+
+/* qwen_forward() with all of its arguments (include/model.cuh:51-60,
+ * src/model.cu:183-223): `w` (may be NULL once weights are bound) is bound
+ * to the state if it differs from the bound set -- same config required;
+ * the step graph is then recorded again -- and the step runs on `stream`
+ * (a hipStream_t) when it is non-NULL, else on the state's own stream, as
+ * the reference's exec_stream (model.cu:193).  Synchronous on that stream. */
+int cq_forward_ex(cq_state* s, const cq_weights* w, int32_t token, int32_t pos, const int32_t* history,
+                  int32_t history_len, void* stream, int32_t* token_out);
 
 /* Greedy decode of n_steps tokens with the step chained on the device: the
  * sampled id of step i is the input of step i+1 and is appended to the
@@ -298,20 +313,45 @@ int64_t cq_kv_v_offset(int32_t kv_head, int32_t t, int32_t d, int32_t max_seq_le
 int cq_rope(void* q, void* k, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, const int32_t* d_pos,
             float rope_theta, void* stream);
 
-/* launch_kv_cache_store (include/kernels.cuh:37, src/kernels.cu:326-367). */
+/* The engine's KV store into its MFMA-tiled cache layout (element
+ * positions: cq_kv_k_offset / cq_kv_v_offset).  The reference's
+ * launch_kv_cache_store over its head-major layout is
+ * cq_kv_cache_store_hm below. */
 int cq_kv_cache_store(const void* k, const void* v, void* layer_k_cache, void* layer_v_cache,
                       const int32_t* d_pos, int32_t n_kv_heads, int32_t max_seq_len, int32_t head_dim,
                       void* stream);
 
-/* launch_gqa_attention_decode (include/kernels.cuh:21-35, src/kernels.cu:105-324):
+/* The engine's decode attention over its MFMA-tiled cache (the layout
+ * cq_kv_cache_store and the decode step write; not the reference's):
  * attn_out[h] = softmax(q_h . K^T / sqrt(hd)) V over keys [0, *d_pos] of kv
- * head h / (n_heads/n_kv_heads).  Split-K over the sequence with an
- * in-kernel log-sum-exp merge; `workspace` replaces the reference's
- * partial_out/max/sum buffers and must hold cq_attention_workspace_bytes(). */
+ * head h / (n_heads/n_kv_heads).  Split-K over the sequence sized for 256
+ * CUs; `workspace` must hold cq_attention_workspace_bytes().  The
+ * reference's launch_gqa_attention_decode over its head-major cache is
+ * cq_gqa_attention_decode_hm below. */
 int cq_gqa_attention_decode(const void* q, const void* layer_k_cache, const void* layer_v_cache, void* attn_out,
                             const int32_t* d_pos, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
                             int32_t max_seq_len, void* workspace, void* stream);
 size_t cq_attention_workspace_bytes(int32_t n_heads, int32_t n_kv_heads, int32_t head_dim);
+
+/* launch_kv_cache_store (include/kernels.cuh:37-47, src/kernels.cu:326-367):
+ * k / v ([n_kv_heads * head_dim] fp16) into row *d_pos of the head-major
+ * layer caches [n_kv_heads][max_seq_len][head_dim] (src/model.cu:112-114). */
+int cq_kv_cache_store_hm(const void* k, const void* v, void* layer_k_cache, void* layer_v_cache,
+                         const int32_t* d_pos, int32_t n_kv_heads, int32_t max_seq_len, int32_t head_dim,
+                         void* stream);
+
+/* launch_gqa_attention_decode (include/kernels.cuh:21-35, src/kernels.cu:105-324)
+ * with the reference's arguments: head-major layer caches
+ * [n_kv_heads][max_seq_len][head_dim], keys [0, *d_pos], 64 partitions of
+ * ceil(T/64) keys, partial buffers as the reference sizes them
+ * (src/model.cu:40-43): partial_out n_kv_heads*16*64*head_dim floats,
+ * partial_max / partial_sum n_kv_heads*16*64 floats, entry
+ * (kv_head*16 + local head)*64 + partition.  head_dim 64 or 128, up to 16
+ * query heads per kv head. */
+int cq_gqa_attention_decode_hm(const void* q, const void* layer_k_cache, const void* layer_v_cache, void* attn_out,
+                               const int32_t* d_pos, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
+                               int32_t max_seq_len, float* partial_out, float* partial_max, float* partial_sum,
+                               void* stream);
 
 /* The same decode attention over an int8 layer cache (see CQ_KV_INT8; no
  * counterpart in the reference): k_new / v_new ([n_kv_heads * head_dim]
