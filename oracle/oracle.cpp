@@ -28,7 +28,7 @@
 namespace {
 
 // ------------------------------------------------------------------ fp16
-float h2f(uint16_t h) {
+float h2f_bits(uint16_t h) {
   const uint32_t sign = (uint32_t)(h & 0x8000) << 16;
   const uint32_t exp = (h >> 10) & 0x1F, man = h & 0x3FF;
   uint32_t bits;
@@ -49,6 +49,16 @@ float h2f(uint16_t h) {
   std::memcpy(&f, &bits, 4);
   return f;
 }
+
+// All 65536 conversions, tabulated once (exact: the table holds h2f_bits).
+struct H2FTable {
+  float v[65536];
+  H2FTable() {
+    for (uint32_t i = 0; i < 65536; ++i) v[i] = h2f_bits((uint16_t)i);
+  }
+};
+const H2FTable kH2F;   // built when the library loads
+inline float h2f(uint16_t h) { return kH2F.v[h]; }
 
 // float -> fp16, round to nearest even (IEEE 754 binary16).
 uint16_t f2h(float f) {
@@ -190,11 +200,12 @@ float gemv_row(int quant, const uint8_t* W, const uint16_t* S, const uint16_t* x
     }
     return (float)acc;
   }
-  float lanes[32];
-  for (int l = 0; l < 32; ++l) {
-    float a = 0.f;
-    for (int64_t c = l; c < nc; c += 32) a += dot8(quant, wrow, srow, c, x, group);
-    lanes[l] = a;
+  // lane l adds chunks l, l+32, l+64, ... in that order; the 32 lanes'
+  // chains are interleaved (independent, so the host overlaps them)
+  float lanes[32] = {0.f};
+  for (int64_t c0 = 0; c0 < nc; c0 += 32) {
+    const int n = (int)std::min<int64_t>(32, nc - c0);
+    for (int l = 0; l < n; ++l) lanes[l] += dot8(quant, wrow, srow, c0 + l, x, group);
   }
   for (int off = 16; off > 0; off >>= 1)
     for (int l = 0; l < off; ++l) lanes[l] += lanes[l + off];
