@@ -130,6 +130,8 @@ def _load():
         "cq_rope": (I32, [P, P, I32, I32, I32, P, ctypes.c_float, P]),
         "cq_gqa_attention_decode": (I32, [P, P, P, P, P, I32, I32, I32, I32, P, P]),
         "cq_attention_workspace_bytes": (SZ, [I32, I32, I32]),
+        "cq_gqa_attention_decode_noalloc": (I32, [P, P, P, P, P, I32, I32, I32, I32, P]),
+        "cq_noalloc_scratch_bytes": (SZ, []),
         "cq_kv_cache_store_hm": (I32, [P, P, P, P, P, I32, I32, I32, P]),
         "cq_gqa_attention_decode_hm": (I32, [P, P, P, P, P, I32, I32, I32, I32, P, P, P, P]),
         "cq_gqa_attention_decode_kv8": (I32, [P, P, P, P, P, P, P, P, P, I32, I32, I32, I32, P, P]),
@@ -168,7 +170,8 @@ EXPORTED = [
     "cq_fused_mlp_stage1", "cq_fused_mlp_stage2", "cq_compute_logits", "cq_apply_repetition_penalty",
     "cq_penalty_workspace_bytes", "cq_argmax", "cq_argmax_workspace_bytes", "cq_kv_k_offset", "cq_kv_v_offset",
     "cq_kv_cache_store", "cq_rope", "cq_gqa_attention_decode", "cq_attention_workspace_bytes", "cq_dequantize",
-    "cq_kv_cache_store_hm", "cq_gqa_attention_decode_hm",
+    "cq_kv_cache_store_hm", "cq_gqa_attention_decode_hm", "cq_gqa_attention_decode_noalloc",
+    "cq_noalloc_scratch_bytes",
     "cq_time_gemv", "cq_state_profile", "cq_tokenizer_load", "cq_tokenizer_free", "cq_tokenizer_encode",
     "cq_tokenizer_decode", "cq_tokenizer_token_id", "cq_tokenizer_vocab_size", "cq_chat_template",
 ]

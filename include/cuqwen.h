@@ -333,6 +333,19 @@ int cq_gqa_attention_decode(const void* q, const void* layer_k_cache, const void
                             int32_t max_seq_len, void* workspace, void* stream);
 size_t cq_attention_workspace_bytes(int32_t n_heads, int32_t n_kv_heads, int32_t head_dim);
 
+/* cq_gqa_attention_decode without a workspace argument, for callers that
+ * cannot allocate (code under HIP graph capture, serving loops that forbid
+ * hipMalloc).  No counterpart in the reference.  The split-K partials live in
+ * a static device array of cq_noalloc_scratch_bytes() bytes (2.75 MiB,
+ * enough for every shape cq_gqa_attention_decode accepts; larger needs
+ * return CQ_ERANGE), one copy per device, held until the process ends.
+ * The call allocates nothing.  All calls on one device share that copy:
+ * calls that overlap on one device (two streams, two threads) race. */
+int cq_gqa_attention_decode_noalloc(const void* q, const void* layer_k_cache, const void* layer_v_cache,
+                                    void* attn_out, const int32_t* d_pos, int32_t n_heads, int32_t n_kv_heads,
+                                    int32_t head_dim, int32_t max_seq_len, void* stream);
+size_t cq_noalloc_scratch_bytes(void);
+
 /* launch_kv_cache_store (include/kernels.cuh:37-47, src/kernels.cu:326-367):
  * k / v ([n_kv_heads * head_dim] fp16) into row *d_pos of the head-major
  * layer caches [n_kv_heads][max_seq_len][head_dim] (src/model.cu:112-114). */
