@@ -83,7 +83,7 @@ extern "C" int cq_fused_attn_block(int32_t quant_type, const void* x, const void
   a.bias[0] = (const __half*)bq; a.bias[1] = (const __half*)bk; a.bias[2] = (const __half*)bv;
   a.out[0] = (__half*)q_out; a.out[1] = (__half*)k_out; a.out[2] = (__half*)v_out;
   a.n_heads = n_heads; a.n_kv = n_kv_heads; a.head_dim = head_dim; a.d_pos = d_pos; a.rope_theta = rope_theta;
-  CQ_TRY(rope_table(rope_theta, head_dim, &a.rope_inv_freq));
+  // no table: the kernel evaluates theta^(-2i/hd) itself
   return launch_gemv(a, as_stream(stream));
 }
 

@@ -101,6 +101,11 @@ __device__ __forceinline__ float wave_max(float v) {
 // in double) is reduced modulo 2 pi in double (2 pi split in a high and a
 // low part) and its sine and cosine taken in fp32; the rotation is rounded
 // at the same points as the reference's fp32 expression.
+// RoPE inverse frequency theta^(-2i/hd) in double, for callers without the
+// host-computed table (the op-level entry points).
+__device__ __forceinline__ double rope_inv_freq_dev(float theta, int i, int hd) {
+  return 1.0 / pow((double)theta, (2.0 * i) / (double)hd);
+}
 __device__ __forceinline__ void rope_sincos(int pos, double inv_freq, float* s, float* c) {
   const double ang = (double)pos * inv_freq;
   const double k = rint(ang * 0.15915494309189535);                                        // 1 / (2 pi)
@@ -148,6 +153,12 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
   for (int i = 0; i < nw; ++i) t += red[i];
   return t;
 }
+
+// s_barrier that is also a compiler memory barrier: no LDS or global access
+// is moved across it (a bare __builtin_amdgcn_s_barrier is not one), while
+// no wait is added -- the caller waits for its own LDS stores (lgkmcnt)
+// first, and the weight loads in flight stay in flight.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
 __device__ __forceinline__ u4_t load_u4(const void* p) { return *reinterpret_cast<const u4_t*>(p); }
 __device__ __forceinline__ u4_t load_u4_stream(const void* p) {

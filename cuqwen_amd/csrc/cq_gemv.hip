@@ -5,10 +5,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
-#include <map>
-#include <mutex>
 #include <string>
-#include <tuple>
 
 namespace cq {
 
@@ -83,7 +80,10 @@ __global__ __launch_bounds__(BLK) void gemv_kernel(const GemvArgs a) {
   // waiting for a load issued after the weight prefetch would wait for the
   // whole prefetch
   double rope_f = 0.0;
-  if constexpr (MODE == GM_QKV) rope_f = a.rope_inv_freq[min((int)threadIdx.x, a.head_dim / 2 - 1)];
+  if constexpr (MODE == GM_QKV) {
+    const int i = min((int)threadIdx.x, a.head_dim / 2 - 1);
+    rope_f = a.rope_inv_freq ? a.rope_inv_freq[i] : rope_inv_freq_dev(a.rope_theta, i, a.head_dim);
+  }
   // the step's control word the epilogue needs (QKV: position; STORE: the
   // penalty epoch), also read up front rather than in the epilogue
   uint32_t step_word = 0;
@@ -161,35 +161,6 @@ void rope_inv_freq_host(float theta, int head_dim, double* out) {
   for (int i = 0; i < head_dim / 2; ++i) out[i] = 1.0 / std::pow((double)theta, (2.0 * i) / (double)head_dim);
 }
 
-int rope_table(float theta, int head_dim, const double** out) {
-  static std::mutex mu;
-  static std::map<std::tuple<int, uint32_t, int>, double*> tables;
-  if (head_dim <= 0 || head_dim > kMaxHeadDim || head_dim % 2) return fail(CQ_EINVAL, "rope: bad head_dim");
-  int dev = 0;
-  CQ_HIP(hipGetDevice(&dev));
-  uint32_t tbits;
-  std::memcpy(&tbits, &theta, 4);
-  std::lock_guard<std::mutex> lock(mu);
-  const auto key = std::make_tuple(dev, tbits, head_dim);
-  auto it = tables.find(key);
-  if (it != tables.end()) {
-    *out = it->second;
-    return CQ_OK;
-  }
-  double host[kMaxHeadDim / 2];
-  rope_inv_freq_host(theta, head_dim, host);
-  double* d = nullptr;
-  CQ_HIP(hipMalloc(&d, sizeof host));
-  const hipError_t e = hipMemcpy(d, host, sizeof(double) * (head_dim / 2), hipMemcpyHostToDevice);
-  if (e != hipSuccess) {
-    (void)hipFree(d);
-    return fail(CQ_EHIP, std::string("rope: table upload failed: ") + hipGetErrorString(e));
-  }
-  tables.emplace(key, d);
-  *out = d;
-  return CQ_OK;
-}
-
 int gemv_check(const GemvArgs& a) {
   if (a.quant < 0 || a.quant > 2) return fail(CQ_EINVAL, "gemv: bad quant type");
   if (a.K <= 0 || a.N <= 0) return fail(CQ_EINVAL, "gemv: empty shape");
@@ -203,8 +174,7 @@ int gemv_check(const GemvArgs& a) {
   if (a.mode == GM_QKV) {
     if (a.head_dim % 4 || a.head_dim > kMaxHeadDim || a.n_heads <= 0 || a.n_kv <= 0 || a.n_heads % a.n_kv)
       return fail(CQ_EINVAL, "gemv: bad head configuration");
-    if (!a.W[1] || !a.W[2] || !a.d_pos || !a.rope_inv_freq)
-      return fail(CQ_EINVAL, "gemv: qkv needs q, k, v weights, d_pos and the RoPE table");
+    if (!a.W[1] || !a.W[2] || !a.d_pos) return fail(CQ_EINVAL, "gemv: qkv needs q, k, v weights and d_pos");
     if (a.quant != CQ_QUANT_FP16 && (!a.S[1] || !a.S[2])) return fail(CQ_EINVAL, "gemv: qkv needs q, k, v scales");
     if (a.kcache && a.max_seq % 32) return fail(CQ_EINVAL, "gemv: max_seq must be a multiple of 32");
   } else if (!a.out[0]) {

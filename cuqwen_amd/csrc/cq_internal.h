@@ -24,7 +24,7 @@ struct GemvArgs {
   int n_heads = 0, n_kv = 0, head_dim = 0;
   const int* d_pos = nullptr;
   float rope_theta = 1e6f;
-  const double* rope_inv_freq = nullptr;   // [head_dim/2] theta^(-2i/hd) (rope_table)
+  const double* rope_inv_freq = nullptr;   // [head_dim/2] theta^(-2i/hd); nullptr: computed on the device
   __half* kcache = nullptr;     // layer slice, tiled layout (kv_k_offset)
   __half* vcache = nullptr;
   int max_seq = 0;
@@ -43,10 +43,6 @@ int launch_gemv(const GemvArgs& a, hipStream_t stream);
 // RoPE inverse frequencies 1 / theta^(2i/hd), i < hd/2, in double, computed
 // on the host exactly as the oracle does (std::pow).
 void rope_inv_freq_host(float theta, int head_dim, double* out);
-// A device copy of that table for the current device, built on first use
-// (hipMalloc + copy, so not from inside a stream capture) and kept for the
-// life of the process.
-int rope_table(float theta, int head_dim, const double** out);
 int gemv_check(const GemvArgs& a);
 
 int launch_dequant(int quant, int group, const void* W, const __half* S, float* out, int rows, int cols,

@@ -105,14 +105,14 @@ int launch_epoch_bump(uint32_t* d_epoch, hipStream_t stream) {
 // head rotated in place at position *d_pos, one thread per rotation pair.
 // The decode step fuses the same rotation into the QKV epilogue.
 __global__ __launch_bounds__(256) void rope_kernel(_Float16* q, _Float16* k, int n_heads, int n_kv, int hd,
-                                                   const int* d_pos, const double* inv_freq) {
+                                                   const int* d_pos, float theta) {
   const int half = hd / 2;
   const int id = blockIdx.x * blockDim.x + threadIdx.x;
   if (id >= (n_heads + n_kv) * half) return;
   const int head = id / half, i = id % half;
   _Float16* v = head < n_heads ? q + (int64_t)head * hd : k + (int64_t)(head - n_heads) * hd;
   float y0 = (float)v[i], y1 = (float)v[i + half];
-  rope_rotate(y0, y1, *d_pos, inv_freq[i]);
+  rope_rotate(y0, y1, *d_pos, rope_inv_freq_dev(theta, i, hd));
   v[i] = (_Float16)y0;
   v[i + half] = (_Float16)y1;
 }
@@ -120,11 +120,10 @@ __global__ __launch_bounds__(256) void rope_kernel(_Float16* q, _Float16* k, int
 int launch_rope(__half* q, __half* k, int n_heads, int n_kv, int head_dim, const int* d_pos, float theta,
                 hipStream_t stream) {
   if (!q || !k || !d_pos || n_heads <= 0 || n_kv <= 0) return fail(CQ_EINVAL, "rope: bad arguments");
-  const double* table = nullptr;
-  CQ_TRY(rope_table(theta, head_dim, &table));
+  if (head_dim <= 0 || head_dim > kMaxHeadDim || head_dim % 2) return fail(CQ_EINVAL, "rope: bad head_dim");
   const int n = (n_heads + n_kv) * (head_dim / 2);
   hipLaunchKernelGGL(rope_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, (_Float16*)q, (_Float16*)k, n_heads,
-                     n_kv, head_dim, d_pos, table);
+                     n_kv, head_dim, d_pos, theta);
   CQ_HIP(hipGetLastError());
   return CQ_OK;
 }

@@ -46,7 +46,10 @@ __device__ __forceinline__ int pf_pos(int k, bool int4) {
   const int e = k & 7;
   return (k & ~7) | (e < 4 ? 2 * e : 2 * e - 7);
 }
-// value stored for element k (exact: a power-of-two scale)
+// value stored for element k.  The /16 is a power-of-two scale, exact for
+// |v| >= 2^-10; below that v/16 falls in fp16's subnormal range and keeps
+// fewer bits (at most 2^-21 absolute error on the element: half the 2^-24
+// subnormal spacing, times 16).
 __device__ __forceinline__ _Float16 pf_val(float v, int k, bool int4) {
   return (_Float16)((int4 && (k & 1)) ? v * 0.0625f : v);
 }
@@ -323,7 +326,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
     else __builtin_amdgcn_s_waitcnt(0x0F70);
     x_store(stg);
     __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): the LDS stores are done
-    __builtin_amdgcn_s_barrier();
+    lds_barrier();
     const _Float16* xb0 = xs0 + stg * XS;
     h2_t s2[NMAT][RT];
     u4_t w[NMAT][RT][L];
@@ -928,7 +931,7 @@ __global__ __launch_bounds__(kPfGqaWaves * kWave) void pf_attention_gqa_kernel(c
     __builtin_amdgcn_s_waitcnt(0x0F70);
     store(sp);
     __builtin_amdgcn_s_waitcnt(0xC07F);
-    __builtin_amdgcn_s_barrier();
+    lds_barrier();
     if (sp + 1 < n_steps) load(sp + 1);
     const int ti = 2 * sp + half;
     if (active && ti < n_tiles) {
@@ -998,7 +1001,9 @@ __global__ __launch_bounds__(kPfGqaWaves * kWave) void pf_attention_gqa_kernel(c
 
 // One row of a GEMM input back to natural order (the int4 layout stores each
 // 8-group as [0,4,1,5,2,6,3,7] with the odd elements / 16; the scale is a
-// power of two, so the round trip is exact).
+// power of two, so the round trip is exact for odd elements of magnitude at
+// least 2^-10 -- smaller ones lost low bits to the subnormal range on the way
+// in).
 __global__ __launch_bounds__(256) void pf_row_natural(const _Float16* src, _Float16* dst, int n, bool int4) {
   for (int k = threadIdx.x; k < n; k += blockDim.x)
     dst[k] = (_Float16)((float)src[pf_pos(k, int4)] * ((int4 && (k & 1)) ? 16.0f : 1.0f));

@@ -35,7 +35,6 @@ struct cq_tokenizer {
   std::unordered_map<std::string, int32_t> encoder;   // byte-alphabet token -> id
   std::unordered_map<int32_t, std::string> decoder;
   std::vector<std::pair<std::string, int32_t>> specials;   // longest first
-  std::unordered_map<int32_t, std::string> special_text;
   std::string byte_token[256];                              // byte -> its one-character token
   std::unordered_map<uint32_t, uint8_t> byte_of_cp;         // alphabet code point -> byte
 };
@@ -399,15 +398,20 @@ void encode(const cq_tokenizer& t, const char* s, size_t n, std::vector<int32_t>
   }
 }
 
+// src/tokenizer.cpp:210-236: the decoder is the vocabulary only -- an id
+// that is not in it (Qwen's added tokens such as <|im_end|> are not in
+// vocab.json) decodes to nothing; a vocabulary entry whose text is one of
+// the added tokens decodes to that text literally; any other entry maps its
+// byte-alphabet characters back to bytes.
 void decode_one(const cq_tokenizer& t, int32_t id, std::string& out) {
-  auto sp = t.special_text.find(id);
-  if (sp != t.special_text.end()) {
-    out += sp->second;
-    return;
-  }
   auto it = t.decoder.find(id);
-  if (it == t.decoder.end()) return;   // unknown ids decode to nothing (src/tokenizer.cpp:211)
+  if (it == t.decoder.end()) return;
   const std::string& tok = it->second;
+  for (const auto& sp : t.specials)
+    if (sp.first == tok) {
+      out += tok;
+      return;
+    }
   for (const Char& ch : decode_utf8(tok.data(), tok.size())) {
     auto b = ch.cp == kInvalid ? t.byte_of_cp.end() : t.byte_of_cp.find(ch.cp);
     if (b != t.byte_of_cp.end()) {
@@ -456,8 +460,6 @@ extern "C" int cq_tokenizer_load(const char* ranks_json_path, cq_tokenizer** out
         const long id = std::strtol(id_text.c_str(), &end, 10);
         if (id_text.empty() || *end || id < 0) return js.fail("bad added-token id '" + id_text + "'");
         t->specials.emplace_back(tok, (int32_t)id);
-        t->special_text[(int32_t)id] = tok;
-        t->decoder[(int32_t)id] = tok;
         return true;
       });
     }
@@ -513,6 +515,7 @@ extern "C" int32_t cq_tokenizer_vocab_size(cq_tokenizer* t) {
   if (!t) return -1;
   int32_t m = -1;
   for (const auto& kv : t->decoder) m = std::max(m, kv.first);
+  for (const auto& sp : t->specials) m = std::max(m, sp.second);   // added tokens count too
   return m + 1;
 }
 

@@ -434,8 +434,10 @@ int cq_tokenizer_encode(cq_tokenizer* t, const char* text, size_t len, int32_t* 
                         int32_t* n_out);
 
 /* QwenTokenizer::decode / decode_single (src/tokenizer.cpp:203-238): the
- * bytes of the ids' tokens (special tokens as their text, unknown ids as
- * nothing).  *len_out = bytes needed; CQ_ERANGE when `cap` is too small. */
+ * bytes of the ids' vocabulary tokens; ids not in the vocabulary -- which
+ * includes added tokens such as <|im_end|> that vocab.json lacks -- decode
+ * to nothing, and a vocabulary entry spelling an added token decodes to its
+ * text.  *len_out = bytes needed; CQ_ERANGE when `cap` is too small. */
 int cq_tokenizer_decode(cq_tokenizer* t, const int32_t* ids, int32_t n, char* buf, size_t cap, size_t* len_out);
 
 /* Id of a vocabulary or special token (e.g. "<|im_end|>"), -1 if absent. */

@@ -128,6 +128,27 @@ def test_gemv_add_residual(g, quant):
 
 
 @pytest.mark.parametrize("quant", [0, 1, 2])
+@pytest.mark.parametrize("dim,inter", [(896, 4864), (3584, 18944)])
+def test_mlp_stage2_down_residual(g, quant, dim, inter):
+    """launch_fused_mlp_stage2 (kernels.cu:590-635) at the 0.5B and 7B down
+    projections: x[r] = half(float(x[r]) + Wd[r] . inter), the residual read
+    and written in place."""
+    Wd, Sd = _weights(quant, dim, inter, 31 + dim)
+    rng = np.random.default_rng(32 + dim)
+    inter_v = (0.5 * rng.standard_normal(inter)).astype(np.float16)
+    x0 = rng.standard_normal(dim).astype(np.float16)
+    xb = g.empty(dim * 2)
+    xb.upload(x0)
+    cq.check(cq.lib.cq_fused_mlp_stage2(quant, xb.ptr, g.put(Wd), g.put(Sd), g.put(inter_v), dim, inter, None))
+    got = xb.to_array(np.float16)
+    y = orc.gemv(quant, Wd, Sd, inter_v, dim, inter, 128, mode=1)
+    assert rel_err(got, x0.astype(np.float32) + y) <= TOL
+    # the stored value is the fp16 rounding of the fp32 sum (the residual stays fp16, kernels.cu:621)
+    y0 = orc.gemv(quant, Wd, Sd, inter_v, dim, inter, 128, mode=0)
+    assert rel_err(got, (x0.astype(np.float32) + y0).astype(np.float16)) <= TOL
+
+
+@pytest.mark.parametrize("quant", [0, 1, 2])
 @pytest.mark.parametrize("norm", [False, True])
 def test_mlp_stage1_swiglu(g, quant, norm):
     """kernels.cu:523-569 (+ the rmsnorm of kernels.cu:689-751 when fused)."""

@@ -73,6 +73,29 @@ def test_prefill_tiny_matches_oracle(quant, segments):
     w.free()
 
 
+@pytest.mark.parametrize("heads,kv_heads,hd", [(16, 1, 64), (12, 1, 128), (10, 1, 64), (24, 2, 64)])
+@pytest.mark.parametrize("quant", [0, 2])
+def test_prefill_large_gqa_groups_match_oracle(quant, heads, kv_heads, hd):
+    """GQA groups of 9-16 query heads per kv head (the per-head prefill
+    attention path for the fp16 cache) against the oracle run token by
+    token: logits, top-1 and the KV cache, then decode continues."""
+    cfg = tiny_config(quant, n_heads=heads, n_kv_heads=kv_heads, head_dim=hd, dim=1024)
+    w = cq.synth_weights(cfg, 23)
+    om = orc.Model.synth(cfg, 23, cfg.max_seq_len)
+    st = cq.State(cfg, w)
+    prompt = _prompt(cfg, 83, 7)
+    ot = _oracle_prompt(om, prompt, 0)
+    gt = st.prefill(prompt, 0)
+    assert _rel(st.logits(), om.logits()) <= TOL
+    if _gap(om.logits()) > 1e-2:
+        assert gt == ot
+    _check_kv(cfg, st, om.kv, len(prompt))
+    a, b = om.forward(ot, len(prompt), []), st.forward(ot, len(prompt), [])
+    assert _rel(st.logits(), om.logits()) <= TOL
+    st.free()
+    w.free()
+
+
 @pytest.mark.parametrize("n", [2100, 2049])
 def test_prefill_crosses_chunks(n):
     """A prompt longer than 2048 tokens is several passes of at most 2048
