@@ -246,6 +246,8 @@ struct Json {
             if (!hex4(&lo)) return false;
             if (lo >= 0xDC00 && lo <= 0xDFFF) cp = 0x10000 + ((cp - 0xD800) << 10) + (lo - 0xDC00);
             else return fail("unpaired surrogate");
+          } else if (cp >= 0xD800 && cp <= 0xDFFF) {
+            return fail("unpaired surrogate");   // a lone half of a pair is not text (RFC 8259 section 8.2)
           }
           put_utf8(cp, *out);
           break;
