@@ -199,30 +199,99 @@ def config_legs(cq):
     return out
 
 
-def cpu_baseline(cfg, ctx, threads):
-    """Host oracle (scalar C++ restatement) on this box's cores: a 1-layer and
-    a 2-layer model of the same shapes at `ctx`, one decode step each;
-    t_token = t1 + (L - 1) * (t2 - t1)."""
+def cpu_baseline(cq, threads):
+    """The host oracle (scalar C++ restatement of the reference kernels) on
+    this box's cores, at 1 thread and at N threads (OpenMP over GEMV rows and
+    attention heads), as BASELINE.md section 3 plans it:
+      * config 1: the W8A16 GEMV (K 4864, N 896), median of 20 calls;
+      * configs 2, 3: whole-model decode steps (0.5B INT8 at 1024, 1.5B INT4
+        at 4096 with the KV cache prefilled), median ms per token;
+      * configs 4, 5: a one-layer model of the real shapes, its layer time
+        and lm_head time measured (median) at the context and extrapolated to
+        all layers: t = t_head + n_layers * t_layer (labelled extrapolated).
+    The headline value is config 4's 7B INT4 at 32K with N threads."""
     from oracle import oracle as orc
-    import numpy as np  # noqa: F401
-    if threads > 0:
-        orc.set_threads(threads)
-    cores = orc.lib.or_max_threads()
-    times = []
-    for nl in (1, 2):
-        c = cfg.replace(n_layers=nl)
-        m = orc.Model.synth(c, 0x5157454E, ctx)
-        m.fill_kv(ctx - 1, 77)
-        t0 = time.perf_counter()
-        m.forward(1, ctx - 1, [], mode=0)
-        times.append(time.perf_counter() - t0)
+    import numpy as np
+    n_cores = threads if threads > 0 else orc.lib.or_max_threads()
+    legs = []
+
+    def timed(fn, reps):
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return float(np.median(ts))
+
+    # config 1
+    rng = np.random.default_rng(1)
+    w = (rng.standard_normal((896, 4864)) * 0.02).astype(np.float16)
+    q, sc = orc.quantize(1, w)
+    x = rng.standard_normal(4864).astype(np.float16)
+    leg = {"config": 1, "what": "W8A16 GEMV K=4864 N=896, median of 20 calls"}
+    for k in (1, n_cores):
+        orc.set_threads(k)
+        t = timed(lambda: orc.gemv(1, q, sc, x, 896, 4864, 128, 0), 20)
+        leg[f"threads_{k}"] = {"us": round(t * 1e6, 1), "GBps": round(4437760 / t / 1e9, 2)}
+    legs.append(leg)
+
+    # configs 2, 3: whole models
+    for cfgno, model, quant, ctx, steps in ((2, "0.5B", "int8", 1024, (6, 2)), (3, "1.5B", "int4", 4096, (6, 2))):
+        cfg = cq.preset(model, quant)
+        orc.set_threads(n_cores)
+        m = orc.Model.synth(cfg, 0x5157454E, ctx + 16)
+        m.fill_kv(ctx, 77)
+        leg = {"config": cfgno, "what": f"Qwen2.5-{model} {quant.upper()} decode steps at {ctx}.., whole model, "
+                                        "median ms per token"}
+        for k, n in zip((n_cores, 1), steps):
+            orc.set_threads(k)
+            ts = []
+            for i in range(n):
+                t0 = time.perf_counter()
+                m.forward(1 + i, ctx + i, [])
+                ts.append(time.perf_counter() - t0)
+            leg[f"threads_{k}"] = {"ms_per_token": round(1e3 * float(np.median(ts)), 2),
+                                   "tok_per_s": round(1.0 / float(np.median(ts)), 3)}
         del m
-    t_layer = max(times[1] - times[0], 1e-9)
-    t_tok = times[0] + (cfg.n_layers - 1) * t_layer
-    return {"value": round(1.0 / t_tok, 4), "unit": "tok/s", "cores": cores, "kind": "port",
-            "sample": f"host oracle, one decode step of a 1-layer and a 2-layer Qwen2.5-{cfg.n_layers}L-shaped "
-                      f"model at ctx {ctx} (t1={times[0]:.3f}s, t2={times[1]:.3f}s), extrapolated to "
-                      f"{cfg.n_layers} layers"}
+        legs.append(leg)
+
+    # configs 4, 5: one layer + head, extrapolated
+    headline = single = None
+    for cfgno, model, quant, ctxs in ((4, "7B", "int4", (1024, 8192, 32768)), (4, "7B", "int8", (1024, 8192, 32768)),
+                                      (4, "7B", "fp16", (1024, 8192, 32768)), (5, "14B", "int4", (32768,))):
+        full = cq.preset(model, quant)
+        orc.set_threads(n_cores)
+        m = orc.Model.synth(full.replace(n_layers=1), 0x5157454E, max(ctxs))
+        m.fill_kv(max(ctxs) - 1, 77)
+        for ctx in ctxs:
+            leg = {"config": cfgno, "what": f"Qwen2.5-{model} {quant.upper()} at ctx {ctx}: one layer + lm_head "
+                                            f"timed, extrapolated to {full.n_layers} layers"}
+            for k, reps in ((n_cores, 3), (1, 1)):
+                if k == 1 and ctx != max(ctxs):
+                    continue   # single-thread sample at the longest context only (bounded run time)
+                orc.set_threads(k)
+                lay, head = [], []
+                for _ in range(reps):
+                    m.forward(1, ctx - 1, [])
+                    a, b = m.last_times()
+                    lay.append(a)
+                    head.append(b)
+                t_tok = float(np.median(head)) + full.n_layers * float(np.median(lay))
+                leg[f"threads_{k}"] = {"layer_ms": round(1e3 * float(np.median(lay)), 2),
+                                       "head_ms": round(1e3 * float(np.median(head)), 2),
+                                       "ms_per_token_extrapolated": round(1e3 * t_tok, 1),
+                                       "tok_per_s_extrapolated": round(1.0 / t_tok, 4)}
+            legs.append(leg)
+            if (model, quant, ctx) == ("7B", "int4", 32768):
+                headline = leg[f"threads_{n_cores}"]["tok_per_s_extrapolated"]
+                single = leg["threads_1"]["tok_per_s_extrapolated"]
+        del m
+    orc.set_threads(n_cores)
+    return {"value": headline, "unit": "tok/s", "cores": n_cores, "kind": "port",
+            "sample": "host oracle (scalar C++ restatement, OpenMP over rows / heads): one decode step of a "
+                      "1-layer Qwen2.5-7B INT4 model at ctx 32768 (KV prefilled), layer and lm_head timed "
+                      "(median of 3), extrapolated to 28 layers",
+            "single_thread": {"value": single, "cores": 1}, "legs": legs}
 
 
 def main():
@@ -304,7 +373,7 @@ def main():
     cpu = None
     if not args.no_cpu_baseline:
         t2 = time.perf_counter()
-        cpu = cpu_baseline(cfg, args.ctx, args.cpu_threads)
+        cpu = cpu_baseline(cq, args.cpu_threads)
         log(f"[bench] cpu baseline {cpu} ({time.perf_counter() - t2:.1f}s)")
 
     res = {

@@ -25,6 +25,8 @@
 #include <vector>
 #include <omp.h>
 
+#include <chrono>
+
 namespace {
 
 // ------------------------------------------------------------------ fp16
@@ -521,6 +523,7 @@ struct Model {
   std::vector<float> Ks, Vs;
   std::vector<uint16_t> logits;
   int nparts = 64;
+  double t_layers = 0.0, t_head = 0.0;   // seconds spent by the last forward() in the layers / after them
 };
 
 void gen_vec(std::vector<uint16_t>& v, int64_t n, uint64_t seed, int layer, int kind, float mean) {
@@ -596,6 +599,7 @@ void store_kv(Model& m, int l, int pos, const uint16_t* k, const uint16_t* v) {
 
 // src/model.cu:76-181: one decode step; returns the argmax id.
 int forward(Model& m, int token, int pos, const int* hist, int hlen, int mode) {
+  const auto t0 = std::chrono::steady_clock::now();
   const Cfg& c = m.c;
   const int64_t d = c.dim, qd = (int64_t)c.heads * c.hd, kvd = (int64_t)c.kv * c.hd, I = c.inter;
   std::vector<uint16_t> x(m.embed.begin() + (int64_t)token * d, m.embed.begin() + (int64_t)(token + 1) * d);
@@ -638,6 +642,7 @@ int forward(Model& m, int token, int pos, const int* hist, int hlen, int mode) {
 #pragma omp parallel for
     for (int64_t r = 0; r < d; ++r) x[r] = f2h(h2f(x[r]) + gemv(Ly.wd, inter.data(), r));   // kernels.cu:621
   }
+  const auto t1 = std::chrono::steady_clock::now();
   rmsnorm(x.data(), m.final_norm.data(), xn.data(), d, eps, mode);
   if (m.lm.rows) {
 #pragma omp parallel for
@@ -648,7 +653,11 @@ int forward(Model& m, int token, int pos, const int* hist, int hlen, int mode) {
       m.logits[r] = f2h(gemv_row(0, reinterpret_cast<const uint8_t*>(m.embed.data()), nullptr, xn.data(), r, d, 128, mode));
   }
   penalty(m.logits.data(), hist, hlen, c.vocab, 1.1f);
-  return argmax(m.logits.data(), c.vocab);
+  const int id = argmax(m.logits.data(), c.vocab);
+  const auto t2 = std::chrono::steady_clock::now();
+  m.t_layers = std::chrono::duration<double>(t1 - t0).count();
+  m.t_head = std::chrono::duration<double>(t2 - t1).count();
+  return id;
 }
 
 }  // namespace
@@ -819,6 +828,13 @@ int or_model_forward(void* h, int token, int pos, const int* hist, int hlen, int
   Model& m = *static_cast<Model*>(h);
   if (pos < 0 || pos >= m.kv_slots || token < 0 || token >= m.c.vocab) return -1;
   return forward(m, token, pos, hist, hlen, mode);
+}
+// Wall time of the last forward(): [0] embedding + layers, [1] final norm +
+// lm_head + penalty + argmax (for the CPU baseline's per-layer extrapolation).
+void or_model_last_times(void* h, double* out) {
+  const Model& m = *static_cast<Model*>(h);
+  out[0] = m.t_layers;
+  out[1] = m.t_head;
 }
 void or_model_logits(void* h, uint16_t* out) {
   Model& m = *static_cast<Model*>(h);

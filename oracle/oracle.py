@@ -55,6 +55,7 @@ def _load():
         "or_model_fill_kv": (None, [P, I, U64]),
         "or_model_forward": (I, [P, I, I, P, I, I]),
         "or_model_logits": (None, [P, P]),
+        "or_model_last_times": (None, [P, P]),
         "or_model_kv": (None, [P, I, I, I, I, P]),
         "or_model_tensor": (I64, [P, I, I, I, P]),
     }
@@ -245,6 +246,12 @@ class Model:
         if r < 0:
             raise ValueError("oracle: bad token / pos")
         return r
+
+    def last_times(self):
+        """(embedding + layers, head) seconds of the last forward()."""
+        t = np.zeros(2, dtype=np.float64)
+        lib.or_model_last_times(self.h, _p(t))
+        return float(t[0]), float(t[1])
 
     def logits(self):
         out = np.zeros(self.cfg.vocab_size, dtype=np.uint16)
