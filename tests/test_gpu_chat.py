@@ -58,3 +58,37 @@ def test_chat_session_two_turns_match_oracle(tmp_path):
     st.free()
     w.free()
     tok.free()
+
+
+def test_chat_cli_matches_chat_session(tmp_path):
+    """python -m cuqwen_amd.chat (the reference's REPL, src/main.cu:14-140):
+    two user turns on stdin, then "exit"; the streamed replies equal
+    ChatSession's on the same weights, and each turn ends with the
+    reference's stats line."""
+    import subprocess
+    import sys
+    hf = train_hf_tokenizer()
+    ranks = tmp_path / "ranks.json"
+    write_ranks(hf, ranks)
+    cfg = tiny_config(2)
+    wpath = str(tmp_path / "tiny.bin")
+    cq.write_synthetic_file(wpath, cfg, 11)
+    turns = ["Hello there! How's it going?", "", "Tell me about 日本語 and numbers 42."]
+    r = subprocess.run([sys.executable, "-m", "cuqwen_amd.chat", "--weights", wpath, "--tokenizer", str(ranks),
+                        "--max-new-tokens", "10"], input="\n".join(turns + ["exit"]) + "\n",
+                       capture_output=True, text=True, timeout=300,
+                       cwd=str(tmp_path), env=dict(__import__("os").environ, PYTHONPATH=cq._HERE + "/.."))
+    assert r.returncode == 0, r.stderr
+    tok = cq.Tokenizer(str(ranks))
+    cfg2, w = cq.load_weights(wpath)
+    st = cq.State(cfg2, w)
+    chat = cq.ChatSession(st, tok, eos_id=tok.token_id("<|endoftext|>"), im_end_id=tok.token_id("<|im_end|>"))
+    replies = [chat.reply(t, max_new_tokens=10)[0] for t in turns if t]
+    out = r.stdout
+    for text in replies:
+        assert "Qwen > " + text + "\n\n[" in out
+    assert out.count("tokens generated |") == 2
+    assert f"Context: {chat.pos}/{cfg.max_seq_len}]" in out
+    st.free()
+    w.free()
+    tok.free()
