@@ -35,6 +35,7 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-profile", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-floors", action="store_true", help="skip the streaming-floor leg")
     ap.add_argument("--no-kv8", action="store_true", help="skip the int8 and fp8 KV cache legs")
     ap.add_argument("--prompt", type=int, default=1024, help="prompt tokens of the batched-prefill measurement")
     ap.add_argument("--configs", action="store_true",
@@ -89,6 +90,33 @@ def gemv_config1(cq, np):
         b[1].free()
     return {"shape": "M=1 K=4864 N=896 W8A16 g128", "us": round(us.value, 3), "bytes": alg,
             "GBps": round(alg / us.value / 1e3, 1), "frac": round(alg / us.value / 1e3 / PEAK_GBPS, 4)}
+
+
+def floors_leg(cq, kernels):
+    """Streaming floor of each decode kernel's algorithmic byte count: a plain
+    16-byte-load read of that many bytes in a graph chain (cq_time_stream),
+    rotated over copies that together exceed the 256 MB last-level cache;
+    plus the empty launch (per-node cost)."""
+    import ctypes
+    out = []
+    items = [("empty_node", 0)] + [(k["kernel"], k["bytes"]) for k in kernels if k["kernel"] != "argmax"]
+    for name, nbytes in items:
+        n = (int(nbytes) + 15) // 16 * 16
+        nbuf = 1 if n == 0 else max(2, min(64, -(-600_000_000 // n)))
+        bufs = [cq.DeviceBuffer(n) for _ in range(nbuf)] if n else []
+        for b in bufs:
+            b.zero()
+        arr = (ctypes.c_void_p * max(1, nbuf))(*[b.value for b in bufs]) if bufs else None
+        us = ctypes.c_double()
+        cq.check(cq.lib.cq_time_stream(n, nbuf, arr, max(8, 4 * nbuf), ctypes.byref(us)))
+        for b in bufs:
+            b.free()
+        leg = {"kernel": name, "bytes": n, "floor_us": round(us.value, 3)}
+        if n:
+            leg["TBps"] = round(n / us.value / 1e6, 3)
+        out.append(leg)
+        log(f"[bench] floor {leg}")
+    return out
 
 
 def prefill_leg(cq, cfg, st, n):
@@ -342,6 +370,9 @@ def main():
         roof = {"bound": "hbm", "kernel": dom["kernel"], "achieved": dom["GBps"], "peak": PEAK_GBPS,
                 "unit": "GB/s", "frac": dom["frac"], "traffic": traffic,
                 "bytes_per_launch": dom["bytes"], "us_per_launch": dom["us"]}
+    floors = None
+    if kernels and not args.no_floors:
+        floors = floors_leg(cq, kernels)
     g1 = None
     if not args.no_profile:
         g1 = gemv_config1(cq, np)
@@ -386,7 +417,7 @@ def main():
                    "model": f"Qwen2.5-{args.model}", "global_batch": 1, "seq_len": args.ctx,
                    "parallelism": "single-gpu"},
         "device_ms_per_step": round(dev_us / 1e3, 5),
-        "roofline": roof, "cpu_baseline": cpu, "kernels": kernels, "gemv_config1": g1, "prefill": pf, "kv_int8": kv8, "kv_fp8": kvf8,
+        "roofline": roof, "cpu_baseline": cpu, "kernels": kernels, "floors": floors, "gemv_config1": g1, "prefill": pf, "kv_int8": kv8, "kv_fp8": kvf8,
         "configs": legs,
     }
     print(json.dumps(res), flush=True)

@@ -402,6 +402,14 @@ int cq_time_gemv(int32_t quant_type, int32_t group_size, int32_t n_bufs, void* c
                  void* const* S_list, const void* x, void* y, int32_t rows, int32_t cols,
                  int32_t iters, double* us_per_launch);
 
+/* Streaming floor: a plain read of n_bytes (16-byte loads, one block per
+ * CU) recorded `iters` times into one HIP graph rotating over the n_bufs
+ * buffers, replayed between HIP events; *us_per_launch = elapsed / iters.
+ * The time any kernel that reads n_bytes meets in the decode step's graph
+ * chain.  n_bytes 0 times the empty launch (per-node cost).  Measurement
+ * hook; no counterpart in the reference. */
+int cq_time_stream(size_t n_bytes, int32_t n_bufs, void* const* bufs, int32_t iters, double* us_per_launch);
+
 /* Per-kernel profile of the decode step at position `pos` (the reference's
  * benchmark/kernel_profile.cu): each kernel of the step is launched for every
  * layer in turn (so weights rotate through all layers), `iters` rounds,

@@ -75,20 +75,20 @@ def test_chat_cli_matches_chat_session(tmp_path):
     cq.write_synthetic_file(wpath, cfg, 11)
     turns = ["Hello there! How's it going?", "", "Tell me about 日本語 and numbers 42."]
     r = subprocess.run([sys.executable, "-m", "cuqwen_amd.chat", "--weights", wpath, "--tokenizer", str(ranks),
-                        "--max-new-tokens", "10"], input="\n".join(turns + ["exit"]) + "\n",
-                       capture_output=True, text=True, timeout=300,
+                        "--max-new-tokens", "10"], input=("\n".join(turns + ["exit"]) + "\n").encode(),
+                       capture_output=True, timeout=300,
                        cwd=str(tmp_path), env=dict(__import__("os").environ, PYTHONPATH=cq._HERE + "/.."))
-    assert r.returncode == 0, r.stderr
+    assert r.returncode == 0, r.stderr.decode(errors="replace")
     tok = cq.Tokenizer(str(ranks))
     cfg2, w = cq.load_weights(wpath)
     st = cq.State(cfg2, w)
     chat = cq.ChatSession(st, tok, eos_id=tok.token_id("<|endoftext|>"), im_end_id=tok.token_id("<|im_end|>"))
-    replies = [chat.reply(t, max_new_tokens=10)[0] for t in turns if t]
-    out = r.stdout
-    for text in replies:
-        assert "Qwen > " + text + "\n\n[" in out
-    assert out.count("tokens generated |") == 2
-    assert f"Context: {chat.pos}/{cfg.max_seq_len}]" in out
+    gens = [chat.reply(t, max_new_tokens=10)[1] for t in turns if t]
+    out = r.stdout   # bytes: a random-weight reply need not be valid UTF-8
+    for gen in gens:
+        assert b"Qwen > " + tok.decode_bytes(gen) + b"\n\n[" in out
+    assert out.count(b"tokens generated |") == 2
+    assert f"Context: {chat.pos}/{cfg.max_seq_len}]".encode() in out
     st.free()
     w.free()
     tok.free()
