@@ -108,7 +108,8 @@ def floors_leg(cq, kernels):
             b.zero()
         arr = (ctypes.c_void_p * max(1, nbuf))(*[b.value for b in bufs]) if bufs else None
         us = ctypes.c_double()
-        cq.check(cq.lib.cq_time_stream(n, nbuf, arr, max(8, 4 * nbuf), ctypes.byref(us)))
+        # enough nodes per graph replay that the replay's own launch cost (~10 us) vanishes
+        cq.check(cq.lib.cq_time_stream(n, nbuf, arr, max(64 if n > 100_000_000 else 256, 4 * nbuf), ctypes.byref(us)))
         for b in bufs:
             b.free()
         leg = {"kernel": name, "bytes": n, "floor_us": round(us.value, 3)}
