@@ -327,9 +327,15 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
         if constexpr (Q != CQ_QUANT_FP16) s[mt][rt] = srow[mt][rt][ks];
       }
   };
+  // Every load is issued unconditionally (step indices clamped to the last
+  // step; the repeats past it are never used): with loads under branches the
+  // compiler's wait-count tracking merges the paths conservatively and waits
+  // for all loads, the next step's weight prefetch included, before the
+  // activation stores of every step.
   load_w_step(kb, wv[0], sv[0]);
   x_load(kb);
-  if (kb + 1 < ke) load_w_step(kb + 1, wv[1], sv[1]);
+  __builtin_amdgcn_sched_barrier(0);
+  load_w_step(min(kb + 1, ke - 1), wv[1], sv[1]);
 
   const UnpackRegs uk = unpack_regs();
   auto step = [&](auto I, int ks) {
@@ -337,8 +343,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
     const int stg = (ks - kb) & 1;
     // simm16 of s_waitcnt on gfx9: vmcnt in bits [3:0] and [15:14], expcnt
     // [6:4], lgkmcnt [11:8]; the fields not waited on are left at their maxima
-    if (ks + 1 < ke) __builtin_amdgcn_s_waitcnt(0x0F70 | (WL & 15) | ((WL >> 4) << 14));
-    else __builtin_amdgcn_s_waitcnt(0x0F70);
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (WL & 15) | ((WL >> 4) << 14));
     x_store(stg);
     __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): the LDS stores are done
     lds_barrier();
@@ -353,8 +358,11 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
 #pragma unroll
         for (int i = 0; i < L; ++i) w[mt][rt][i] = wv[S][mt][rt][i];
       }
-    if (ks + 1 < ke) x_load(ks + 1);
-    if (ks + 2 < ke) load_w_step(ks + 2, wv[S], sv[S]);
+    // activations first: the next step waits for them with the weights
+    // requested here still in flight (the wait counts loads in issue order)
+    x_load(min(ks + 1, ke - 1));
+    __builtin_amdgcn_sched_barrier(0);
+    load_w_step(min(ks + 2, ke - 1), wv[S], sv[S]);
     // B fragments of one sub-step
     auto read_b = [&](int s4, h8_t* xb) {
 #pragma unroll
