@@ -169,6 +169,8 @@ struct cq_state {
   int* host_pinned = nullptr;     // staging for the per-step control words
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
+  hipGraph_t graph_run = nullptr;       // kStepsPerRun chained steps (cq_decode)
+  hipGraphExec_t exec_run = nullptr;
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
   double last_us = 0.0;
   double last_prefill_us = 0.0;
@@ -287,6 +289,28 @@ int step_body(cq_state* s) {
   return CQ_OK;
 }
 
+// Steps recorded back to back in the chained-decode graph: one graph launch
+// per kStepsPerRun tokens instead of one per token.
+constexpr int kStepsPerRun = 8;
+
+int ensure_run_graph(cq_state* s) {
+  if (s->exec_run) return CQ_OK;
+  if (!s->w) return fail(CQ_EINVAL, "no weights bound to the state (pass them to cq_forward_ex)");
+  CQ_HIP(hipStreamBeginCapture(s->stream, hipStreamCaptureModeThreadLocal));
+  int rc = CQ_OK;
+  for (int i = 0; i < kStepsPerRun && rc == CQ_OK; ++i) rc = step_body(s);
+  hipGraph_t g = nullptr;
+  const hipError_t e = hipStreamEndCapture(s->stream, &g);
+  if (rc != CQ_OK) {
+    if (g) hipGraphDestroy(g);
+    return rc;
+  }
+  CQ_HIP(e);
+  s->graph_run = g;
+  CQ_HIP(hipGraphInstantiate(&s->exec_run, g, nullptr, nullptr, 0));
+  return CQ_OK;
+}
+
 int ensure_graph(cq_state* s) {
   if (s->exec) return CQ_OK;
   if (!s->w) return fail(CQ_EINVAL, "no weights bound to the state (pass them to cq_forward_ex)");
@@ -333,6 +357,14 @@ int bind_weights(cq_state* s, const cq_weights* w) {
   if (s->graph) {
     hipGraphDestroy(s->graph);
     s->graph = nullptr;
+  }
+  if (s->exec_run) {
+    hipGraphExecDestroy(s->exec_run);
+    s->exec_run = nullptr;
+  }
+  if (s->graph_run) {
+    hipGraphDestroy(s->graph_run);
+    s->graph_run = nullptr;
   }
   s->w = w;
   return CQ_OK;
@@ -600,6 +632,8 @@ extern "C" int cq_state_destroy(cq_state* s) {
   if (s->stream) hipStreamSynchronize(s->stream);
   if (s->exec) hipGraphExecDestroy(s->exec);
   if (s->graph) hipGraphDestroy(s->graph);
+  if (s->exec_run) hipGraphExecDestroy(s->exec_run);
+  if (s->graph_run) hipGraphDestroy(s->graph_run);
   if (s->ev0) hipEventDestroy(s->ev0);
   if (s->ev1) hipEventDestroy(s->ev1);
   if (s->host_pinned) hipHostFree(s->host_pinned);
@@ -643,9 +677,12 @@ extern "C" int cq_decode(cq_state* s, int32_t token, int32_t pos0, int32_t n_ste
   if (n_steps <= 0 || (int64_t)pos0 + n_steps > s->cfg.max_seq_len)
     return fail(CQ_ERANGE, "decode: pos0 + n_steps exceeds max_seq_len");
   CQ_TRY(ensure_graph(s));
+  if (n_steps >= kStepsPerRun) CQ_TRY(ensure_run_graph(s));
   CQ_TRY(set_ctl(s, token, pos0, history, history_len, 1));
   CQ_HIP(hipEventRecord(s->ev0, s->stream));
-  for (int i = 0; i < n_steps; ++i) CQ_HIP(hipGraphLaunch(s->exec, s->stream));
+  int left = n_steps;
+  for (; left >= kStepsPerRun; left -= kStepsPerRun) CQ_HIP(hipGraphLaunch(s->exec_run, s->stream));
+  for (; left > 0; --left) CQ_HIP(hipGraphLaunch(s->exec, s->stream));
   CQ_HIP(hipEventRecord(s->ev1, s->stream));
   if (tokens_out)
     CQ_HIP(hipMemcpyAsync(tokens_out, s->tokens_dev, (size_t)n_steps * sizeof(int), hipMemcpyDeviceToHost, s->stream));
