@@ -109,6 +109,31 @@ def test_decode_tiny_matches_oracle(tmp_path, quant):
     w.free()
 
 
+@pytest.mark.parametrize("quant", [1, 2])
+def test_chained_decode_run_boundaries_match_forward(quant):
+    """cq_decode replays a graph of several recorded steps plus single steps
+    for the remainder; across those boundaries it reproduces the host-driven
+    chain (one cq_forward per token, the generated ids appended to the
+    penalty history) token for token."""
+    cfg = tiny_config(quant)
+    w = cq.synth_weights(cfg, 7)
+    hist0, tok0, pos0 = [3, 9, 3], 17, 40
+    ref_state = cq.State(cfg, w)
+    ref_state.forward(tok0, pos0 - 1, [])   # same cache contents before pos0 in every state below
+    ref, tok = [], tok0
+    for i in range(25):
+        tok = ref_state.forward(tok, pos0 + i, hist0 + ref)
+        ref.append(tok)
+    ref_state.free()
+    for n in (1, 7, 8, 9, 16, 17, 25):
+        st = cq.State(cfg, w)
+        st.forward(tok0, pos0 - 1, [])
+        out = st.decode(tok0, pos0, n, history=hist0)
+        assert list(out) == ref[:n], n
+        st.free()
+    w.free()
+
+
 @pytest.mark.parametrize("quant", ["int4", "fp16"])
 def test_converted_checkpoint_decodes_like_oracle(tmp_path, quant):
     """A HuggingFace-layout checkpoint through the offline converter (random
