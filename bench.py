@@ -41,6 +41,8 @@ def parse():
     ap.add_argument("--configs", action="store_true",
                     help="also measure decode (and prefill) at every BASELINE config (adds about a minute)")
     ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--attention-compare", action="store_true",
+                    help="also time the MFMA tiled decode attention against the VALU head-major one at 7B, T=32768")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a 256 MiB device-to-device copy (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     return ap.parse_args()
@@ -118,6 +120,45 @@ def floors_leg(cq, kernels):
         out.append(leg)
         log(f"[bench] floor {leg}")
     return out
+
+
+def attention_compare_leg(cq, np):
+    """The engine's decode attention (MFMA-tiled cache, cq_gqa_attention_decode)
+    against the reference-layout compatibility path (head-major cache, VALU,
+    cq_gqa_attention_decode_hm) at Qwen2.5-7B shapes, position 32767, over 8
+    layer caches (537 MB > the 256 MB last-level cache), 3 rounds each.
+    Wall-clock per call includes the launches (no graph); rocprofv3's kernel
+    trace of this leg gives the kernel durations."""
+    H, KV, hd, ms, lay = 28, 4, 128, 32768, 8
+    nbytes = KV * ms * hd * 2
+    rng = np.random.default_rng(0)
+    q = cq.DeviceBuffer.from_array((rng.standard_normal(H * hd) * 0.1).astype(np.float16))
+    out = cq.DeviceBuffer(H * hd * 2)
+    dpos = cq.DeviceBuffer.from_array(np.array([ms - 1], dtype=np.int32))
+    ks = [cq.DeviceBuffer(nbytes) for _ in range(lay)]
+    vs = [cq.DeviceBuffer(nbytes) for _ in range(lay)]
+    for b in ks + vs:
+        b.zero()
+    ws = cq.DeviceBuffer(cq.lib.cq_attention_workspace_bytes(H, KV, hd))
+    po, pm, psum = cq.DeviceBuffer(KV * 16 * 64 * hd * 4), cq.DeviceBuffer(KV * 16 * 64 * 4), cq.DeviceBuffer(KV * 16 * 64 * 4)
+    tiled = lambda l: cq.lib.cq_gqa_attention_decode(q.ptr, ks[l].ptr, vs[l].ptr, out.ptr, dpos.ptr, H, KV, hd, ms,
+                                                      ws.ptr, None)
+    headmajor = lambda l: cq.lib.cq_gqa_attention_decode_hm(q.ptr, ks[l].ptr, vs[l].ptr, out.ptr, dpos.ptr, H, KV, hd,
+                                                             ms, po.ptr, pm.ptr, psum.ptr, None)
+    res = {"shape": "H=28 KV=4 hd=128 T=32768", "bytes": 2 * nbytes}
+    for name, f in (("mfma_tiled", tiled), ("valu_head_major", headmajor)):
+        for l in range(lay):
+            cq.check(f(l))   # warm-up
+        cq.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(3):
+            for l in range(lay):
+                cq.check(f(l))
+        cq.synchronize()
+        res[name + "_us_per_call_wall"] = round((time.perf_counter() - t0) * 1e6 / (3 * lay), 2)
+    for b in [q, out, dpos, ws, po, pm, psum] + ks + vs:
+        b.free()
+    return res
 
 
 def prefill_leg(cq, cfg, st, n):
@@ -401,6 +442,10 @@ def main():
         dst.free()
 
     legs = config_legs(cq) if args.configs else None
+    attn_cmp = None
+    if args.attention_compare:
+        attn_cmp = attention_compare_leg(cq, np)
+        log(f"[bench] attention compare: {attn_cmp}")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -421,6 +466,8 @@ def main():
         "roofline": roof, "cpu_baseline": cpu, "kernels": kernels, "floors": floors, "gemv_config1": g1, "prefill": pf, "kv_int8": kv8, "kv_fp8": kvf8,
         "configs": legs,
     }
+    if attn_cmp is not None:
+        res["attention_compare"] = attn_cmp
     print(json.dumps(res), flush=True)
 
 
