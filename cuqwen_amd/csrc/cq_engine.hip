@@ -167,6 +167,7 @@ struct cq_state {
   uint32_t* stamp = nullptr;
   double* rope_inv_freq = nullptr;   // [head_dim/2]
   int* host_pinned = nullptr;     // staging for the per-step control words
+  uint32_t epoch = 1u;            // penalty epoch of the last set_ctl
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
   hipGraph_t graph_run = nullptr;       // kStepsPerRun chained steps (cq_decode)
@@ -269,10 +270,10 @@ GemvArgs lm_head_gemv(const cq_state* s) {
 //   per layer: RMSNorm+QKV+bias+RoPE+KV store | attention | O-proj+residual |
 //              RMSNorm+gate/up+SwiGLU | down+residual
 //   final RMSNorm+lm_head+penalty | argmax (+ on-device step chaining)
-int step_body(cq_state* s) {
+int step_body(cq_state* s, bool begin = true) {
   const cq_config& c = s->cfg;
   hipStream_t st = s->stream;
-  CQ_TRY(launch_step_begin(s->w->embed, s->ctl, s->history, s->stamp, s->x, c.dim, c.vocab_size, st));
+  if (begin) CQ_TRY(launch_step_begin(s->w->embed, s->ctl, s->history, s->stamp, s->x, c.dim, c.vocab_size, st));
   for (int l = 0; l < c.n_layers; ++l) {
     GemvArgs qkv, o, m1, m2;
     layer_gemvs(s, l, &qkv, &o, &m1, &m2);
@@ -285,7 +286,9 @@ int step_body(cq_state* s) {
   GemvArgs lm = lm_head_gemv(s);
   lm.argmax_out = s->argmax_ws;   // one key per wave, reduced below
   CQ_TRY(launch_gemv(lm, st));
-  CQ_TRY(launch_argmax_reduce(s->argmax_ws, kArgmaxPartials, s->ctl, nullptr, s->history, s->tokens_dev, st));
+  StepBegin next;   // in a chained decode: the next step's embedding row and its new stamp
+  next.embed = s->w->embed; next.x = s->x; next.dim = c.dim; next.stamp = s->stamp;
+  CQ_TRY(launch_argmax_reduce(s->argmax_ws, kArgmaxPartials, s->ctl, nullptr, s->history, s->tokens_dev, st, next));
   return CQ_OK;
 }
 
@@ -298,7 +301,8 @@ int ensure_run_graph(cq_state* s) {
   if (!s->w) return fail(CQ_EINVAL, "no weights bound to the state (pass them to cq_forward_ex)");
   CQ_HIP(hipStreamBeginCapture(s->stream, hipStreamCaptureModeThreadLocal));
   int rc = CQ_OK;
-  for (int i = 0; i < kStepsPerRun && rc == CQ_OK; ++i) rc = step_body(s);
+  // steps after the first take their prologue from the previous step's argmax
+  for (int i = 0; i < kStepsPerRun && rc == CQ_OK; ++i) rc = step_body(s, i == 0);
   hipGraph_t g = nullptr;
   const hipError_t e = hipStreamEndCapture(s->stream, &g);
   if (rc != CQ_OK) {
@@ -328,13 +332,16 @@ int ensure_graph(cq_state* s) {
   return CQ_OK;
 }
 
-// Writes the host-owned control words (token, pos, history_len, chain, step).
+// Writes the control words: token, pos, history_len, chain, step, and a new
+// penalty epoch for the new history (stamps of earlier calls never match it).
 int set_ctl(cq_state* s, int token, int pos, const int32_t* history, int history_len, int chain,
             hipStream_t st = nullptr) {
   if (!st) st = s->stream;
-  int* h = s->host_pinned;
-  h[0] = token; h[1] = pos; h[2] = history_len; h[3] = chain; h[4] = 0;
-  CQ_HIP(hipMemcpyAsync(s->ctl, h, 5 * sizeof(int), hipMemcpyHostToDevice, st));
+  if (++s->epoch == 0u) s->epoch = 1u;   // stamps start at 0
+  StepCtl* h = reinterpret_cast<StepCtl*>(s->host_pinned);
+  h->token = token; h->pos = pos; h->history_len = history_len; h->chain = chain; h->step = 0;
+  h->sampled = -1; h->max_history = s->cfg.max_seq_len; h->epoch = s->epoch;
+  CQ_HIP(hipMemcpyAsync(s->ctl, h, sizeof(StepCtl), hipMemcpyHostToDevice, st));
   if (history_len > 0) {
     CQ_HIP(hipMemcpyAsync(s->history, history, (size_t)history_len * sizeof(int), hipMemcpyHostToDevice, st));
   }

@@ -152,7 +152,7 @@ int launch_penalty_apply(__half* logits, const uint32_t* stamp, const uint32_t* 
 
 // Decode-step control block in device memory.
 struct StepCtl {
-  // written by the host before a step / a chained decode (first 5 ints)
+  // written by the host before a step / a chained decode (all 8 words)
   int token;        // input token of the next step
   int pos;          // position of the next step
   int history_len;  // ids in the history buffer
@@ -161,7 +161,7 @@ struct StepCtl {
   // maintained on the device
   int sampled;      // id sampled by the last step
   int max_history;  // history buffer capacity
-  uint32_t epoch;   // penalty stamp epoch of the current step
+  uint32_t epoch;   // penalty stamp epoch, set by the host with each new history
 };
 
 // Argmax over fp16 logits (ties -> lowest index).  `partials` holds
@@ -170,9 +170,18 @@ struct StepCtl {
 // ctl->step.
 constexpr int kArgmaxBlocks = 256;
 constexpr int kArgmaxPartials = 4096;   // keys written by the lm_head GEMV (one per wave)
+// Work of the next chained step's prologue folded into the argmax reduce:
+// when ctl->chain, the sampled id's embedding row goes to x and its penalty
+// stamp gets the current epoch.  All null: no prologue work.
+struct StepBegin {
+  const __half* embed = nullptr;
+  __half* x = nullptr;
+  int dim = 0;
+  uint32_t* stamp = nullptr;
+};
 // Reduces n argmax keys and does the step bookkeeping of launch_argmax.
 int launch_argmax_reduce(const unsigned long long* partials, int n, StepCtl* ctl, int* d_token_out, int* history,
-                         int* tokens_out, hipStream_t stream);
+                         int* tokens_out, hipStream_t stream, StepBegin next = StepBegin());
 int launch_argmax(const __half* logits, int vocab, unsigned long long* partials, StepCtl* ctl,
                   int* d_token_out, int* history, int* tokens_out, hipStream_t stream);
 

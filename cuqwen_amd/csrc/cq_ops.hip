@@ -159,8 +159,9 @@ __global__ __launch_bounds__(256) void argmax_stage1(const _Float16* logits, int
 constexpr int kArgmaxReduceThreads = 1024;
 __global__ __launch_bounds__(kArgmaxReduceThreads) void argmax_stage2(const unsigned long long* partials, int n,
                                                                      StepCtl* ctl, int* d_token_out, int* history,
-                                                                     int* tokens_out) {
+                                                                     int* tokens_out, StepBegin next) {
   __shared__ unsigned long long red[16];
+  __shared__ int next_token;
   unsigned long long v = 0ull;
   for (int i = threadIdx.x; i < n; i += kArgmaxReduceThreads) v = partials[i] > v ? partials[i] : v;
   const unsigned long long b = block_max_u64(v, red);
@@ -171,24 +172,38 @@ __global__ __launch_bounds__(kArgmaxReduceThreads) void argmax_stage2(const unsi
       ctl->sampled = token;
       if (tokens_out) tokens_out[ctl->step] = token;
       ctl->step += 1;
-      ctl->epoch += 1u;
+      int chained = -1;
       if (ctl->chain) {
         ctl->token = token;
         ctl->pos += 1;
         if (ctl->history_len < ctl->max_history) {
           history[ctl->history_len] = token;
           ctl->history_len += 1;
+          // the history only grows within a chained decode, so the epoch
+          // stays and only the appended id needs its stamp
+          if (next.stamp) next.stamp[token] = ctl->epoch;
         }
+        chained = token;
       }
+      next_token = chained;
     }
   }
+  if (!next.x) return;
+  __syncthreads();
+  // the next chained step's embedding row, so that it needs no step_begin
+  const int t = next_token;
+  if (t < 0) return;
+  const int vec_dim = next.dim / 8;
+  const u4_t* row = reinterpret_cast<const u4_t*>(next.embed) + (int64_t)t * vec_dim;
+  for (int i = threadIdx.x; i < vec_dim; i += kArgmaxReduceThreads) reinterpret_cast<u4_t*>(next.x)[i] = row[i];
 }
 
 int launch_argmax_reduce(const unsigned long long* partials, int n, StepCtl* ctl, int* d_token_out, int* history,
-                         int* tokens_out, hipStream_t stream) {
+                         int* tokens_out, hipStream_t stream, StepBegin next) {
   if (!partials || n <= 0) return fail(CQ_EINVAL, "argmax: bad arguments");
+  if (next.x && (!ctl || !next.embed || next.dim <= 0 || next.dim % 8)) return fail(CQ_EINVAL, "argmax: bad step-begin arguments");
   hipLaunchKernelGGL(argmax_stage2, dim3(1), dim3(kArgmaxReduceThreads), 0, stream, partials, n, ctl, d_token_out,
-                     history, tokens_out);
+                     history, tokens_out, next);
   CQ_HIP(hipGetLastError());
   return CQ_OK;
 }
@@ -203,7 +218,8 @@ int launch_argmax(const __half* logits, int vocab, unsigned long long* partials,
 
 // ------------------------------------------------------------ step begin
 // Embedding of ctl->token into x (block 0) and history stamping with the
-// step's epoch (all blocks).
+// step's epoch (all blocks).  The epoch is set by the host with each new
+// history (a fresh value per call), so stale stamps never match.
 __global__ __launch_bounds__(256) void step_begin_kernel(const u4_t* embed, const StepCtl* ctl, const int* history,
                                                          uint32_t* stamp, u4_t* x, int vec_dim, int vocab) {
   const int token = ctl->token;
