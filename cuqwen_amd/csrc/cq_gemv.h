@@ -259,7 +259,7 @@ __device__ __forceinline__ float stage_finish(const GemvArgs& a, XStage<Q, NORM,
 
 // Rows handled by one wave unit.
 template <int MODE, int R>
-__device__ __forceinline__ int units_total(const GemvArgs& a) {
+__host__ __device__ __forceinline__ int units_total(const GemvArgs& a) {
   if constexpr (MODE == GM_SWIGLU) return (a.N + R / 2 - 1) / (R / 2);
   else if constexpr (MODE == GM_QKV) return (a.n_heads + 2 * a.n_kv) * (a.head_dim / 2) / (R / 2);
   else return (a.N + R - 1) / R;

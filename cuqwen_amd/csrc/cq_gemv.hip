@@ -206,10 +206,7 @@ int launch_variant(const GemvArgs& a, hipStream_t stream, int max_blocks) {
   using T = QTraits<Q>;
   const int NC = a.K / T::EPC;
   const size_t lds = (size_t)T::PLANES * NC * 16 + (Q != CQ_QUANT_FP16 ? (size_t)NC * 4 : 0);
-  int units;
-  if (MODE == GM_SWIGLU) units = (a.N + R / 2 - 1) / (R / 2);
-  else if (MODE == GM_QKV) units = (a.n_heads + 2 * a.n_kv) * (a.head_dim / 2) / (R / 2);
-  else units = (a.N + R - 1) / R;
+  const int units = units_total<MODE, R>(a);
   // persistent grid: up to max_blocks blocks, each owning a contiguous range
   // of at least one unit per wave
   const int blocks = std::max(1, std::min(max_blocks, (units + kWavesPerBlock - 1) / kWavesPerBlock));
@@ -256,6 +253,19 @@ static int launch_q(const GemvArgs& a, hipStream_t stream) {
       return launch_variant<Q, MODE, TN::R, 1, false, true, TN::BLK>(a, stream, TN::PER_CU * kNumCUs);
     }
     return launch_t<Q, MODE, false, true>(a, stream);
+  } else if constexpr (MODE == GM_QKV) {
+    // Equal work per CU: when the rotation-pair units split evenly over the
+    // CUs (7B: 2304 = 9 per CU, 14B: 3584 = 14), one block per CU with one
+    // wave per unit.  The default 4 x 256-thread blocks per CU would give
+    // 576 blocks for 7B, i.e. CUs with 2 and with 3 blocks, and the launch
+    // would last as long as the CUs with 3.
+    using TN = GemvTune<MODE>;
+    const int units = units_total<MODE, TN::R>(a);
+    if (norm && units % kNumCUs == 0) {
+      if (units / kNumCUs == 9) return launch_variant<Q, MODE, TN::R, TN::U, true, true, 9 * kWave>(a, stream, kNumCUs);
+      if (units / kNumCUs == 14) return launch_variant<Q, MODE, TN::R, TN::U, true, true, 14 * kWave>(a, stream, kNumCUs);
+    }
+    return norm ? launch_t<Q, MODE, true, true>(a, stream) : launch_t<Q, MODE, false, true>(a, stream);
   } else {
     return norm ? launch_t<Q, MODE, true, true>(a, stream) : launch_t<Q, MODE, false, true>(a, stream);
   }
