@@ -13,7 +13,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libcuqwen.so")
-SOURCES = ["cq_format.cpp", "cq_tokenizer.cpp", "cq_gemv.hip", "cq_attention.hip", "cq_attention_hm.hip", "cq_prefill.hip", "cq_ops.hip", "cq_engine.hip", "cq_capi.hip", "cq_noalloc.hip"]
+SOURCES = ["cq_format.cpp", "cq_tokenizer.cpp", "cq_gemv.hip", "cq_attention.hip", "cq_attention_hm.hip", "cq_omerge.hip", "cq_prefill.hip", "cq_ops.hip", "cq_engine.hip", "cq_capi.hip", "cq_noalloc.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = os.environ.get("CQ_OFFLOAD_ARCH", "gfx950")

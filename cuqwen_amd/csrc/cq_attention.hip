@@ -238,7 +238,7 @@ __global__ __launch_bounds__(kWave) void attention_stage2(const AttnArgs a, int 
     if (lane == i) out[i] = (_Float16)(O[i] * inv);
 }
 
-int launch_attention(const AttnArgs& a, hipStream_t stream) {
+static int attention_check(const AttnArgs& a) {
   if (a.head_dim != 64 && a.head_dim != 128) return fail(CQ_EINVAL, "attention: head_dim must be 64 or 128");
   if (a.n_kv <= 0 || a.n_heads % a.n_kv || a.n_heads / a.n_kv > 16 || a.n_kv > 64)
     return fail(CQ_EINVAL, "attention: need n_heads/n_kv_heads <= 16 and n_kv_heads <= 64");
@@ -248,6 +248,12 @@ int launch_attention(const AttnArgs& a, hipStream_t stream) {
   if (kv8 && a.kv_fmt != CQ_KV_INT8 && a.kv_fmt != CQ_KV_FP8) return fail(CQ_EINVAL, "attention: unknown KV code format");
   if (kv8 ? (!a.vcache8 || !a.kscale || !a.vscale || !a.k_new || !a.v_new) : (!a.kcache || !a.vcache))
     return fail(CQ_EINVAL, "attention: null cache pointer");
+  return CQ_OK;
+}
+
+int launch_attention_stage1(const AttnArgs& a, hipStream_t stream) {
+  CQ_TRY(attention_check(a));
+  const bool kv8 = a.kcache8 != nullptr;
   const int P = attention_max_parts(a.n_kv);
   const dim3 grid(P, a.n_kv);
   if (kv8 && a.kv_fmt == CQ_KV_FP8) {
@@ -260,6 +266,13 @@ int launch_attention(const AttnArgs& a, hipStream_t stream) {
     if (a.head_dim == 128) hipLaunchKernelGGL(attention_stage1<128>, grid, dim3(kAttnThreads), 0, stream, a);
     else hipLaunchKernelGGL(attention_stage1<64>, grid, dim3(kAttnThreads), 0, stream, a);
   }
+  CQ_HIP(hipGetLastError());
+  return CQ_OK;
+}
+
+int launch_attention(const AttnArgs& a, hipStream_t stream) {
+  CQ_TRY(launch_attention_stage1(a, stream));
+  const int P = attention_max_parts(a.n_kv);
   if (a.head_dim == 128)
     hipLaunchKernelGGL(attention_stage2<128>, dim3(a.n_heads * (128 / kMergeDims)), dim3(kWave), 0, stream, a, P);
   else

@@ -86,6 +86,24 @@ int weights_layout(cq_weights* w) {
   return CQ_OK;
 }
 
+// The O-projections into the 128-column panel layout the decode's merged
+// O-projection streams contiguously (wo_to_panels); done once, after the
+// weights are in the arena, whatever filled it.
+int weights_panelize(cq_weights* w) {
+  const cq_config& c = w->cfg;
+  const int qd = c.n_heads * c.head_dim;
+  const int epc = c.quant_type == CQ_QUANT_INT4 ? 32 : c.quant_type == CQ_QUANT_INT8 ? 16 : 8;
+  void* tmp = nullptr;
+  if (hipMalloc(&tmp, (size_t)c.dim * (qd / epc) * 16) != hipSuccess) return fail(CQ_ENOMEM, "weights: panel staging allocation failed");
+  int rc = CQ_OK;
+  for (int l = 0; l < c.n_layers && rc == CQ_OK; ++l)
+    rc = wo_to_panels(c.quant_type, w->layers[l].wo, w->layers[l].so, c.dim, qd, tmp, nullptr);
+  const hipError_t e = hipStreamSynchronize(nullptr);
+  hipFree(tmp);
+  if (rc == CQ_OK && e != hipSuccess) rc = fail(CQ_EHIP, std::string("weights: panel conversion: ") + hipGetErrorString(e));
+  return rc;
+}
+
 // ------------------------------------------------------ on-device synthesis
 __global__ void synth_half_kernel(uint16_t* out, int64_t n, uint64_t seed, uint64_t stream, float mul, float mean) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
@@ -160,6 +178,8 @@ struct cq_state {
   int kv_dtype = CQ_KV_FP16;        // CQ_KV_INT8 / CQ_KV_FP8: kcache / vcache hold 1-byte codes, scales below
   float *kscale = nullptr, *vscale = nullptr;   // [layer][kv_head][max_seq] (quantized cache)
   void* attn_ws = nullptr;
+  long long* oacc = nullptr;   // [dim] O-projection sum, 64-bit fixed point (2^-32), zero between layers
+  __half* xh = nullptr;        // [dim] residual stream after the attention block (h)
   unsigned long long* argmax_ws = nullptr;
   StepCtl* ctl = nullptr;
   int* history = nullptr;
@@ -187,7 +207,7 @@ struct cq_state {
 
 namespace {
 
-int layer_gemvs(const cq_state* s, int l, GemvArgs* qkv, GemvArgs* o, GemvArgs* mlp1, GemvArgs* mlp2) {
+int layer_gemvs(const cq_state* s, int l, GemvArgs* qkv, GemvArgs* mlp1, GemvArgs* mlp2) {
   const cq_config& c = s->cfg;
   const LayerW& L = s->w->layers[l];
   const int qd = c.n_heads * c.head_dim;
@@ -206,12 +226,6 @@ int layer_gemvs(const cq_state* s, int l, GemvArgs* qkv, GemvArgs* o, GemvArgs* 
     a.rope_theta = c.rope_theta; a.rope_inv_freq = s->rope_inv_freq;
     a.kcache = kc; a.vcache = vc; a.max_seq = c.max_seq_len;
     *qkv = a;
-  }
-  if (o) {
-    GemvArgs a;
-    a.mode = GM_RESID; a.quant = c.quant_type; a.x = s->xb; a.K = qd; a.N = c.dim;
-    a.W[0] = L.wo; a.S[0] = L.so; a.out[0] = s->x;
-    *o = a;
   }
   if (mlp1) {
     GemvArgs a;
@@ -265,24 +279,49 @@ GemvArgs lm_head_gemv(const cq_state* s) {
   return a;
 }
 
+// The layer's O-projection as one launch with the attention merge
+// (cq_omerge.hip): the head contributions go to s->oacc.
+OMergeArgs layer_omerge(const cq_state* s, int l) {
+  const cq_config& c = s->cfg;
+  OMergeArgs a;
+  a.workspace = s->attn_ws; a.attn = s->xb;
+  a.W = s->w->layers[l].wo; a.S = s->w->layers[l].so; a.acc = s->oacc; a.d_pos = &s->ctl->pos;
+  a.quant = c.quant_type; a.n_heads = c.n_heads; a.n_kv = c.n_kv_heads; a.head_dim = c.head_dim;
+  a.K = c.n_heads * c.head_dim; a.N = c.dim; a.Pmax = attention_max_parts(c.n_kv_heads);
+  return a;
+}
+
+// The MLP GEMVs of the fused step: gate/up first forms h = half(x + oacc)
+// (also into s->xh), down adds to h and clears oacc for the next layer.
+void fused_mlp(const cq_state* s, GemvArgs* m1, GemvArgs* m2) {
+  m1->x_acc = s->oacc; m1->x_out = s->xh;
+  m2->resid = s->xh; m2->zero = s->oacc; m2->zero_n = s->cfg.dim;
+}
+
+// One decoder layer of the step (src/model.cu:96-176) in 5 launches:
+// RMSNorm+QKV+bias+RoPE+KV store | attention stage 1 | merge+O-proj |
+// h = x + O, RMSNorm+gate/up+SwiGLU | down + residual.
+int layer_step(cq_state* s, int l, hipStream_t st) {
+  GemvArgs qkv, m1, m2;
+  layer_gemvs(s, l, &qkv, &m1, &m2);
+  fused_mlp(s, &m1, &m2);
+  CQ_TRY(launch_gemv(qkv, st));
+  CQ_TRY(launch_attention_stage1(layer_attn(s, l), st));
+  CQ_TRY(launch_omerge(layer_omerge(s, l), st));
+  CQ_TRY(launch_gemv(m1, st));
+  CQ_TRY(launch_gemv(m2, st));
+  return CQ_OK;
+}
+
 // The decode step (src/model.cu:76-181), 5 launches per layer + 3:
 //   step_begin (embedding + penalty stamps)
-//   per layer: RMSNorm+QKV+bias+RoPE+KV store | attention | O-proj+residual |
-//              RMSNorm+gate/up+SwiGLU | down+residual
+//   per layer: layer_step (5 launches)
 //   final RMSNorm+lm_head+penalty | argmax (+ on-device step chaining)
 int step_body(cq_state* s, bool begin = true) {
   const cq_config& c = s->cfg;
   hipStream_t st = s->stream;
   if (begin) CQ_TRY(launch_step_begin(s->w->embed, s->ctl, s->history, s->stamp, s->x, c.dim, c.vocab_size, st));
-  for (int l = 0; l < c.n_layers; ++l) {
-    GemvArgs qkv, o, m1, m2;
-    layer_gemvs(s, l, &qkv, &o, &m1, &m2);
-    CQ_TRY(launch_gemv(qkv, st));
-    CQ_TRY(launch_attention(layer_attn(s, l), st));
-    CQ_TRY(launch_gemv(o, st));
-    CQ_TRY(launch_gemv(m1, st));
-    CQ_TRY(launch_gemv(m2, st));
-  }
+  for (int l = 0; l < c.n_layers; ++l) CQ_TRY(layer_step(s, l, st));
   GemvArgs lm = lm_head_gemv(s);
   lm.argmax_out = s->argmax_ws;   // one key per wave, reduced below
   CQ_TRY(launch_gemv(lm, st));
@@ -501,6 +540,7 @@ extern "C" int cq_load_weights(const char* path, const cq_config* expect, cq_con
   }
   std::fclose(f);
   hipHostFree(staging);
+  if (rc == CQ_OK) rc = weights_panelize(w.get());
   if (rc != CQ_OK) {
     hipFree(w->arena);
     return rc;
@@ -516,7 +556,8 @@ extern "C" int cq_synth_weights(const cq_config* cfg, uint64_t seed, cq_weights*
   std::unique_ptr<cq_weights> w(new cq_weights);
   w->cfg = *cfg;
   CQ_TRY(weights_layout(w.get()));
-  const int rc = synth_device(w.get(), seed);
+  int rc = synth_device(w.get(), seed);
+  if (rc == CQ_OK) rc = weights_panelize(w.get());
   if (rc != CQ_OK) {
     hipFree(w->arena);
     return rc;
@@ -591,7 +632,8 @@ extern "C" int cq_state_create_kv(const cq_config* cfg, const cq_weights* w, int
                o_ctl = take(sizeof(StepCtl)), o_hist = take((size_t)c.max_seq_len * 4),
                o_tok = take((size_t)c.max_seq_len * 4), o_stamp = take((size_t)c.vocab_size * 4),
                o_attn = take(attention_workspace_bytes(c.n_heads, c.n_kv_heads, c.head_dim)),
-               o_arg = take(kArgmaxPartials * 8 + 64), o_rope = take((size_t)c.head_dim / 2 * sizeof(double));
+               o_arg = take(kArgmaxPartials * 8 + 64), o_rope = take((size_t)c.head_dim / 2 * sizeof(double)),
+               o_oacc = take(d * 8), o_xh = take(d * 2);
   const size_t small = off;
   const size_t o_kc = take(kv_bytes), o_vc = take(kv_bytes), o_ks = take(sc_bytes), o_vs = take(sc_bytes);
   if (hipMalloc(&s->arena, off) != hipSuccess) return fail(CQ_ENOMEM, "state_create: device allocation failed");
@@ -603,6 +645,8 @@ extern "C" int cq_state_create_kv(const cq_config* cfg, const cq_weights* w, int
   s->kcache = (__half*)(a + o_kc); s->vcache = (__half*)(a + o_vc);
   if (sc_bytes) { s->kscale = (float*)(a + o_ks); s->vscale = (float*)(a + o_vs); }
   s->rope_inv_freq = (double*)(a + o_rope);
+  s->oacc = (long long*)(a + o_oacc);   // zeroed with the rest of the small region
+  s->xh = (__half*)(a + o_xh);
   int rc = CQ_OK;
   auto chk = [&](hipError_t e, const char* what) {
     if (e != hipSuccess && rc == CQ_OK) rc = fail(CQ_EHIP, std::string("state_create: ") + what + ": " + hipGetErrorString(e));
@@ -861,9 +905,12 @@ int prefill_tail(cq_state* s, int M) {
   const int d = c.dim, qd = c.n_heads * c.head_dim;
   CQ_HIP(hipMemcpyAsync(s->x, s->pf_x + (size_t)(M - 1) * d, (size_t)d * 2, hipMemcpyDeviceToDevice, st));
   CQ_TRY(launch_pf_row_natural(s->pf_ao + (size_t)(M - 1) * qd, s->xb, qd, c.quant_type, st));
-  GemvArgs o, m1, m2;
-  layer_gemvs(s, c.n_layers - 1, nullptr, &o, &m1, &m2);
-  CQ_TRY(launch_gemv(o, st));
+  GemvArgs m1, m2;
+  layer_gemvs(s, c.n_layers - 1, nullptr, &m1, &m2);
+  fused_mlp(s, &m1, &m2);
+  OMergeArgs o = layer_omerge(s, c.n_layers - 1);
+  o.direct = true;   // xb holds the token's attention output
+  CQ_TRY(launch_omerge(o, st));
   CQ_TRY(launch_gemv(m1, st));
   CQ_TRY(launch_gemv(m2, st));
   GemvArgs lm = lm_head_gemv(s);
@@ -926,7 +973,7 @@ int prefill_batched(cq_state* s, const int32_t* tokens, int n, int pos0) {
       }
       PfGemmArgs o;
       o.mode = GM_RESID; o.quant = c.quant_type; o.A = (const _Float16*)s->pf_ao; o.M = M; o.N = d; o.K = qd;
-      o.W[0] = L.wo; o.S[0] = (const _Float16*)L.so; o.rows[0] = d; o.out = (_Float16*)s->pf_x;
+      o.W[0] = L.wo; o.S[0] = (const _Float16*)L.so; o.panels = true; o.rows[0] = d; o.out = (_Float16*)s->pf_x;
       o.part = s->pf_part; o.part_bytes = kPrefillPartBytes;
       o.norm_w = (const _Float16*)L.post_norm; o.norm_eps = c.norm_eps;
       o.norm_out = (_Float16*)s->pf_a; o.norm_inv = s->pf_inv;
@@ -1011,9 +1058,9 @@ extern "C" int cq_state_profile(cq_state* s, int32_t pos, int32_t iters, int32_t
   // bytes: weights + scales + activations in/out (+ bias, residual)
   const K ks[] = {
       {"qkv_rope_kvstore", wbytes(qt, qd + 2 * kvd, d) + 2 * d * 2 + 2 * (qd + 2 * kvd) * 2, 0},
-      {"attention", 2.0 * c.n_kv_heads * T * c.head_dim * 2 + 2 * qd * 2, 1},
-      {"o_proj_residual", wbytes(qt, d, qd) + 2 * qd + 2 * d * 2, 2},
-      {"gate_up_swiglu", wbytes(qt, 2 * I, d) + 2 * d * 2 + 2 * I, 3},
+      {"attention_stage1", 2.0 * c.n_kv_heads * T * c.head_dim * 2 + 2 * qd * 2, 1},
+      {"merge_o_proj", wbytes(qt, d, qd) + 8 * d * (double)c.n_heads, 2},
+      {"gate_up_swiglu", wbytes(qt, 2 * I, d) + 2 * d * 2 + 8 * d + 2 * I, 3},
       {"down_residual", wbytes(qt, d, I) + 2 * I + 2 * d * 2, 4},
       {"lm_head", wbytes(lmq, V, d) + 2 * d * 2 + 2 * V, 5},
       {"argmax", 8.0 * kArgmaxPartials, 6},   // the lm_head GEMV already reduced the logits to one key per wave
@@ -1026,12 +1073,13 @@ extern "C" int cq_state_profile(cq_state* s, int32_t pos, int32_t iters, int32_t
     const int reps = per_layer ? c.n_layers : 1;
     auto run = [&]() -> int {
       for (int l = 0; l < reps; ++l) {
-        GemvArgs qkv, o, m1, m2;
-        layer_gemvs(s, l, &qkv, &o, &m1, &m2);
+        GemvArgs qkv, m1, m2;
+        layer_gemvs(s, l, &qkv, &m1, &m2);
+        fused_mlp(s, &m1, &m2);
         switch (k.kind) {
           case 0: CQ_TRY(launch_gemv(qkv, s->stream)); break;
-          case 1: CQ_TRY(launch_attention(layer_attn(s, l), s->stream)); break;
-          case 2: CQ_TRY(launch_gemv(o, s->stream)); break;
+          case 1: CQ_TRY(launch_attention_stage1(layer_attn(s, l), s->stream)); break;
+          case 2: CQ_TRY(launch_omerge(layer_omerge(s, l), s->stream)); break;
           case 3: CQ_TRY(launch_gemv(m1, s->stream)); break;
           case 4: CQ_TRY(launch_gemv(m2, s->stream)); break;
           case 5: {

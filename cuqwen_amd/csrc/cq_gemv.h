@@ -379,7 +379,7 @@ __device__ __forceinline__ EpiPre epi_prefetch(const GemvArgs& a, int unit, int 
   if constexpr (MODE == GM_STORE || MODE == GM_RESID) {
     const RowRef me = row_of<MODE, R>(a, unit, min(lane, R - 1));
     if constexpr (MODE == GM_RESID) {
-      e.a = ld_u16(reinterpret_cast<const _Float16*>(a.out[0]) + me.row);
+      e.a = ld_u16(reinterpret_cast<const _Float16*>(a.resid ? a.resid : a.out[0]) + me.row);
     } else {
       e.a = ld_u16(a.bias[0] ? reinterpret_cast<const _Float16*>(a.bias[0]) + me.row
                              : reinterpret_cast<const _Float16*>(a.x));

@@ -9,6 +9,15 @@
 
 namespace cq {
 
+// Value of a 64-bit fixed-point sum (2^-32 units, |value| < 2^30 by the
+// producer's clamp) from its low and high words: the signed high word
+// converts in one instruction (exactly below 2^24), the low word adds its
+// fraction in one fma.  A full int64 conversion has no instruction and would
+// cost the staging waves tens of instructions per element.
+__device__ __forceinline__ float fix_to_float(uint32_t lo, uint32_t hi) {
+  return fmaf((float)lo, 2.3283064365386963e-10f, (float)(int32_t)hi);
+}
+
 // Persistent GEMV.  Block b owns the contiguous unit range
 // [b*n/G, (b+1)*n/G); inside the block, wave w starts on units begin + w and
 // begin + WPB + w and then claims further units from an LDS counter.  The
@@ -22,8 +31,15 @@ namespace cq {
 // input-vector prologue overlaps them.  The main loop issues loads only for
 // real work, and unconditionally inside its body (clamped chunk indices),
 // keeping the compiler's load counters exact.
-template <int Q, int MODE, int R, int U, bool NORM, bool G128, int BLK>
+//
+// ADD (SWIGLU with the norm fused): x is first replaced by half(x + x_acc *
+// 2^-32), the residual plus the O-projection's fixed-point sum
+// (cq_omerge.hip; rounded as kernels.cu:671 rounds the residual add); the
+// sums ride in the staging registers next to x, and h is written back to
+// x_out, a chunk per block.
+template <int Q, int MODE, int R, int U, bool NORM, bool G128, int BLK, bool ADD = false>
 __global__ __launch_bounds__(BLK) void gemv_kernel(const GemvArgs a) {
+  static_assert(!ADD || (NORM && MODE == GM_SWIGLU), "ADD is the norm-fused SWIGLU prologue");
   using T = QTraits<Q>;
   extern __shared__ u4_t smem[];
   __shared__ float red[BLK / kWave];
@@ -76,6 +92,23 @@ __global__ __launch_bounds__(BLK) void gemv_kernel(const GemvArgs a) {
   __builtin_amdgcn_s_setprio(3);
   XStage<Q, NORM, BLK> st;
   stage_issue<Q, NORM, BLK>(a, st, 0, NC);
+  // ADD: the fixed-point sums of the same elements (8 bytes each, two per
+  // 16-byte load), next to x in the staging registers
+  constexpr int XB = XStage<Q, NORM, BLK>::XB;
+  u4_t xacc[ADD ? XB : 1][ADD ? T::PLANES : 1][4];
+  if constexpr (ADD) {
+#pragma unroll
+    for (int i = 0; i < XB; ++i) {
+      const int c0 = stage_base<Q, NORM, BLK>(0, i);
+      if (c0 < NC) {
+        const int c = min(c0 + lane, NC - 1);
+#pragma unroll
+        for (int p = 0; p < T::PLANES; ++p)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) xacc[i][p][q] = load_u4(a.x_acc + c * T::EPC + p * 8 + 2 * q);
+      }
+    }
+  }
   // the RoPE table rides with the x loads (every thread, clamped index):
   // waiting for a load issued after the weight prefetch would wait for the
   // whole prefetch
@@ -100,7 +133,45 @@ __global__ __launch_bounds__(BLK) void gemv_kernel(const GemvArgs a) {
   load_step<Q, MODE, R, U, G128>(a, B, cb.unit, cb.kb, NC, lane);
   EpiPre pb = epi_prefetch<MODE, R>(a, cb.unit, lane);
   if constexpr (MODE == GM_QKV) inv_freq[min((int)threadIdx.x, a.head_dim / 2 - 1)] = rope_f;   // duplicates write equal values
+  if constexpr (ADD) {
+    // h = half(x + sum): the O-projection sum (fp32) plus the fp16
+    // residual, rounded once
+#pragma unroll
+    for (int i = 0; i < XB; ++i) {
+      if (stage_base<Q, NORM, BLK>(0, i) < NC) {
+#pragma unroll
+        for (int p = 0; p < T::PLANES; ++p) {
+          uint32_t w[4] = {st.x[i][p].x, st.x[i][p].y, st.x[i][p].z, st.x[i][p].w};
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const u4_t s4 = xacc[i][p][q];
+            const float o0 = fix_to_float(s4.x, s4.y);
+            const float o1 = fix_to_float(s4.z, s4.w);
+            const h2_t xv = as_h2(w[q]);
+            h2_t h;
+            h.x = (_Float16)(o0 + (float)xv.x);
+            h.y = (_Float16)(o1 + (float)xv.y);
+            w[q] = as_u32(h);
+          }
+          st.x[i][p] = u4_t{w[0], w[1], w[2], w[3]};
+        }
+      }
+    }
+  }
   const float scale = stage_finish<Q, NORM, BLK>(a, st, NC, xs, sx, red);
+  if constexpr (ADD) {
+    // chunk c of h is written by block c % gridDim.x (after the staging
+    // barrier: a store pending at a barrier could make it wait for the
+    // weight loads too)
+#pragma unroll
+    for (int i = 0; i < XB; ++i) {
+      const int c = stage_base<Q, NORM, BLK>(0, i) + lane;
+      if (c < NC && c % (int)gridDim.x == (int)blockIdx.x) {
+#pragma unroll
+        for (int p = 0; p < T::PLANES; ++p) *reinterpret_cast<u4_t*>(a.x_out + c * T::EPC + p * 8) = st.x[i][p];
+      }
+    }
+  }
 
   const UnpackRegs uk = unpack_regs();
   float acc[R];
@@ -147,6 +218,10 @@ __global__ __launch_bounds__(BLK) void gemv_kernel(const GemvArgs a) {
       }
     }
   }
+  if constexpr (MODE == GM_RESID) {
+    if (a.zero)
+      for (int i = blockIdx.x * BLK + threadIdx.x; i < a.zero_n; i += gridDim.x * BLK) a.zero[i] = 0;
+  }
   if constexpr (MODE == GM_STORE) {
     // every launched wave writes its slot (0 when it stored nothing)
     if (a.argmax_out) {
@@ -186,6 +261,10 @@ int gemv_check(const GemvArgs& a) {
   if (lds > 60 * 1024) return fail(CQ_EINVAL, "gemv: input vector too long for LDS staging");
   if (a.norm_w && a.K > kNormMaxK) return fail(CQ_EINVAL, "gemv: fused RMSNorm supports K <= 16384");
   if (a.argmax_out && a.mode != GM_STORE) return fail(CQ_EINVAL, "gemv: argmax keys need the store mode");
+  if (a.x_acc && (a.mode != GM_SWIGLU || !a.norm_w || !a.x_out))
+    return fail(CQ_EINVAL, "gemv: the accumulator prologue needs swiglu, a fused norm and x_out");
+  if ((a.resid || a.zero) && a.mode != GM_RESID) return fail(CQ_EINVAL, "gemv: resid / zero are residual-mode options");
+  if (a.zero_n < 0 || (a.zero_n > 0 && !a.zero)) return fail(CQ_EINVAL, "gemv: bad zero range");
   return CQ_OK;
 }
 
@@ -200,7 +279,7 @@ template <> struct GemvTune<GM_RESID> { static constexpr int R = 1, U = 2, BLK =
 template <> struct GemvTune<GM_SWIGLU> { static constexpr int R = 2, U = 1, BLK = 1024, PER_CU = 1; };
 template <> struct GemvTune<GM_QKV> { static constexpr int R = 2, U = 1, BLK = 256, PER_CU = 4; };
 
-template <int Q, int MODE, int R, int U, bool NORM, bool G128, int BLK = 256>
+template <int Q, int MODE, int R, int U, bool NORM, bool G128, int BLK = 256, bool ADD = false>
 int launch_variant(const GemvArgs& a, hipStream_t stream, int max_blocks) {
   constexpr int kWavesPerBlock = BLK / kWave;
   using T = QTraits<Q>;
@@ -211,7 +290,7 @@ int launch_variant(const GemvArgs& a, hipStream_t stream, int max_blocks) {
   // of at least one unit per wave
   const int blocks = std::max(1, std::min(max_blocks, (units + kWavesPerBlock - 1) / kWavesPerBlock));
   if (a.argmax_out && blocks * kWavesPerBlock > kArgmaxPartials) return fail(CQ_EINVAL, "gemv: too many waves for the argmax slots");
-  hipLaunchKernelGGL((gemv_kernel<Q, MODE, R, U, NORM, G128, BLK>), dim3(blocks), dim3(BLK), lds, stream, a);
+  hipLaunchKernelGGL((gemv_kernel<Q, MODE, R, U, NORM, G128, BLK, ADD>), dim3(blocks), dim3(BLK), lds, stream, a);
   CQ_HIP(hipGetLastError());
   return CQ_OK;
 }
@@ -267,6 +346,12 @@ static int launch_q(const GemvArgs& a, hipStream_t stream) {
     }
     return norm ? launch_t<Q, MODE, true, true>(a, stream) : launch_t<Q, MODE, false, true>(a, stream);
   } else {
+    if constexpr (MODE == GM_SWIGLU) {
+      if (a.x_acc) {
+        using TN = GemvTune<MODE>;
+        return launch_variant<Q, MODE, TN::R, TN::U, true, true, TN::BLK, true>(a, stream, TN::PER_CU * kNumCUs);
+      }
+    }
     return norm ? launch_t<Q, MODE, true, true>(a, stream) : launch_t<Q, MODE, false, true>(a, stream);
   }
 }

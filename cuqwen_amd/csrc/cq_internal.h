@@ -35,6 +35,16 @@ struct GemvArgs {
   // STORE mode: each wave writes the argmax key of the rows it stored to
   // argmax_out[wave] (at most kArgmaxPartials waves)
   unsigned long long* argmax_out = nullptr;
+  // SWIGLU with the RMSNorm fused, optional: x is first replaced by
+  // half(x + x_acc * 2^-32) (the residual plus the O-projection's
+  // fixed-point sum), and that vector is also written to x_out
+  const long long* x_acc = nullptr;
+  __half* x_out = nullptr;
+  // RESID, optional: residual source (nullptr: out[0]); zero[0..zero_n) is
+  // cleared once every wave has finished its rows
+  const __half* resid = nullptr;
+  long long* zero = nullptr;
+  int zero_n = 0;
 };
 
 // Validates shapes and launches; returns CQ_OK or an error code.
@@ -71,6 +81,33 @@ struct AttnArgs {
 size_t attention_workspace_bytes(int n_heads, int n_kv, int head_dim);
 int launch_attention(const AttnArgs& a, hipStream_t stream);
 int attention_max_parts(int n_kv);
+// Attention stage 1 alone (the partials stay in the workspace, or the output
+// in `out` when one partition covers the context).
+int launch_attention_stage1(const AttnArgs& a, hipStream_t stream);
+
+// Attention merge + O-projection split over heads (cq_omerge.hip): merges
+// the stage-1 partials of each head (or takes the single-partition output
+// from attn) and adds Wo * attention to acc as 64-bit fixed point (2^-32).
+struct OMergeArgs {
+  const void* workspace = nullptr;   // stage-1 partials (attention workspace layout)
+  const __half* attn = nullptr;      // stage 1's output when it used one partition
+  const void* W = nullptr;           // Wo [N][K]
+  const __half* S = nullptr;         // its group-128 scales (quantized)
+  long long* acc = nullptr;          // [N], added to
+  const int* d_pos = nullptr;
+  int quant = CQ_QUANT_FP16;
+  int n_heads = 0, n_kv = 0, head_dim = 0;
+  int K = 0, N = 0;                  // K = n_heads * head_dim
+  int Pmax = 0;                      // partition slots per kv head (stage 1's grid)
+  int bands = 0;                     // set by the launcher
+  bool direct = false;               // attn holds the finished output (no partials)
+};
+int launch_omerge(const OMergeArgs& a, hipStream_t stream);
+// Converts a row-major [N][K] O-projection (and its [N][K/128] scales) in
+// place into K/128 column panels [N][128] (scales [K/128][N]), the layout
+// launch_omerge and the prefill O-projection read; tmp holds N*K weight bytes.
+int wo_to_panels(int quant, void* W, __half* S, int N, int K, void* tmp, hipStream_t stream);
+int omerge_plan(int quant, int head_dim, int n_heads, int N, int* hpb, int* bands, int* rounds);
 // Head-major cache path (cq_attention_hm.hip): the reference's layout and
 // partial buffers (partial index (kv_head * 16 + head) * 64 + partition).
 int launch_attention_hm(const __half* q, const __half* kc, const __half* vc, __half* out, const int* d_pos,
@@ -109,6 +146,7 @@ struct PfGemmArgs {
   float* kscale = nullptr;   // [n_kv][max_seq] of this layer
   float* vscale = nullptr;
   int kv_fmt = CQ_KV_INT8;   // CQ_KV_INT8 / CQ_KV_FP8 codes
+  bool panels = false;       // W[0] / S[0] in 128-column panels (wo_to_panels), not row-major
   // RESID only, optional: RMSNorm of the updated rows (as launch_pf_norm) into
   // norm_out / norm_inv with weight norm_w
   const _Float16* norm_w = nullptr;

@@ -1,0 +1,289 @@
+// Attention merge + O-projection in one launch, split over query heads.
+//
+// Reference: the split-K attention's stage 2 (src/kernels.cu:222-288) and the
+// O-projection gemv_add (kernels.cu:640-687) are two dependent launches.
+// Here block (head h, row band c) merges head h's stage-1 partials itself
+// (the log-sum-exp rule of stage 2, same arithmetic order: one wave per
+// 16-dimension slice, one lane per partition, DPP wave sums, so the fp16
+// attention output is bit-identical to stage 2's), stages it in LDS and
+// multiplies it by the column slice Wo[band rows][h*hd .. (h+1)*hd), which
+// the 128-column panel layout of Wo (wo_to_panels, below) makes one
+// contiguous run of HBM.  The head contributions of an output row
+// are summed in a 64-bit fixed-point accumulator (value * 2^32, one atomic
+// add per row and head; integer adds are associative, so the result does
+// not depend on arrival order and every run is bit-identical).  The next
+// launch (RMSNorm + gate/up) turns accumulator + residual into the fp16
+// residual stream, h = half(residual + sum) as in kernels.cu:671, and the
+// down projection clears the accumulator for the next layer.
+//
+// What this saves is the stage-2 launch: on this part every dependent graph
+// node costs about 1.6 us before its first wave runs, and the merge itself is
+// latency-bound, so doing it in the projection's prologue -- while the
+// projection's weights are already in flight -- hides most of it.
+#include "cq_attention.h"
+#include "cq_gemv.h"
+
+#include <algorithm>
+
+namespace cq {
+
+constexpr int kOmDims = 16;                 // dimensions merged by one wave
+constexpr float kFixScale = 4294967296.f;   // 2^32
+// |contribution| <= 2^20 (far beyond fp16's range: a row whose sum gets
+// there ends as +-inf in fp16 either way) keeps the sum of up to 1024 heads
+// below 2^62 in int64 and its integer part inside int32
+constexpr float kFixClamp = 1048576.f;
+
+// Row band of a block, blocks of one head placed XCD-major: workgroups are
+// dealt round robin to the 8 XCDs (blockIdx % 8), so numbering them by
+// (blockIdx % 8, blockIdx / 8) gives each XCD a contiguous run of heads and
+// the blocks of one head mostly share their XCD's L2 copy of its partials.
+__device__ __forceinline__ int om_order(int b, int nb) {
+  const int x = b & 7, j = b >> 3;
+  const int before = x * (nb >> 3) + min(x, nb & 7);   // blocks on XCDs 0..x-1
+  return before + j;
+}
+
+// Q: weight format of Wo, HD: head dim, HPB: heads per block (the block
+// covers one 128-column panel: two heads at head_dim 64), NR: rounds of row
+// loads per wave.  One wave per 16 merged dimensions: 8 waves for a
+// 128-column panel, 4 for a 64-column one.
+template <int Q, int HD, int HPB>
+struct OmShape {
+  static constexpr int W = HPB * HD;                 // columns of the block's slice
+  static constexpr int WAVES = W / kOmDims;          // one merge slice per wave
+  static constexpr int THREADS = WAVES * kWave;
+};
+
+template <int Q, int HD, int HPB, int NR>
+__global__ __launch_bounds__(HPB * HD / kOmDims * kWave) void omerge_kernel(const OMergeArgs a) {
+  using T = QTraits<Q>;
+  using S = OmShape<Q, HD, HPB>;
+  constexpr int W = S::W;
+  constexpr int NCH = W / T::EPC;           // 16-byte chunks of one row slice
+  constexpr int RPW = kWave / NCH;          // rows per wave per round
+  constexpr int RPR = S::WAVES * RPW;       // rows per block per round
+  constexpr int NS = HD / kOmDims;          // merge slices per head
+  static_assert(NCH >= 1 && NCH <= kWave, "omerge: head_dim / format");
+  __shared__ __align__(16) _Float16 attn[W];
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int g = om_order(blockIdx.x, gridDim.x);
+  const int hq0 = (g / a.bands) * HPB, band = g % a.bands;
+  const int row0 = (int)(((int64_t)band * a.N) / a.bands);
+  const int row1 = (int)(((int64_t)(band + 1) * a.N) / a.bands);
+  const int gsz = a.n_heads / a.n_kv;
+
+  // 1. the first 64 partials of this wave's merge slice (independent of the
+  //    position: slots past the partition count are selected out below)
+  const int hq = hq0 + wave / NS, d0 = (wave % NS) * kOmDims;
+  const float* ws_m = reinterpret_cast<const float*>(a.workspace);
+  const float* ws_l = ws_m + (size_t)a.n_kv * a.Pmax * 16;
+  const float* ws_o = ws_l + (size_t)a.n_kv * a.Pmax * 16;
+  auto load_round = [&](int p0, float& mp, float& lp, f4_t* ov) {
+    const size_t slot = ((size_t)(hq / gsz) * a.Pmax + min(p0 + lane, a.Pmax - 1)) * 16 + hq % gsz;
+    mp = ws_m[slot];
+    lp = ws_l[slot];
+    const f4_t* op = reinterpret_cast<const f4_t*>(ws_o + slot * HD + d0);
+#pragma unroll
+    for (int i = 0; i < kOmDims / 4; ++i) ov[i] = op[i];
+  };
+  float mp, lp;
+  f4_t ov[kOmDims / 4];
+  load_round(0, mp, lp, ov);
+  // the single-partition case finds the normalised output where stage 1 wrote it
+  uint32_t direct = 0;
+  const _Float16* xb = reinterpret_cast<const _Float16*>(a.attn) + (size_t)hq0 * HD;
+  if (threadIdx.x < W / 2) direct = reinterpret_cast<const uint32_t*>(xb)[threadIdx.x];
+  const int T_ = *a.d_pos + 1;
+
+  // 2. the weight slice: round r, wave w, lane -> row row0 + r*RPR + w*RPW +
+  //    lane/NCH, chunk lane%NCH; rows past the band re-read its last row
+  //    (never used).  Wo is held in 128-column panels (wo_panels): panel p =
+  //    [N rows][128 columns], so a band's slice is one contiguous run.
+  constexpr int CP = kGroup / T::EPC;       // chunks of a panel row
+  const int cch = lane % NCH;
+  const int kc = hq0 * HD / T::EPC + cch;   // this lane's chunk within a row
+  const int pan = kc / CP;
+  const char* wbase = reinterpret_cast<const char*>(a.W) + ((size_t)pan * a.N * CP + kc % CP) * 16;
+  const _Float16* sbase = reinterpret_cast<const _Float16*>(a.S) + (size_t)pan * a.N;   // scales [panel][N]
+  u4_t wv[NR];
+  _Float16 sc[NR];
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    const int row = min(row0 + r * RPR + wave * RPW + lane / NCH, row1 - 1);
+    wv[r] = load_u4_stream(wbase + (size_t)row * CP * 16);
+    if constexpr (Q != CQ_QUANT_FP16) sc[r] = sbase[row];
+  }
+
+  // 3. merge (kernels.cu:222-288, 1 / (L + 1e-9))
+  int tpp;
+  const int nparts = a.direct ? 1 : attn_nparts(T_, a.Pmax, &tpp);
+  if (nparts == 1) {
+    if (threadIdx.x < W / 2) reinterpret_cast<uint32_t*>(attn)[threadIdx.x] = direct;
+  } else {
+    float M = -INFINITY, L = 0.f, O[kOmDims];
+#pragma unroll
+    for (int i = 0; i < kOmDims; ++i) O[i] = 0.f;
+    auto merge_round = [&](int p0) {
+      const bool valid = p0 + lane < nparts && mp != -INFINITY;
+      const float Mn = fmaxf(M, wave_max(valid ? mp : -INFINITY));
+      const float f = M == -INFINITY ? 0.f : __expf(M - Mn);
+      const float w = valid ? __expf(mp - Mn) : 0.f;
+      L = L * f + wave_sum(valid ? lp * w : 0.f);
+#pragma unroll
+      for (int i = 0; i < kOmDims / 4; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) O[4 * i + e] = O[4 * i + e] * f + wave_sum(valid ? ov[i][e] * w : 0.f);
+      M = Mn;
+    };
+    // the first round straight from the registers loaded above (outside the
+    // loop, so the wait for them leaves the weight loads in flight)
+    merge_round(0);
+    for (int p0 = kWave; p0 < nparts; p0 += kWave) {
+      load_round(p0, mp, lp, ov);
+      merge_round(p0);
+    }
+    const float inv = 1.0f / (L + 1e-9f);
+    const int base = (hq - hq0) * HD + d0;
+#pragma unroll
+    for (int i = 0; i < kOmDims; ++i)
+      if (lane == i) attn[base + i] = (_Float16)(O[i] * inv);
+  }
+  __syncthreads();
+
+  // 4. this lane's chunk of the heads' vector in the GEMV's plane order (plus
+  //    the unpack-bias term), straight from LDS
+  u4_t xv[T::PLANES];
+  float corr = 0.f;
+  {
+    const u4_t* src = reinterpret_cast<const u4_t*>(attn) + cch * T::PLANES;
+#pragma unroll
+    for (int p = 0; p < T::PLANES; ++p) corr += plane_order_packed<Q>(src[p], xv[p]);
+  }
+
+  // 5. row dots, reduced over the NCH lanes of a row, one atomic per row
+  const UnpackRegs uk = unpack_regs();
+  unsigned long long* acc = reinterpret_cast<unsigned long long*>(a.acc);
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    float v = chunk_dot<Q>(wv[r], xv, uk);
+    if constexpr (Q != CQ_QUANT_FP16) v = (v - corr) * (float)sc[r];
+#pragma unroll
+    for (int off = NCH / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+    const int row = row0 + r * RPR + wave * RPW + lane / NCH;
+    if (cch == 0 && row < row1) {
+      v = fminf(kFixClamp, fmaxf(-kFixClamp, v));
+      const long long fx = __float2ll_rn(v * kFixScale);
+      atomicAdd(acc + row, (unsigned long long)fx);
+    }
+  }
+}
+
+template <int Q, int HD, int HPB>
+static void omerge_launch_h(const OMergeArgs& a, hipStream_t stream, int nr, int blocks) {
+  const dim3 grid(blocks), block(OmShape<Q, HD, HPB>::THREADS);
+  switch (nr) {
+    case 1: hipLaunchKernelGGL((omerge_kernel<Q, HD, HPB, 1>), grid, block, 0, stream, a); break;
+    case 2: hipLaunchKernelGGL((omerge_kernel<Q, HD, HPB, 2>), grid, block, 0, stream, a); break;
+    case 4: hipLaunchKernelGGL((omerge_kernel<Q, HD, HPB, 4>), grid, block, 0, stream, a); break;
+    case 8: hipLaunchKernelGGL((omerge_kernel<Q, HD, HPB, 8>), grid, block, 0, stream, a); break;
+    default: hipLaunchKernelGGL((omerge_kernel<Q, HD, HPB, 16>), grid, block, 0, stream, a); break;
+  }
+}
+
+template <int Q, int HD>
+static void omerge_launch_q(const OMergeArgs& a, hipStream_t stream, int hpb, int nr, int blocks) {
+  if constexpr (HD == 64) {
+    if (hpb == 2) return omerge_launch_h<Q, HD, 2>(a, stream, nr, blocks);
+  }
+  omerge_launch_h<Q, HD, 1>(a, stream, nr, blocks);
+}
+
+// ------------------------------------------------------------ Wo panels
+// Row-major [N][K] (the file's layout) -> K/128 panels of [N][128]: 16-byte
+// chunk c of row n (chunk c % CP of panel c / CP) moves to
+// ((c / CP) * N + n) * CP + c % CP; group-128 scales [N][K/128] -> [K/128][N].
+__global__ void panelize_kernel(const u4_t* src, u4_t* dst, int N, int NC, int CP) {
+  const int64_t total = (int64_t)N * NC;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int n = (int)(i / NC), c = (int)(i % NC);
+    dst[((int64_t)(c / CP) * N + n) * CP + c % CP] = src[i];
+  }
+}
+__global__ void panelize_scales_kernel(const uint16_t* src, uint16_t* dst, int N, int G) {
+  const int64_t total = (int64_t)N * G;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int n = (int)(i / G), g = (int)(i % G);
+    dst[(int64_t)g * N + n] = src[i];
+  }
+}
+
+int wo_to_panels(int quant, void* W, __half* S, int N, int K, void* tmp, hipStream_t stream) {
+  if (K % kGroup) return fail(CQ_EINVAL, "wo panels: K must be a multiple of 128");
+  const int epc = quant == CQ_QUANT_INT4 ? 32 : quant == CQ_QUANT_INT8 ? 16 : 8;
+  const int NC = K / epc, CP = kGroup / epc;
+  const size_t wbytes = (size_t)N * NC * 16;
+  hipLaunchKernelGGL(panelize_kernel, dim3(1024), dim3(256), 0, stream, (const u4_t*)W, (u4_t*)tmp, N, NC, CP);
+  CQ_HIP(hipGetLastError());
+  CQ_HIP(hipMemcpyAsync(W, tmp, wbytes, hipMemcpyDeviceToDevice, stream));
+  if (quant != CQ_QUANT_FP16) {
+    const int G = K / kGroup;
+    hipLaunchKernelGGL(panelize_scales_kernel, dim3(256), dim3(256), 0, stream, (const uint16_t*)S, (uint16_t*)tmp, N, G);
+    CQ_HIP(hipGetLastError());
+    CQ_HIP(hipMemcpyAsync(S, tmp, (size_t)N * G * 2, hipMemcpyDeviceToDevice, stream));
+  }
+  return CQ_OK;
+}
+
+// Heads per block: one 128-column panel (two heads at head_dim 64, when the
+// head count is even).  Bands per head group: as many as fit one block per
+// CU (7B: 28 heads x 9 bands = 252 blocks), more when a band would need more
+// than 16 rounds of row loads.
+int omerge_plan(int quant, int head_dim, int n_heads, int N, int* hpb, int* bands, int* rounds) {
+  const int epc = quant == CQ_QUANT_INT4 ? 32 : quant == CQ_QUANT_INT8 ? 16 : 8;
+  const int h = (head_dim == 64 && n_heads % 2 == 0) ? 2 : 1;
+  const int nch = h * head_dim / epc;
+  const int rpr = (h * head_dim / kOmDims) * (kWave / nch);
+  const int groups = n_heads / h;
+  int b = std::max(1, kNumCUs / groups);
+  b = std::max(b, (N + 16 * rpr - 1) / (16 * rpr));
+  b = std::min(b, N);
+  const int rows = (N + b - 1) / b;
+  const int nr = (rows + rpr - 1) / rpr;
+  int p2 = 1;
+  while (p2 < nr) p2 <<= 1;
+  *hpb = h;
+  *bands = b;
+  *rounds = p2;
+  return CQ_OK;
+}
+
+int launch_omerge(const OMergeArgs& a0, hipStream_t stream) {
+  OMergeArgs a = a0;
+  if (a.head_dim != 64 && a.head_dim != 128) return fail(CQ_EINVAL, "omerge: head_dim must be 64 or 128");
+  if (a.quant < 0 || a.quant > 2) return fail(CQ_EINVAL, "omerge: bad quant type");
+  if (a.n_kv <= 0 || a.n_heads % a.n_kv || a.n_heads / a.n_kv > 16) return fail(CQ_EINVAL, "omerge: bad head layout");
+  if (a.K != a.n_heads * a.head_dim || a.N <= 0) return fail(CQ_EINVAL, "omerge: bad shape");
+  if (!a.workspace || !a.attn || !a.W || !a.acc || !a.d_pos || (a.quant != CQ_QUANT_FP16 && !a.S))
+    return fail(CQ_EINVAL, "omerge: null pointer");
+  if (a.Pmax <= 0) return fail(CQ_EINVAL, "omerge: bad partition count");
+  int hpb = 1, nr = 1;
+  omerge_plan(a.quant, a.head_dim, a.n_heads, a.N, &hpb, &a.bands, &nr);
+  const int blocks = a.n_heads / hpb * a.bands;
+  if (a.quant == CQ_QUANT_INT4) {
+    if (a.head_dim == 128) omerge_launch_q<CQ_QUANT_INT4, 128>(a, stream, hpb, nr, blocks);
+    else omerge_launch_q<CQ_QUANT_INT4, 64>(a, stream, hpb, nr, blocks);
+  } else if (a.quant == CQ_QUANT_INT8) {
+    if (a.head_dim == 128) omerge_launch_q<CQ_QUANT_INT8, 128>(a, stream, hpb, nr, blocks);
+    else omerge_launch_q<CQ_QUANT_INT8, 64>(a, stream, hpb, nr, blocks);
+  } else {
+    if (a.head_dim == 128) omerge_launch_q<CQ_QUANT_FP16, 128>(a, stream, hpb, nr, blocks);
+    else omerge_launch_q<CQ_QUANT_FP16, 64>(a, stream, hpb, nr, blocks);
+  }
+  CQ_HIP(hipGetLastError());
+  return CQ_OK;
+}
+
+}  // namespace cq

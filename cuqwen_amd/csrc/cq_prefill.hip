@@ -182,7 +182,9 @@ __device__ __forceinline__ void pf_kv8_store(const PfGemmArgs& a, int mat, int k
 template <int Q>
 __device__ __forceinline__ void pf_load_w(const PfGemmArgs& a, const char* rowp, int ks, int j, u4_t* w) {
   constexpr int L = PfW<Q>::LOADS;
-  const char* p = rowp + (int64_t)ks * (64 * L) + j * (L * 16);   // 64*L bytes of the row per step, L*16 per lane
+  // 64*L bytes of the row per step (panels: one panel row, panel stride N rows), L*16 per lane
+  const int64_t kstep = a.panels ? (int64_t)a.N * (64 * L) : 64 * L;
+  const char* p = rowp + (int64_t)ks * kstep + j * (L * 16);
 #pragma unroll
   for (int i = 0; i < L; ++i) w[i] = load_u4(p + i * 16);
 }
@@ -259,6 +261,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
   const int ke = SPLIT ? (int)((int64_t)(blockIdx.z + 1) * nks / gridDim.z) : nks;
 
   // weight row (A operand row r of each slice) and its scale row
+  const int64_t sstep = a.panels ? a.N : 1;   // scale stride of one K step
   const char* rowp[NMAT][RT];
   const _Float16* srow[NMAT][RT];
 #pragma unroll
@@ -268,9 +271,11 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
       int local, row = min(nw0 + rt * 16 + r, a.N - 1);
       const int mat = MODE == GM_SWIGLU ? mt : pf_mat(a, row, &local);
       if (MODE == GM_SWIGLU) local = row;
-      const int64_t rbytes = Q == CQ_QUANT_INT4 ? K / 2 : Q == CQ_QUANT_INT8 ? K : 2 * K;
+      // row-major: step ks is bytes [64*L*ks, 64*L*(ks+1)) of the row; panels: row
+      // `local` of panel ks (wo_to_panels), scales [panel][N]
+      const int64_t rbytes = a.panels ? 64 * L : Q == CQ_QUANT_INT4 ? K / 2 : Q == CQ_QUANT_INT8 ? K : 2 * K;
       rowp[mt][rt] = reinterpret_cast<const char*>(sel3(a.W, mat)) + (int64_t)local * rbytes;
-      srow[mt][rt] = Q == CQ_QUANT_FP16 ? nullptr : sel3(a.S, mat) + (int64_t)local * (K / kGroup);
+      srow[mt][rt] = Q == CQ_QUANT_FP16 ? nullptr : sel3(a.S, mat) + (a.panels ? (int64_t)local : (int64_t)local * (K / kGroup));
     }
 
   // Activation tiles: global -> registers one step ahead, then 16-byte LDS
@@ -324,7 +329,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) {
         pf_load_w<Q>(a, rowp[mt][rt], ks, j, w[mt][rt]);
-        if constexpr (Q != CQ_QUANT_FP16) s[mt][rt] = srow[mt][rt][ks];
+        if constexpr (Q != CQ_QUANT_FP16) s[mt][rt] = srow[mt][rt][(int64_t)ks * sstep];
       }
   };
   // Every load is issued unconditionally (step indices clamped to the last
@@ -1125,6 +1130,7 @@ int launch_pf_gemm(const PfGemmArgs& a, hipStream_t stream) {
     return fail(CQ_EINVAL, "prefill gemm: swiglu needs gate, up, the norm and rows a multiple of 8");
   if (a.mode == GM_RESID && (a.N % 8 || (a.norm_w && (!a.norm_out || !a.norm_inv))))
     return fail(CQ_EINVAL, "prefill gemm: residual rows must be a multiple of 8 wide; the norm needs its outputs");
+  if (a.panels && a.mode != GM_RESID) return fail(CQ_EINVAL, "prefill gemm: paneled weights are a residual-mode option");
   if (a.mode == GM_QKV) {
     if (!a.inv || !a.W[1] || !a.W[2] || !a.inv_freq) return fail(CQ_EINVAL, "prefill gemm: qkv operands");
     if (a.kcache8 ? (!a.vcache8 || !a.kscale || !a.vscale) : (!a.kcache || !a.vcache))

@@ -98,7 +98,12 @@ int cq_free_weights(cq_weights* w);
 /* Device pointers of one tensor, for op-level tests and tools.  `name` is one
  * of: embed, final_norm, lm_head, lm_head_scale, and per layer (layer >= 0):
  * in_norm, wq, sq, bq, wk, sk, bk, wv, sv, bv, wo, so, post_norm, wg, sg, wu,
- * su, wd, sd.  *bytes receives the tensor size. */
+ * su, wd, sd.  *bytes receives the tensor size.  Every tensor is held in
+ * the exporter's row-major layout except the O-projection: wo is stored as
+ * K/128 column panels, panel p = rows 0..N-1 of columns [128p, 128p+128)
+ * (row-major within the panel), and so as [K/128][N], so that the decode's
+ * merged attention + O-projection streams each head's columns contiguously
+ * (converted once when the weights are loaded or synthesized). */
 int cq_weights_tensor(const cq_weights* w, const char* name, int32_t layer, void** dptr, size_t* bytes);
 
 /* ---------------------------------------------------------------- state */

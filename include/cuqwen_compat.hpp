@@ -115,9 +115,10 @@ struct QwenConfig {
   }
 };
 
-// Device pointers into the engine's weight arena (exporter layout), filled
-// by load_weights so op-level callers find every tensor where the
-// reference's loader puts it.
+// Device pointers into the engine's weight arena, filled by load_weights so
+// op-level callers find every tensor where the reference's loader puts it.
+// Exporter layout, except o_proj_weight / o_proj_scale: 128-column panels
+// (see cq_weights_tensor in cuqwen.h).
 struct LayerWeights {
   __half* input_layernorm_weight = nullptr;
   qweight_t* q_proj_weight = nullptr;

@@ -37,6 +37,25 @@ def test_device_synthesis_equals_file_load(tmp_path, quant, tied, lm):
     ws.free()
 
 
+@pytest.mark.parametrize("quant", [0, 1, 2])
+def test_o_projection_held_in_128_column_panels(quant):
+    """The device O-projection is the file's row-major [N][K] matrix cut into
+    K/128 column panels [N][128] (scales [N][K/128] -> [K/128][N]); checked
+    against the oracle's row-major bytes of the same seeded weights."""
+    cfg = tiny_config(quant)
+    w = cq.synth_weights(cfg, 77)
+    om = orc.Model.synth(cfg, 77, cfg.max_seq_len)
+    N, K = cfg.dim, cfg.n_heads * cfg.head_dim
+    pb = {0: 256, 1: 128, 2: 64}[quant]   # bytes of one 128-column panel row
+    for layer in range(cfg.n_layers):
+        rm = om.tensor(layer, orc.K_WO, 0).reshape(N, K // 128, pb)
+        assert np.array_equal(_dump(w, "wo", layer), rm.transpose(1, 0, 2).reshape(-1)), layer
+        if quant:
+            sc = om.tensor(layer, orc.K_WO, 1).reshape(N, K // 128, 2)
+            assert np.array_equal(_dump(w, "so", layer), sc.transpose(1, 0, 2).reshape(-1)), layer
+    w.free()
+
+
 def test_load_weights_rejects_mismatch(tmp_path):
     cfg = tiny_config(1)
     path = str(tmp_path / "w.bin")
