@@ -141,11 +141,12 @@ __device__ __forceinline__ void block_merge_write(const AttnArgs& a, int kvh, in
   }
   __syncthreads();
 
+  // partial slots head-major: slot (kvh * 16 + head) * Pmax + part, so the
+  // merge reads each head's partitions as one contiguous run
   float* ws_m = reinterpret_cast<float*>(a.workspace);
   const int Pmax = gridDim.x;
   float* ws_l = ws_m + (size_t)a.n_kv * Pmax * 16;
   float* ws_o = ws_l + (size_t)a.n_kv * Pmax * 16;
-  const size_t pslot = (size_t)kvh * Pmax + part;
   _Float16* out = reinterpret_cast<_Float16*>(a.out);
 
   for (int idx = threadIdx.x; idx < g * HD; idx += kAttnThreads) {
@@ -163,8 +164,9 @@ __device__ __forceinline__ void block_merge_write(const AttnArgs& a, int kvh, in
     if (nparts == 1) {
       out[(int64_t)(kvh * g + hh) * HD + d] = (_Float16)(O * (1.0f / (L + 1e-9f)));
     } else {
-      ws_o[(pslot * 16 + hh) * HD + d] = O;
-      if (d == 0) { ws_m[pslot * 16 + hh] = M; ws_l[pslot * 16 + hh] = L; }
+      const size_t slot = ((size_t)kvh * 16 + hh) * Pmax + part;
+      ws_o[slot * HD + d] = O;
+      if (d == 0) { ws_m[slot] = M; ws_l[slot] = L; }
     }
   }
 }

@@ -31,7 +31,8 @@ namespace cq {
 
 int attention_max_parts(int n_kv) { return (kAttnBlocksTarget + n_kv - 1) / n_kv; }
 
-// Workspace: [m: n_kv*P*16] [l: n_kv*P*16] [o: n_kv*P*16*hd] floats.
+// Workspace: [m: n_kv*16*P] [l: n_kv*16*P] [o: n_kv*16*P*hd] floats, slot
+// (kv head * 16 + head within the group) * P + partition.
 size_t attention_workspace_bytes(int n_heads, int n_kv, int head_dim) {
   (void)n_heads;
   const size_t P = (size_t)attention_max_parts(n_kv);
@@ -195,13 +196,13 @@ __global__ __launch_bounds__(kWave) void attention_stage2(const AttnArgs a, int 
   const float* ws_m = reinterpret_cast<const float*>(a.workspace);
   const float* ws_l = ws_m + (size_t)a.n_kv * Pmax * 16;
   const float* ws_o = ws_l + (size_t)a.n_kv * Pmax * 16;
-  const size_t base = (size_t)kvh * Pmax;
+  const size_t base = ((size_t)kvh * 16 + hh) * Pmax;   // head-major slots
   // the first round's slots (partition = lane) are requested before the
   // position is known: they do not depend on it, and slots past the
   // partition count are masked below (selected out, so stale contents of
   // unused slots never reach the sums)
   auto load_round = [&](int p0, float& mp, float& lp, f4_t* ov) {
-    const size_t slot = (base + min(p0 + lane, Pmax - 1)) * 16 + hh;
+    const size_t slot = base + min(p0 + lane, Pmax - 1);
     mp = ws_m[slot];
     lp = ws_l[slot];
     const f4_t* op = reinterpret_cast<const f4_t*>(ws_o + slot * HD + d0);

@@ -3,10 +3,10 @@
 // Reference: the split-K attention's stage 2 (src/kernels.cu:222-288) and the
 // O-projection gemv_add (kernels.cu:640-687) are two dependent launches.
 // Here block (head h, row band c) merges head h's stage-1 partials itself
-// (the log-sum-exp rule of stage 2, same arithmetic order: one wave per
-// 16-dimension slice, one lane per partition, DPP wave sums, so the fp16
-// attention output is bit-identical to stage 2's), stages it in LDS and
-// multiplies it by the column slice Wo[band rows][h*hd .. (h+1)*hd), which
+// (the log-sum-exp rule of stage 2; the partials read as whole contiguous
+// rows, each wave weighting its rows, the sums finished across lanes and
+// waves), stages the fp16 attention output in LDS and multiplies it by the
+// column slice Wo[band rows][h*hd .. (h+1)*hd), which
 // the 128-column panel layout of Wo (wo_to_panels, below) makes one
 // contiguous run of HBM.  The head contributions of an output row
 // are summed in a 64-bit fixed-point accumulator (value * 2^32, one atomic
@@ -27,7 +27,7 @@
 
 namespace cq {
 
-constexpr int kOmDims = 16;                 // dimensions merged by one wave
+constexpr int kOmDims = 16;                 // columns of the block's slice per wave
 constexpr float kFixScale = 4294967296.f;   // 2^32
 // |contribution| <= 2^20 (far beyond fp16's range: a row whose sum gets
 // there ends as +-inf in fp16 either way) keeps the sum of up to 1024 heads
@@ -46,26 +46,28 @@ __device__ __forceinline__ int om_order(int b, int nb) {
 
 // Q: weight format of Wo, HD: head dim, HPB: heads per block (the block
 // covers one 128-column panel: two heads at head_dim 64), NR: rounds of row
-// loads per wave.  One wave per 16 merged dimensions: 8 waves for a
-// 128-column panel, 4 for a 64-column one.
+// loads per wave.  One wave per 16 columns: 8 waves for a 128-column panel,
+// 4 for a 64-column one.
 template <int Q, int HD, int HPB>
 struct OmShape {
-  static constexpr int W = HPB * HD;                 // columns of the block's slice
-  static constexpr int WAVES = W / kOmDims;          // one merge slice per wave
-  static constexpr int THREADS = WAVES * kWave;
+  static constexpr int THREADS = HPB * HD / kOmDims * kWave;
 };
 
 template <int Q, int HD, int HPB, int NR>
 __global__ __launch_bounds__(HPB * HD / kOmDims * kWave) void omerge_kernel(const OMergeArgs a) {
   using T = QTraits<Q>;
-  using S = OmShape<Q, HD, HPB>;
-  constexpr int W = S::W;
+  constexpr int W = HPB * HD;               // columns of the block's slice
+  constexpr int WAVES = W / kOmDims;
   constexpr int NCH = W / T::EPC;           // 16-byte chunks of one row slice
   constexpr int RPW = kWave / NCH;          // rows per wave per round
-  constexpr int RPR = S::WAVES * RPW;       // rows per block per round
-  constexpr int NS = HD / kOmDims;          // merge slices per head
+  constexpr int RPR = WAVES * RPW;          // rows per block per round
+  constexpr int LPR = HD / 4;               // lanes per partition row (16 bytes each)
+  constexpr int RPI = kWave / LPR;          // partition rows per wave instruction
+  constexpr int NI = kWave / (WAVES * RPI); // instructions per wave per head and 64 partitions
   static_assert(NCH >= 1 && NCH <= kWave, "omerge: head_dim / format");
+  static_assert(NI >= 1 && NI * WAVES * RPI == kWave, "omerge: merge tiling");
   __shared__ __align__(16) _Float16 attn[W];
+  __shared__ __align__(16) float part[WAVES][W];
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -75,23 +77,37 @@ __global__ __launch_bounds__(HPB * HD / kOmDims * kWave) void omerge_kernel(cons
   const int row1 = (int)(((int64_t)(band + 1) * a.N) / a.bands);
   const int gsz = a.n_heads / a.n_kv;
 
-  // 1. the first 64 partials of this wave's merge slice (independent of the
-  //    position: slots past the partition count are selected out below)
-  const int hq = hq0 + wave / NS, d0 = (wave % NS) * kOmDims;
+  // 1. the first 64 partitions of the block's heads, read coalesced: the
+  //    partials are head-major (a head's partitions are contiguous 512-byte
+  //    rows at head_dim 128), so one wave instruction covers RPI whole rows.
+  //    (Lane-per-partition reads touched 64 cache lines per instruction and
+  //    held the CU's memory pipeline -- and the weight loads queued behind
+  //    them -- for microseconds.)  Independent of the position: rows past the
+  //    partition count are weighted 0 below.
   const float* ws_m = reinterpret_cast<const float*>(a.workspace);
   const float* ws_l = ws_m + (size_t)a.n_kv * a.Pmax * 16;
   const float* ws_o = ws_l + (size_t)a.n_kv * a.Pmax * 16;
-  auto load_round = [&](int p0, float& mp, float& lp, f4_t* ov) {
-    const size_t slot = ((size_t)(hq / gsz) * a.Pmax + min(p0 + lane, a.Pmax - 1)) * 16 + hq % gsz;
-    mp = ws_m[slot];
-    lp = ws_l[slot];
-    const f4_t* op = reinterpret_cast<const f4_t*>(ws_o + slot * HD + d0);
-#pragma unroll
-    for (int i = 0; i < kOmDims / 4; ++i) ov[i] = op[i];
+  auto head_base = [&](int j) {
+    const int hq = hq0 + j;
+    return ((size_t)(hq / gsz) * 16 + hq % gsz) * a.Pmax;
   };
-  float mp, lp;
-  f4_t ov[kOmDims / 4];
-  load_round(0, mp, lp, ov);
+  const int rsub = lane / LPR, d4 = (lane % LPR) * 4;
+  float mp[HPB], lp[HPB];
+  f4_t ov[HPB][NI];
+  auto load_chunk = [&](int p0) {
+#pragma unroll
+    for (int j = 0; j < HPB; ++j) {
+      const size_t base = head_base(j);
+      mp[j] = ws_m[base + min(p0 + lane, a.Pmax - 1)];
+      lp[j] = ws_l[base + min(p0 + lane, a.Pmax - 1)];
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const int p = p0 + (i * WAVES + wave) * RPI + rsub;
+        ov[j][i] = *reinterpret_cast<const f4_t*>(ws_o + (base + min(p, a.Pmax - 1)) * HD + d4);
+      }
+    }
+  };
+  load_chunk(0);
   // the single-partition case finds the normalised output where stage 1 wrote it
   uint32_t direct = 0;
   const _Float16* xb = reinterpret_cast<const _Float16*>(a.attn) + (size_t)hq0 * HD;
@@ -117,39 +133,66 @@ __global__ __launch_bounds__(HPB * HD / kOmDims * kWave) void omerge_kernel(cons
     if constexpr (Q != CQ_QUANT_FP16) sc[r] = sbase[row];
   }
 
-  // 3. merge (kernels.cu:222-288, 1 / (L + 1e-9))
+  // 3. merge (kernels.cu:222-288, 1 / (L + 1e-9)): every wave forms the
+  //    running max M and sum L of each head from its 64 m / l values (the
+  //    same on every wave), weights its own rows, and the per-dimension sums
+  //    are finished across the lanes of a row group and then across the
+  //    waves in LDS
   int tpp;
   const int nparts = a.direct ? 1 : attn_nparts(T_, a.Pmax, &tpp);
+  float L[HPB];
   if (nparts == 1) {
     if (threadIdx.x < W / 2) reinterpret_cast<uint32_t*>(attn)[threadIdx.x] = direct;
   } else {
-    float M = -INFINITY, L = 0.f, O[kOmDims];
+    float M[HPB];
+    f4_t acc4[HPB];
 #pragma unroll
-    for (int i = 0; i < kOmDims; ++i) O[i] = 0.f;
-    auto merge_round = [&](int p0) {
-      const bool valid = p0 + lane < nparts && mp != -INFINITY;
-      const float Mn = fmaxf(M, wave_max(valid ? mp : -INFINITY));
-      const float f = M == -INFINITY ? 0.f : __expf(M - Mn);
-      const float w = valid ? __expf(mp - Mn) : 0.f;
-      L = L * f + wave_sum(valid ? lp * w : 0.f);
-#pragma unroll
-      for (int i = 0; i < kOmDims / 4; ++i)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) O[4 * i + e] = O[4 * i + e] * f + wave_sum(valid ? ov[i][e] * w : 0.f);
-      M = Mn;
-    };
-    // the first round straight from the registers loaded above (outside the
-    // loop, so the wait for them leaves the weight loads in flight)
-    merge_round(0);
-    for (int p0 = kWave; p0 < nparts; p0 += kWave) {
-      load_round(p0, mp, lp, ov);
-      merge_round(p0);
+    for (int j = 0; j < HPB; ++j) {
+      M[j] = -INFINITY;
+      L[j] = 0.f;
+      acc4[j] = f4_t{0.f, 0.f, 0.f, 0.f};
     }
-    const float inv = 1.0f / (L + 1e-9f);
-    const int base = (hq - hq0) * HD + d0;
+    auto merge_chunk = [&](int p0) {
 #pragma unroll
-    for (int i = 0; i < kOmDims; ++i)
-      if (lane == i) attn[base + i] = (_Float16)(O[i] * inv);
+      for (int j = 0; j < HPB; ++j) {
+        const bool valid = p0 + lane < nparts && mp[j] != -INFINITY;
+        const float Mn = fmaxf(M[j], wave_max(valid ? mp[j] : -INFINITY));
+        const float f = M[j] == -INFINITY ? 0.f : __expf(M[j] - Mn);
+        const float wgt = valid ? __expf(mp[j] - Mn) : 0.f;
+        L[j] = L[j] * f + wave_sum(valid ? lp[j] * wgt : 0.f);
+        f4_t s4 = acc4[j] * f;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) s4 += ov[j][i] * __shfl(wgt, (i * WAVES + wave) * RPI + rsub, kWave);
+        acc4[j] = s4;
+        M[j] = Mn;
+      }
+    };
+    // the first chunk straight from the registers loaded above (outside the
+    // loop, so the wait for them leaves the weight loads in flight)
+    merge_chunk(0);
+    for (int p0 = kWave; p0 < nparts; p0 += kWave) {
+      load_chunk(p0);
+      merge_chunk(p0);
+    }
+#pragma unroll
+    for (int j = 0; j < HPB; ++j) {
+#pragma unroll
+      for (int off = LPR; off < kWave; off <<= 1)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc4[j][e] += __shfl_xor(acc4[j][e], off, kWave);
+      if (rsub == 0) *reinterpret_cast<f4_t*>(&part[wave][j * HD + d4]) = acc4[j];
+    }
+  }
+  __syncthreads();
+  if (nparts > 1 && threadIdx.x < W) {
+    float o = 0.f;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) o += part[w][threadIdx.x];
+    const int j = threadIdx.x / HD;
+    float lj = L[0];
+#pragma unroll
+    for (int jj = 1; jj < HPB; ++jj) lj = j == jj ? L[jj] : lj;
+    attn[threadIdx.x] = (_Float16)(o * (1.0f / (lj + 1e-9f)));
   }
   __syncthreads();
 
