@@ -160,6 +160,17 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 // first, and the weight loads in flight stay in flight.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
+// A 32-bit word that no wave of the running kernel writes (a control word
+// written by an earlier launch or the host), read through the constant
+// address space: the compiler issues a scalar load, whose wait counts only
+// scalar loads.  As a vector load from a uniform address it was turned into
+// a scalar with readfirstlane right away, behind a full vmcnt(0) that waited
+// for every load the wave had in flight.  (The scalar cache is invalidated
+// at each kernel launch, so earlier writes are seen.)
+__device__ __forceinline__ uint32_t load_ctl_u32(const void* p) {
+  return *(const __attribute__((address_space(4))) uint32_t*)p;
+}
+
 __device__ __forceinline__ u4_t load_u4(const void* p) { return *reinterpret_cast<const u4_t*>(p); }
 __device__ __forceinline__ u4_t load_u4_stream(const void* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(p));

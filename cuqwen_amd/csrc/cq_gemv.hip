@@ -120,8 +120,8 @@ __global__ __launch_bounds__(BLK) void gemv_kernel(const GemvArgs a) {
   // the step's control word the epilogue needs (QKV: position; STORE: the
   // penalty epoch), also read up front rather than in the epilogue
   uint32_t step_word = 0;
-  if constexpr (MODE == GM_QKV) step_word = (uint32_t)*a.d_pos;
-  if constexpr (MODE == GM_STORE) step_word = a.stamp ? *a.d_epoch : 0u;
+  if constexpr (MODE == GM_QKV) step_word = load_ctl_u32(a.d_pos);
+  if constexpr (MODE == GM_STORE) step_word = a.stamp ? load_ctl_u32(a.d_epoch) : 0u;
   __builtin_amdgcn_s_setprio(0);
   StepBuf<R, U> A, B;
   Cursor ca = make(u_begin + wave, 0);
