@@ -90,6 +90,19 @@ __device__ __forceinline__ void attend_tile(KVTile<HD>& t, const h8_t* qb, int t
   for (int dt = 0; dt < DT; ++dt) o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(t.va[dt], pb, o[dt], 0, 0, 0);
 }
 
+// All kernel arguments of a stage-1 launch in one batch of scalar loads
+// (CQ_PIN); KV8 adds the quantized cache's.
+template <bool KV8>
+__device__ __forceinline__ void pin_attn_args(const AttnArgs& a) {
+  CQ_PIN(gridDim.x); CQ_PIN(a.q); CQ_PIN(a.out); CQ_PIN(a.d_pos); CQ_PIN(a.n_heads); CQ_PIN(a.n_kv);
+  CQ_PIN(a.max_seq); CQ_PIN(a.workspace);
+  if constexpr (KV8) {
+    CQ_PIN(a.kcache8); CQ_PIN(a.vcache8); CQ_PIN(a.kscale); CQ_PIN(a.vscale); CQ_PIN(a.k_new); CQ_PIN(a.v_new);
+  } else {
+    CQ_PIN(a.kcache); CQ_PIN(a.vcache);
+  }
+}
+
 __device__ __forceinline__ int attn_nparts(int T, int P, int* tpp_out) {
   const int n_tiles = (T + kTileKeys - 1) / kTileKeys;
   int tpp = (n_tiles + P - 1) / P;

@@ -41,6 +41,7 @@ size_t attention_workspace_bytes(int n_heads, int n_kv, int head_dim) {
 
 template <int HD>
 __global__ __launch_bounds__(kAttnThreads) void attention_stage1(const AttnArgs a) {
+  pin_attn_args<false>(a);
   constexpr int KK = HD / 32;
   constexpr int DT = HD / 16;
   const int kvh = blockIdx.y;
@@ -48,7 +49,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_stage1(const AttnArgs 
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int g = a.n_heads / a.n_kv;
-  const int T = *a.d_pos + 1;
+  const int T = (int)load_ctl_u32(a.d_pos) + 1;
   const int n_tiles = (T + kTileKeys - 1) / kTileKeys;
   int tpp;
   const int nparts = attn_nparts(T, gridDim.x, &tpp);
@@ -92,11 +93,12 @@ __global__ __launch_bounds__(kAttnThreads) void attention_stage1(const AttnArgs 
 // reads that position, so no block synchronisation is needed.
 template <int HD, int F>
 __global__ __launch_bounds__(kAttnThreads) void attention_stage1_kv8(const AttnArgs a) {
+  pin_attn_args<true>(a);
   constexpr int KK = HD / 32, DT = HD / 16, E = HD / kWave;
   const int kvh = blockIdx.y, part = blockIdx.x;
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
   const int g = a.n_heads / a.n_kv;
-  const int pos = *a.d_pos, T = pos + 1;
+  const int pos = (int)load_ctl_u32(a.d_pos), T = pos + 1;
   const int n_tiles = (T + kTileKeys - 1) / kTileKeys;
   int tpp;
   const int nparts = attn_nparts(T, gridDim.x, &tpp);
@@ -212,7 +214,7 @@ __global__ __launch_bounds__(kWave) void attention_stage2(const AttnArgs a, int 
   float mp, lp;
   f4_t ov[kMergeDims / 4];
   load_round(0, mp, lp, ov);
-  const int T = *a.d_pos + 1;
+  const int T = (int)load_ctl_u32(a.d_pos) + 1;
   int tpp;
   const int nparts = attn_nparts(T, Pmax, &tpp);
   if (nparts == 1) return;   // stage 1 wrote the output

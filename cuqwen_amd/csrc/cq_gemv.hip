@@ -18,6 +18,35 @@ __device__ __forceinline__ float fix_to_float(uint32_t lo, uint32_t hi) {
   return fmaf((float)lo, 2.3283064365386963e-10f, (float)(int32_t)hi);
 }
 
+// Every kernel-argument word a mode reads, fetched in one batch of scalar
+// loads at entry (CQ_PIN): the GEMV prologue otherwise waited for three or
+// four dependent kernel-argument round trips between its address
+// computations before the weight prefetch was out.
+template <int Q, int MODE, bool NORM, bool ADD>
+__device__ __forceinline__ void pin_args(const GemvArgs& a) {
+  CQ_PIN(gridDim.x);   // an implicit kernel argument
+  CQ_PIN(a.x); CQ_PIN(a.K); CQ_PIN(a.N); CQ_PIN(a.W[0]); CQ_PIN(a.out[0]);
+  if constexpr (Q != CQ_QUANT_FP16) CQ_PIN(a.S[0]);
+  if constexpr (NORM) { CQ_PIN(a.norm_w); CQ_PIN(a.eps); }
+  if constexpr (MODE == GM_SWIGLU || MODE == GM_QKV) {
+    CQ_PIN(a.W[1]);
+    if constexpr (Q != CQ_QUANT_FP16) CQ_PIN(a.S[1]);
+  }
+  if constexpr (MODE == GM_QKV) {
+    CQ_PIN(a.W[2]); CQ_PIN(a.bias[0]); CQ_PIN(a.bias[1]); CQ_PIN(a.bias[2]);
+    CQ_PIN(a.out[1]); CQ_PIN(a.out[2]);
+    if constexpr (Q != CQ_QUANT_FP16) CQ_PIN(a.S[2]);
+    CQ_PIN(a.n_heads); CQ_PIN(a.n_kv); CQ_PIN(a.head_dim); CQ_PIN(a.d_pos); CQ_PIN(a.rope_inv_freq);
+    CQ_PIN(a.rope_theta);
+    CQ_PIN(a.kcache); CQ_PIN(a.vcache); CQ_PIN(a.max_seq);
+  }
+  if constexpr (MODE == GM_STORE) {
+    CQ_PIN(a.bias[0]); CQ_PIN(a.stamp); CQ_PIN(a.d_epoch); CQ_PIN(a.argmax_out); CQ_PIN(a.penalty);
+  }
+  if constexpr (MODE == GM_RESID) { CQ_PIN(a.resid); CQ_PIN(a.zero); }
+  if constexpr (ADD) { CQ_PIN(a.x_acc); CQ_PIN(a.x_out); }
+}
+
 // Persistent GEMV.  Block b owns the contiguous unit range
 // [b*n/G, (b+1)*n/G); inside the block, wave w starts on units begin + w and
 // begin + WPB + w and then claims further units from an LDS counter.  The
@@ -41,6 +70,7 @@ template <int Q, int MODE, int R, int U, bool NORM, bool G128, int BLK, bool ADD
 __global__ __launch_bounds__(BLK) void gemv_kernel(const GemvArgs a) {
   static_assert(!ADD || (NORM && MODE == GM_SWIGLU), "ADD is the norm-fused SWIGLU prologue");
   using T = QTraits<Q>;
+  pin_args<Q, MODE, NORM, ADD>(a);
   extern __shared__ u4_t smem[];
   __shared__ float red[BLK / kWave];
   __shared__ double inv_freq[MODE == GM_QKV ? kMaxHeadDim / 2 : 1];

@@ -56,6 +56,9 @@ struct OmShape {
 template <int Q, int HD, int HPB, int NR>
 __global__ __launch_bounds__(HPB * HD / kOmDims * kWave) void omerge_kernel(const OMergeArgs a) {
   using T = QTraits<Q>;
+  CQ_PIN(gridDim.x); CQ_PIN(a.workspace); CQ_PIN(a.attn); CQ_PIN(a.W); CQ_PIN(a.acc); CQ_PIN(a.d_pos);
+  CQ_PIN(a.n_heads); CQ_PIN(a.n_kv); CQ_PIN(a.K); CQ_PIN(a.N); CQ_PIN(a.Pmax); CQ_PIN(a.bands); CQ_PIN((int)a.direct);
+  if constexpr (Q != CQ_QUANT_FP16) CQ_PIN(a.S);
   constexpr int W = HPB * HD;               // columns of the block's slice
   constexpr int WAVES = W / kOmDims;
   constexpr int NCH = W / T::EPC;           // 16-byte chunks of one row slice
@@ -112,7 +115,7 @@ __global__ __launch_bounds__(HPB * HD / kOmDims * kWave) void omerge_kernel(cons
   uint32_t direct = 0;
   const _Float16* xb = reinterpret_cast<const _Float16*>(a.attn) + (size_t)hq0 * HD;
   if (threadIdx.x < W / 2) direct = reinterpret_cast<const uint32_t*>(xb)[threadIdx.x];
-  const int T_ = *a.d_pos + 1;
+  const int T_ = (int)load_ctl_u32(a.d_pos) + 1;
 
   // 2. the weight slice: round r, wave w, lane -> row row0 + r*RPR + w*RPW +
   //    lane/NCH, chunk lane%NCH; rows past the band re-read its last row
