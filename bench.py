@@ -27,8 +27,8 @@ PEAK_GBPS = 8000.0   # MI355X HBM3E
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=128)
-    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--steps", type=int, default=512)
+    ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--model", default="7B")
     ap.add_argument("--quant", default="int4")
     ap.add_argument("--ctx", type=int, default=32768, help="context length at the end of the timed steps")

@@ -48,19 +48,21 @@ __device__ __forceinline__ int om_order(int b, int nb) {
 // covers one 128-column panel: two heads at head_dim 64), NR: rounds of row
 // loads per wave.  One wave per 16 columns: 8 waves for a 128-column panel,
 // 4 for a 64-column one.
-template <int Q, int HD, int HPB>
+// WM: 1, or 2 for twice the waves (bands of many rows: half the load rounds
+// per wave).
+template <int HD, int HPB, int WM>
 struct OmShape {
-  static constexpr int THREADS = HPB * HD / kOmDims * kWave;
+  static constexpr int THREADS = HPB * HD / kOmDims * WM * kWave;
 };
 
-template <int Q, int HD, int HPB, int NR>
-__global__ __launch_bounds__(HPB * HD / kOmDims * kWave) void omerge_kernel(const OMergeArgs a) {
+template <int Q, int HD, int HPB, int NR, int WM>
+__global__ __launch_bounds__(HPB * HD / kOmDims * WM * kWave) void omerge_kernel(const OMergeArgs a) {
   using T = QTraits<Q>;
   CQ_PIN(gridDim.x); CQ_PIN(a.workspace); CQ_PIN(a.attn); CQ_PIN(a.W); CQ_PIN(a.acc); CQ_PIN(a.d_pos);
   CQ_PIN(a.n_heads); CQ_PIN(a.n_kv); CQ_PIN(a.K); CQ_PIN(a.N); CQ_PIN(a.Pmax); CQ_PIN(a.bands); CQ_PIN((int)a.direct);
   if constexpr (Q != CQ_QUANT_FP16) CQ_PIN(a.S);
   constexpr int W = HPB * HD;               // columns of the block's slice
-  constexpr int WAVES = W / kOmDims;
+  constexpr int WAVES = W / kOmDims * WM;
   constexpr int NCH = W / T::EPC;           // 16-byte chunks of one row slice
   constexpr int RPW = kWave / NCH;          // rows per wave per round
   constexpr int RPR = WAVES * RPW;          // rows per block per round
@@ -228,23 +230,34 @@ __global__ __launch_bounds__(HPB * HD / kOmDims * kWave) void omerge_kernel(cons
 }
 
 template <int Q, int HD, int HPB>
-static void omerge_launch_h(const OMergeArgs& a, hipStream_t stream, int nr, int blocks) {
-  const dim3 grid(blocks), block(OmShape<Q, HD, HPB>::THREADS);
+static void omerge_launch_h(const OMergeArgs& a, hipStream_t stream, int nr, int wm, int blocks) {
+  const dim3 grid(blocks);
+  if (wm == 2) {
+    const dim3 block(OmShape<HD, HPB, 2>::THREADS);
+    switch (nr) {
+      case 1: hipLaunchKernelGGL((omerge_kernel<Q, HD, HPB, 1, 2>), grid, block, 0, stream, a); break;
+      case 2: hipLaunchKernelGGL((omerge_kernel<Q, HD, HPB, 2, 2>), grid, block, 0, stream, a); break;
+      case 4: hipLaunchKernelGGL((omerge_kernel<Q, HD, HPB, 4, 2>), grid, block, 0, stream, a); break;
+      default: hipLaunchKernelGGL((omerge_kernel<Q, HD, HPB, 8, 2>), grid, block, 0, stream, a); break;
+    }
+    return;
+  }
+  const dim3 block(OmShape<HD, HPB, 1>::THREADS);
   switch (nr) {
-    case 1: hipLaunchKernelGGL((omerge_kernel<Q, HD, HPB, 1>), grid, block, 0, stream, a); break;
-    case 2: hipLaunchKernelGGL((omerge_kernel<Q, HD, HPB, 2>), grid, block, 0, stream, a); break;
-    case 4: hipLaunchKernelGGL((omerge_kernel<Q, HD, HPB, 4>), grid, block, 0, stream, a); break;
-    case 8: hipLaunchKernelGGL((omerge_kernel<Q, HD, HPB, 8>), grid, block, 0, stream, a); break;
-    default: hipLaunchKernelGGL((omerge_kernel<Q, HD, HPB, 16>), grid, block, 0, stream, a); break;
+    case 1: hipLaunchKernelGGL((omerge_kernel<Q, HD, HPB, 1, 1>), grid, block, 0, stream, a); break;
+    case 2: hipLaunchKernelGGL((omerge_kernel<Q, HD, HPB, 2, 1>), grid, block, 0, stream, a); break;
+    case 4: hipLaunchKernelGGL((omerge_kernel<Q, HD, HPB, 4, 1>), grid, block, 0, stream, a); break;
+    case 8: hipLaunchKernelGGL((omerge_kernel<Q, HD, HPB, 8, 1>), grid, block, 0, stream, a); break;
+    default: hipLaunchKernelGGL((omerge_kernel<Q, HD, HPB, 16, 1>), grid, block, 0, stream, a); break;
   }
 }
 
 template <int Q, int HD>
-static void omerge_launch_q(const OMergeArgs& a, hipStream_t stream, int hpb, int nr, int blocks) {
+static void omerge_launch_q(const OMergeArgs& a, hipStream_t stream, int hpb, int nr, int wm, int blocks) {
   if constexpr (HD == 64) {
-    if (hpb == 2) return omerge_launch_h<Q, HD, 2>(a, stream, nr, blocks);
+    if (hpb == 2) return omerge_launch_h<Q, HD, 2>(a, stream, nr, wm, blocks);
   }
-  omerge_launch_h<Q, HD, 1>(a, stream, nr, blocks);
+  omerge_launch_h<Q, HD, 1>(a, stream, nr, wm, blocks);
 }
 
 // ------------------------------------------------------------ Wo panels
@@ -286,23 +299,26 @@ int wo_to_panels(int quant, void* W, __half* S, int N, int K, void* tmp, hipStre
 // Heads per block: one 128-column panel (two heads at head_dim 64, when the
 // head count is even).  Bands per head group: as many as fit one block per
 // CU (7B: 28 heads x 9 bands = 252 blocks), more when a band would need more
-// than 16 rounds of row loads.
-int omerge_plan(int quant, int head_dim, int n_heads, int N, int* hpb, int* bands, int* rounds) {
+// than 16 rounds of row loads.  Bands that need more than 4 rounds with the
+// base wave count (int8 / fp16 at 7B, 14B) run twice the waves.
+int omerge_plan(int quant, int head_dim, int n_heads, int N, int* hpb, int* bands, int* rounds, int* wm) {
   const int epc = quant == CQ_QUANT_INT4 ? 32 : quant == CQ_QUANT_INT8 ? 16 : 8;
   const int h = (head_dim == 64 && n_heads % 2 == 0) ? 2 : 1;
   const int nch = h * head_dim / epc;
-  const int rpr = (h * head_dim / kOmDims) * (kWave / nch);
+  const int rpr1 = (h * head_dim / kOmDims) * (kWave / nch);
   const int groups = n_heads / h;
   int b = std::max(1, kNumCUs / groups);
-  b = std::max(b, (N + 16 * rpr - 1) / (16 * rpr));
+  b = std::max(b, (N + 16 * rpr1 - 1) / (16 * rpr1));
   b = std::min(b, N);
   const int rows = (N + b - 1) / b;
-  const int nr = (rows + rpr - 1) / rpr;
+  int w = (rows + rpr1 - 1) / rpr1 > 4 ? 2 : 1;
+  const int nr = (rows + w * rpr1 - 1) / (w * rpr1);
   int p2 = 1;
   while (p2 < nr) p2 <<= 1;
   *hpb = h;
   *bands = b;
   *rounds = p2;
+  *wm = w;
   return CQ_OK;
 }
 
@@ -315,18 +331,18 @@ int launch_omerge(const OMergeArgs& a0, hipStream_t stream) {
   if (!a.workspace || !a.attn || !a.W || !a.acc || !a.d_pos || (a.quant != CQ_QUANT_FP16 && !a.S))
     return fail(CQ_EINVAL, "omerge: null pointer");
   if (a.Pmax <= 0) return fail(CQ_EINVAL, "omerge: bad partition count");
-  int hpb = 1, nr = 1;
-  omerge_plan(a.quant, a.head_dim, a.n_heads, a.N, &hpb, &a.bands, &nr);
+  int hpb = 1, nr = 1, wm = 1;
+  omerge_plan(a.quant, a.head_dim, a.n_heads, a.N, &hpb, &a.bands, &nr, &wm);
   const int blocks = a.n_heads / hpb * a.bands;
   if (a.quant == CQ_QUANT_INT4) {
-    if (a.head_dim == 128) omerge_launch_q<CQ_QUANT_INT4, 128>(a, stream, hpb, nr, blocks);
-    else omerge_launch_q<CQ_QUANT_INT4, 64>(a, stream, hpb, nr, blocks);
+    if (a.head_dim == 128) omerge_launch_q<CQ_QUANT_INT4, 128>(a, stream, hpb, nr, wm, blocks);
+    else omerge_launch_q<CQ_QUANT_INT4, 64>(a, stream, hpb, nr, wm, blocks);
   } else if (a.quant == CQ_QUANT_INT8) {
-    if (a.head_dim == 128) omerge_launch_q<CQ_QUANT_INT8, 128>(a, stream, hpb, nr, blocks);
-    else omerge_launch_q<CQ_QUANT_INT8, 64>(a, stream, hpb, nr, blocks);
+    if (a.head_dim == 128) omerge_launch_q<CQ_QUANT_INT8, 128>(a, stream, hpb, nr, wm, blocks);
+    else omerge_launch_q<CQ_QUANT_INT8, 64>(a, stream, hpb, nr, wm, blocks);
   } else {
-    if (a.head_dim == 128) omerge_launch_q<CQ_QUANT_FP16, 128>(a, stream, hpb, nr, blocks);
-    else omerge_launch_q<CQ_QUANT_FP16, 64>(a, stream, hpb, nr, blocks);
+    if (a.head_dim == 128) omerge_launch_q<CQ_QUANT_FP16, 128>(a, stream, hpb, nr, wm, blocks);
+    else omerge_launch_q<CQ_QUANT_FP16, 64>(a, stream, hpb, nr, wm, blocks);
   }
   CQ_HIP(hipGetLastError());
   return CQ_OK;
