@@ -147,7 +147,10 @@ constexpr int kNormMaxK = 16384;
 template <int Q, bool NORM, int BLK>
 struct XStage {
   static constexpr int P = QTraits<Q>::PLANES;
-  static constexpr int XB = NORM ? (kNormMaxK / QTraits<Q>::EPC + BLK - 1) / BLK : 1;
+  // chunk slots per thread in one batch: all of x with the norm fused; without
+  // it at least 512 chunks per batch (a 256-thread block would otherwise
+  // stage the 304 chunks of the K=4864 int8 GEMV in two dependent round trips)
+  static constexpr int XB = NORM ? (kNormMaxK / QTraits<Q>::EPC + BLK - 1) / BLK : (BLK < 512 ? 512 / BLK : 1);
   u4_t x[XB][P];
   u4_t w[NORM ? XB : 1][P];
 };
