@@ -288,6 +288,26 @@ def test_config3_qwen15b_int4_decode_parity():
     assert _prefilled_parity(cfg, 4096, 256, 42) >= 200
 
 
+@pytest.mark.parametrize("n_heads,n_kv,hd,quant", [(4, 1, 64, 2), (2, 2, 128, 1), (4, 2, 64, 0)])
+def test_merged_o_projection_over_64_partitions(n_heads, n_kv, hd, quant):
+    """With one or two KV heads the attention splits a long context into more
+    than 64 partitions per KV head (here 79 at 20,000 positions), so the
+    merged attention + O-projection merges its partials in several 64-row
+    chunks with the running max / sum; checked against the oracle."""
+    cfg = tiny_config(quant, n_heads=n_heads, n_kv_heads=n_kv, head_dim=hd, max_seq_len=20480)
+    assert _prefilled_parity(cfg, 20000, 4, 11) >= 0
+
+
+def test_config3_shapes_qwen15b_int4_20k():
+    """Qwen2.5-1.5B INT4 shapes (2 KV heads: 128 partition slots per head) at
+    20,000 positions, 2 of 28 layers: the merged O-projection's multi-chunk
+    merge at a real head layout."""
+    cfg = cq.preset("1.5B", "int4")
+    cfg.n_layers = 2
+    cfg.max_seq_len = 20480
+    assert _prefilled_parity(cfg, 20000, 4, 5) >= 2
+
+
 def test_config5_shapes_qwen14b_int4_32k():
     """BASELINE config 5 shapes (Qwen2.5-14B INT4: d 5120, I 13824, 40 q / 8
     kv heads, int8 lm_head) at the full 32K context, with 4 of the 48 layers
