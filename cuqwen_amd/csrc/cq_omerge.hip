@@ -234,12 +234,9 @@ static void omerge_launch_h(const OMergeArgs& a, hipStream_t stream, int nr, int
   const dim3 grid(blocks);
   if (wm == 2) {
     const dim3 block(OmShape<HD, HPB, 2>::THREADS);
-    switch (nr) {
-      case 1: hipLaunchKernelGGL((omerge_kernel<Q, HD, HPB, 1, 2>), grid, block, 0, stream, a); break;
-      case 2: hipLaunchKernelGGL((omerge_kernel<Q, HD, HPB, 2, 2>), grid, block, 0, stream, a); break;
-      case 4: hipLaunchKernelGGL((omerge_kernel<Q, HD, HPB, 4, 2>), grid, block, 0, stream, a); break;
-      default: hipLaunchKernelGGL((omerge_kernel<Q, HD, HPB, 8, 2>), grid, block, 0, stream, a); break;
-    }
+    // twice the waves only when one wave set needed more than 4 rounds: 4 or 8 remain
+    if (nr <= 4) hipLaunchKernelGGL((omerge_kernel<Q, HD, HPB, 4, 2>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((omerge_kernel<Q, HD, HPB, 8, 2>), grid, block, 0, stream, a);
     return;
   }
   const dim3 block(OmShape<HD, HPB, 1>::THREADS);
@@ -252,12 +249,11 @@ static void omerge_launch_h(const OMergeArgs& a, hipStream_t stream, int nr, int
   }
 }
 
+// head_dim 64 always pairs heads (the config check makes n_heads * 64 a
+// multiple of 128, so the head count is even)
 template <int Q, int HD>
-static void omerge_launch_q(const OMergeArgs& a, hipStream_t stream, int hpb, int nr, int wm, int blocks) {
-  if constexpr (HD == 64) {
-    if (hpb == 2) return omerge_launch_h<Q, HD, 2>(a, stream, nr, wm, blocks);
-  }
-  omerge_launch_h<Q, HD, 1>(a, stream, nr, wm, blocks);
+static void omerge_launch_q(const OMergeArgs& a, hipStream_t stream, int nr, int wm, int blocks) {
+  omerge_launch_h<Q, HD, HD == 64 ? 2 : 1>(a, stream, nr, wm, blocks);
 }
 
 // ------------------------------------------------------------ Wo panels
@@ -296,14 +292,13 @@ int wo_to_panels(int quant, void* W, __half* S, int N, int K, void* tmp, hipStre
   return CQ_OK;
 }
 
-// Heads per block: one 128-column panel (two heads at head_dim 64, when the
-// head count is even).  Bands per head group: as many as fit one block per
+// Heads per block: one 128-column panel (two heads at head_dim 64).  Bands per head group: as many as fit one block per
 // CU (7B: 28 heads x 9 bands = 252 blocks), more when a band would need more
 // than 16 rounds of row loads.  Bands that need more than 4 rounds with the
 // base wave count (int8 / fp16 at 7B, 14B) run twice the waves.
 int omerge_plan(int quant, int head_dim, int n_heads, int N, int* hpb, int* bands, int* rounds, int* wm) {
   const int epc = quant == CQ_QUANT_INT4 ? 32 : quant == CQ_QUANT_INT8 ? 16 : 8;
-  const int h = (head_dim == 64 && n_heads % 2 == 0) ? 2 : 1;
+  const int h = head_dim == 64 ? 2 : 1;
   const int nch = h * head_dim / epc;
   const int rpr1 = (h * head_dim / kOmDims) * (kWave / nch);
   const int groups = n_heads / h;
@@ -327,7 +322,7 @@ int launch_omerge(const OMergeArgs& a0, hipStream_t stream) {
   if (a.head_dim != 64 && a.head_dim != 128) return fail(CQ_EINVAL, "omerge: head_dim must be 64 or 128");
   if (a.quant < 0 || a.quant > 2) return fail(CQ_EINVAL, "omerge: bad quant type");
   if (a.n_kv <= 0 || a.n_heads % a.n_kv || a.n_heads / a.n_kv > 16) return fail(CQ_EINVAL, "omerge: bad head layout");
-  if (a.K != a.n_heads * a.head_dim || a.N <= 0) return fail(CQ_EINVAL, "omerge: bad shape");
+  if (a.K != a.n_heads * a.head_dim || a.N <= 0 || a.K % kGroup) return fail(CQ_EINVAL, "omerge: bad shape");
   if (!a.workspace || !a.attn || !a.W || !a.acc || !a.d_pos || (a.quant != CQ_QUANT_FP16 && !a.S))
     return fail(CQ_EINVAL, "omerge: null pointer");
   if (a.Pmax <= 0) return fail(CQ_EINVAL, "omerge: bad partition count");
@@ -335,14 +330,14 @@ int launch_omerge(const OMergeArgs& a0, hipStream_t stream) {
   omerge_plan(a.quant, a.head_dim, a.n_heads, a.N, &hpb, &a.bands, &nr, &wm);
   const int blocks = a.n_heads / hpb * a.bands;
   if (a.quant == CQ_QUANT_INT4) {
-    if (a.head_dim == 128) omerge_launch_q<CQ_QUANT_INT4, 128>(a, stream, hpb, nr, wm, blocks);
-    else omerge_launch_q<CQ_QUANT_INT4, 64>(a, stream, hpb, nr, wm, blocks);
+    if (a.head_dim == 128) omerge_launch_q<CQ_QUANT_INT4, 128>(a, stream, nr, wm, blocks);
+    else omerge_launch_q<CQ_QUANT_INT4, 64>(a, stream, nr, wm, blocks);
   } else if (a.quant == CQ_QUANT_INT8) {
-    if (a.head_dim == 128) omerge_launch_q<CQ_QUANT_INT8, 128>(a, stream, hpb, nr, wm, blocks);
-    else omerge_launch_q<CQ_QUANT_INT8, 64>(a, stream, hpb, nr, wm, blocks);
+    if (a.head_dim == 128) omerge_launch_q<CQ_QUANT_INT8, 128>(a, stream, nr, wm, blocks);
+    else omerge_launch_q<CQ_QUANT_INT8, 64>(a, stream, nr, wm, blocks);
   } else {
-    if (a.head_dim == 128) omerge_launch_q<CQ_QUANT_FP16, 128>(a, stream, hpb, nr, wm, blocks);
-    else omerge_launch_q<CQ_QUANT_FP16, 64>(a, stream, hpb, nr, wm, blocks);
+    if (a.head_dim == 128) omerge_launch_q<CQ_QUANT_FP16, 128>(a, stream, nr, wm, blocks);
+    else omerge_launch_q<CQ_QUANT_FP16, 64>(a, stream, nr, wm, blocks);
   }
   CQ_HIP(hipGetLastError());
   return CQ_OK;
