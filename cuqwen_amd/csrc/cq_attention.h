@@ -12,7 +12,7 @@ namespace cq {
 constexpr int kAttnWaves = 8;
 constexpr int kAttnThreads = kAttnWaves * kWave;
 constexpr int kAttnBlocksTarget = 256;   // one block per CU of MI355X
-constexpr int kMinTilesPerPart = 8;      // 256 keys: one tile per wave at least
+constexpr int kMinTilesPerPart = 1;      // short contexts spread over as many blocks as the slots allow
 constexpr int kTileKeys = 32;
 
 template <int HD>
