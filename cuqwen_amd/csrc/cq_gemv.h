@@ -323,18 +323,21 @@ struct StepBuf {
 template <int Q, int MODE, int R, int U, bool G128>
 __device__ __forceinline__ void load_step(const GemvArgs& a, StepBuf<R, U>& b, int unit, int kb, int NC, int lane) {
   using T = QTraits<Q>;
-  const int64_t rbytes = (int64_t)NC * 16;
-  const int sstride = G128 ? a.K / kGroup : 1;
+  // 32-bit offsets (every matrix is below 2 GiB, host-checked): the
+  // prologue's address arithmetic runs on the CU's one scalar unit for all
+  // its waves at once, and 64-bit multiplies cost it several instructions each
+  const uint32_t rbytes = (uint32_t)NC * 16u;
+  const uint32_t sstride = G128 ? (uint32_t)(a.K / kGroup) : 1u;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const RowRef rr = row_of<MODE, R>(a, unit, r);
-    const char* rp = reinterpret_cast<const char*>(sel3(a.W, rr.mat)) + (int64_t)rr.row * rbytes;
+    const char* rp = reinterpret_cast<const char*>(sel3(a.W, rr.mat)) + (uint32_t)rr.row * rbytes;
     const _Float16* sp = nullptr;
-    if constexpr (quantized<Q>()) sp = reinterpret_cast<const _Float16*>(sel3(a.S, rr.mat)) + (int64_t)rr.row * sstride;
+    if constexpr (quantized<Q>()) sp = reinterpret_cast<const _Float16*>(sel3(a.S, rr.mat)) + (uint32_t)rr.row * sstride;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int c = min(kb * (kWave * U) + u * kWave + lane, NC - 1);
-      b.w[u][r] = load_u4_stream(rp + (int64_t)c * 16);
+      b.w[u][r] = load_u4_stream(rp + (uint32_t)c * 16u);
       if constexpr (quantized<Q>()) b.sc[u][r] = sp[G128 ? (c * T::EPC) / kGroup : 0];
     }
   }

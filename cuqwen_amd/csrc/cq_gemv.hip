@@ -85,8 +85,9 @@ __global__ __launch_bounds__(BLK) void gemv_kernel(const GemvArgs a) {
   // per-unit quantity is wave-uniform and keeps the unit / k-step / row
   // address arithmetic in scalar registers (and the loop a scalar loop)
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  const int u_begin = (int)(((int64_t)blockIdx.x * n_units) / gridDim.x);
-  const int u_end = (int)(((int64_t)(blockIdx.x + 1) * n_units) / gridDim.x);
+  // 32-bit: n_units * gridDim.x < 2^31 (host-checked)
+  const int u_begin = (int)((blockIdx.x * (uint32_t)n_units) / gridDim.x);
+  const int u_end = (int)(((blockIdx.x + 1) * (uint32_t)n_units) / gridDim.x);
   const int u_last = max(u_end - 1, min(u_begin, n_units - 1));   // always a valid unit
   const int NB = (NC + kWave * U - 1) / (kWave * U);
   if (threadIdx.x == 0) next_unit = u_begin + 2 * WPB;   // published by the staging barrier
@@ -291,6 +292,9 @@ int gemv_check(const GemvArgs& a) {
   if (lds > 60 * 1024) return fail(CQ_EINVAL, "gemv: input vector too long for LDS staging");
   if (a.norm_w && a.K > kNormMaxK) return fail(CQ_EINVAL, "gemv: fused RMSNorm supports K <= 16384");
   if (a.argmax_out && a.mode != GM_STORE) return fail(CQ_EINVAL, "gemv: argmax keys need the store mode");
+  // the kernel's address and unit arithmetic is 32-bit
+  if ((int64_t)a.N * a.K * (a.quant == CQ_QUANT_FP16 ? 2 : 1) >= ((int64_t)1 << 31) || (int64_t)a.N * 2 * kNumCUs * 16 >= ((int64_t)1 << 31))
+    return fail(CQ_EINVAL, "gemv: matrix too large (2 GiB per weight matrix)");
   if (a.x_acc && (a.mode != GM_SWIGLU || !a.norm_w || !a.x_out))
     return fail(CQ_EINVAL, "gemv: the accumulator prologue needs swiglu, a fused norm and x_out");
   if ((a.resid || a.zero) && a.mode != GM_RESID) return fail(CQ_EINVAL, "gemv: resid / zero are residual-mode options");
