@@ -162,26 +162,45 @@ __global__ __launch_bounds__(kArgmaxReduceThreads) void argmax_stage2(const unsi
                                                                      int* tokens_out, StepBegin next) {
   __shared__ unsigned long long red[16];
   __shared__ int next_token;
+  // The control block is read once, up front, in flight with the keys:
+  // nothing else touches it during this launch, and field-by-field reads
+  // behind the stores below would each be a dependent memory round trip.
+  // all kernel arguments in the first scalar batch
+  CQ_PIN(partials); CQ_PIN(n); CQ_PIN(ctl); CQ_PIN(d_token_out); CQ_PIN(history); CQ_PIN(tokens_out);
+  CQ_PIN(next.embed); CQ_PIN(next.x); CQ_PIN(next.dim); CQ_PIN(next.stamp);
+  // every key of a thread requested before the first is waited for
+  constexpr int kPer = 8;
+  unsigned long long k[kPer];
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    // clamped, not branched (a repeated key leaves the maximum unchanged)
+    k[j] = partials[min((int)threadIdx.x + j * kArgmaxReduceThreads, n - 1)];
+  }
+  StepCtl c{};
+  if (ctl && threadIdx.x == 0) c = *ctl;
   unsigned long long v = 0ull;
-  for (int i = threadIdx.x; i < n; i += kArgmaxReduceThreads) v = partials[i] > v ? partials[i] : v;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) v = k[j] > v ? k[j] : v;
+  for (int i = threadIdx.x + kPer * kArgmaxReduceThreads; i < n; i += kArgmaxReduceThreads)
+    v = partials[i] > v ? partials[i] : v;
   const unsigned long long b = block_max_u64(v, red);
   if (threadIdx.x == 0) {
     const int token = (int)(~(uint32_t)(b & 0xffffffffu));
     if (d_token_out) *d_token_out = token;
     if (ctl) {
       ctl->sampled = token;
-      if (tokens_out) tokens_out[ctl->step] = token;
-      ctl->step += 1;
+      if (tokens_out) tokens_out[c.step] = token;
+      ctl->step = c.step + 1;
       int chained = -1;
-      if (ctl->chain) {
+      if (c.chain) {
         ctl->token = token;
-        ctl->pos += 1;
-        if (ctl->history_len < ctl->max_history) {
-          history[ctl->history_len] = token;
-          ctl->history_len += 1;
+        ctl->pos = c.pos + 1;
+        if (c.history_len < c.max_history) {
+          history[c.history_len] = token;
+          ctl->history_len = c.history_len + 1;
           // the history only grows within a chained decode, so the epoch
           // stays and only the appended id needs its stamp
-          if (next.stamp) next.stamp[token] = ctl->epoch;
+          if (next.stamp) next.stamp[token] = c.epoch;
         }
         chained = token;
       }
