@@ -43,7 +43,7 @@ __device__ __forceinline__ void pin_args(const GemvArgs& a) {
   if constexpr (MODE == GM_STORE) {
     CQ_PIN(a.bias[0]); CQ_PIN(a.stamp); CQ_PIN(a.d_epoch); CQ_PIN(a.argmax_out); CQ_PIN(a.penalty);
   }
-  if constexpr (MODE == GM_RESID) { CQ_PIN(a.resid); CQ_PIN(a.zero); }
+  if constexpr (MODE == GM_RESID) { CQ_PIN(a.resid); CQ_PIN(a.zero); CQ_PIN(a.zero_n); }
   if constexpr (ADD) { CQ_PIN(a.x_acc); CQ_PIN(a.x_out); }
 }
 

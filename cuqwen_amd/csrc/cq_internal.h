@@ -7,13 +7,17 @@ namespace cq {
 
 enum GemvMode { GM_STORE = 0, GM_RESID = 1, GM_SWIGLU = 2, GM_QKV = 3 };
 
+// Fields ordered so that the struct has no padding holes: the kernels read
+// their arguments in a few wide scalar loads, and a dead padding word inside
+// one lets the register allocator reuse its register for a later argument
+// load, which then has to wait for the whole first batch.
 struct GemvArgs {
   int mode = GM_STORE;
   int quant = CQ_QUANT_FP16;
   int group = kGroup;           // 128, or 0 for one scale per row
+  float eps = 1e-6f;            // fused RMSNorm epsilon
   const __half* x = nullptr;    // input vector [K]
   const __half* norm_w = nullptr;  // fused RMSNorm weight (nullptr: x is used as is)
-  float eps = 1e-6f;
   int K = 0;                    // contraction length
   int N = 0;                    // output rows (SWIGLU: inter rows; QKV: qd + 2 kvd)
   const void* W[3] = {nullptr, nullptr, nullptr};      // QKV: q,k,v  SWIGLU: gate, up
@@ -21,17 +25,17 @@ struct GemvArgs {
   const __half* bias[3] = {nullptr, nullptr, nullptr};
   __half* out[3] = {nullptr, nullptr, nullptr};        // RESID: out[0] is read and written
   // QKV / RoPE / KV store
-  int n_heads = 0, n_kv = 0, head_dim = 0;
-  const int* d_pos = nullptr;
+  int n_heads = 0, n_kv = 0;
+  int head_dim = 0;
   float rope_theta = 1e6f;
+  const int* d_pos = nullptr;
   const double* rope_inv_freq = nullptr;   // [head_dim/2] theta^(-2i/hd); nullptr: computed on the device
   __half* kcache = nullptr;     // layer slice, tiled layout (kv_k_offset)
   __half* vcache = nullptr;
   int max_seq = 0;
-  // repetition penalty applied to the stored value (logits)
+  float penalty = 1.f;          // repetition penalty applied to the stored value (logits)
   const uint32_t* stamp = nullptr;
   const uint32_t* d_epoch = nullptr;
-  float penalty = 1.f;
   // STORE mode: each wave writes the argmax key of the rows it stored to
   // argmax_out[wave] (at most kArgmaxPartials waves)
   unsigned long long* argmax_out = nullptr;
