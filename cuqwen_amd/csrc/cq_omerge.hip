@@ -76,11 +76,16 @@ __global__ __launch_bounds__(HPB * HD / kOmDims * WM * kWave) void omerge_kernel
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  const int g = om_order(blockIdx.x, gridDim.x);
-  const int hq0 = (g / a.bands) * HPB, band = g % a.bands;
-  const int row0 = (int)(((int64_t)band * a.N) / a.bands);
-  const int row1 = (int)(((int64_t)(band + 1) * a.N) / a.bands);
-  const int gsz = a.n_heads / a.n_kv;
+  // Unsigned 32-bit index arithmetic throughout (every offset here is far
+  // below 2^31, host-checked): the prologue's address math runs on the CU's
+  // one scalar unit for every resident wave, and signed or 64-bit division
+  // and multiplication cost it several times the instructions.
+  const uint32_t g = om_order(blockIdx.x, gridDim.x);
+  const uint32_t bands = (uint32_t)a.bands, N = (uint32_t)a.N, Pmax = (uint32_t)a.Pmax;
+  const int hq0 = (int)(g / bands) * HPB, band = (int)(g % bands);
+  const int row0 = (int)(((uint32_t)band * N) / bands);
+  const int row1 = (int)(((uint32_t)(band + 1) * N) / bands);
+  const uint32_t gsz = (uint32_t)(a.n_heads / a.n_kv);
 
   // 1. the first 64 partitions of the block's heads, read coalesced: the
   //    partials are head-major (a head's partitions are contiguous 512-byte
@@ -90,11 +95,11 @@ __global__ __launch_bounds__(HPB * HD / kOmDims * WM * kWave) void omerge_kernel
   //    them -- for microseconds.)  Independent of the position: rows past the
   //    partition count are weighted 0 below.
   const float* ws_m = reinterpret_cast<const float*>(a.workspace);
-  const float* ws_l = ws_m + (size_t)a.n_kv * a.Pmax * 16;
-  const float* ws_o = ws_l + (size_t)a.n_kv * a.Pmax * 16;
+  const float* ws_l = ws_m + (uint32_t)a.n_kv * Pmax * 16u;
+  const float* ws_o = ws_l + (uint32_t)a.n_kv * Pmax * 16u;
   auto head_base = [&](int j) {
-    const int hq = hq0 + j;
-    return ((size_t)(hq / gsz) * 16 + hq % gsz) * a.Pmax;
+    const uint32_t hq = (uint32_t)(hq0 + j);
+    return ((hq / gsz) * 16u + hq % gsz) * Pmax;
   };
   const int rsub = lane / LPR, d4 = (lane % LPR) * 4;
   float mp[HPB], lp[HPB];
@@ -102,20 +107,20 @@ __global__ __launch_bounds__(HPB * HD / kOmDims * WM * kWave) void omerge_kernel
   auto load_chunk = [&](int p0) {
 #pragma unroll
     for (int j = 0; j < HPB; ++j) {
-      const size_t base = head_base(j);
-      mp[j] = ws_m[base + min(p0 + lane, a.Pmax - 1)];
-      lp[j] = ws_l[base + min(p0 + lane, a.Pmax - 1)];
+      const uint32_t base = head_base(j);
+      mp[j] = ws_m[base + (uint32_t)min(p0 + lane, a.Pmax - 1)];
+      lp[j] = ws_l[base + (uint32_t)min(p0 + lane, a.Pmax - 1)];
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
         const int p = p0 + (i * WAVES + wave) * RPI + rsub;
-        ov[j][i] = *reinterpret_cast<const f4_t*>(ws_o + (base + min(p, a.Pmax - 1)) * HD + d4);
+        ov[j][i] = *reinterpret_cast<const f4_t*>(ws_o + (base + (uint32_t)min(p, a.Pmax - 1)) * HD + d4);
       }
     }
   };
   load_chunk(0);
   // the single-partition case finds the normalised output where stage 1 wrote it
   uint32_t direct = 0;
-  const _Float16* xb = reinterpret_cast<const _Float16*>(a.attn) + (size_t)hq0 * HD;
+  const _Float16* xb = reinterpret_cast<const _Float16*>(a.attn) + (uint32_t)hq0 * HD;
   if (threadIdx.x < W / 2) direct = reinterpret_cast<const uint32_t*>(xb)[threadIdx.x];
   const int T_ = (int)load_ctl_u32(a.d_pos) + 1;
 
@@ -127,14 +132,14 @@ __global__ __launch_bounds__(HPB * HD / kOmDims * WM * kWave) void omerge_kernel
   const int cch = lane % NCH;
   const int kc = hq0 * HD / T::EPC + cch;   // this lane's chunk within a row
   const int pan = kc / CP;
-  const char* wbase = reinterpret_cast<const char*>(a.W) + ((size_t)pan * a.N * CP + kc % CP) * 16;
-  const _Float16* sbase = reinterpret_cast<const _Float16*>(a.S) + (size_t)pan * a.N;   // scales [panel][N]
+  const char* wbase = reinterpret_cast<const char*>(a.W) + ((uint32_t)pan * N * CP + kc % CP) * 16u;
+  const _Float16* sbase = reinterpret_cast<const _Float16*>(a.S) + (uint32_t)pan * N;   // scales [panel][N]
   u4_t wv[NR];
   _Float16 sc[NR];
 #pragma unroll
   for (int r = 0; r < NR; ++r) {
     const int row = min(row0 + r * RPR + wave * RPW + lane / NCH, row1 - 1);
-    wv[r] = load_u4_stream(wbase + (size_t)row * CP * 16);
+    wv[r] = load_u4_stream(wbase + (uint32_t)row * (CP * 16u));
     if constexpr (Q != CQ_QUANT_FP16) sc[r] = sbase[row];
   }
 
@@ -326,6 +331,10 @@ int launch_omerge(const OMergeArgs& a0, hipStream_t stream) {
   if (!a.workspace || !a.attn || !a.W || !a.acc || !a.d_pos || (a.quant != CQ_QUANT_FP16 && !a.S))
     return fail(CQ_EINVAL, "omerge: null pointer");
   if (a.Pmax <= 0) return fail(CQ_EINVAL, "omerge: bad partition count");
+  // the kernel indexes in unsigned 32 bits: Wo bytes, the partial slots and the band rows
+  if ((int64_t)a.N * a.K * 2 >= ((int64_t)1 << 31) || (int64_t)a.n_kv * 16 * a.Pmax * a.head_dim >= ((int64_t)1 << 31) ||
+      (int64_t)a.N * (a.bands + 1) >= ((int64_t)1 << 31))
+    return fail(CQ_EINVAL, "omerge: shape too large for 32-bit indexing");
   int hpb = 1, nr = 1, wm = 1;
   omerge_plan(a.quant, a.head_dim, a.n_heads, a.N, &hpb, &a.bands, &nr, &wm);
   const int blocks = a.n_heads / hpb * a.bands;
