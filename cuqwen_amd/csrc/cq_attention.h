@@ -35,6 +35,39 @@ __device__ __forceinline__ void load_tile(KVTile<HD>& t, const _Float16* kbase, 
   for (int dt = 0; dt < HD / 16; ++dt) t.va[dt] = __builtin_bit_cast(h8_t, load_u4_stream(vt + (dt * 64 + lane) * 8));
 }
 
+// The K and V of one kv head read through buffer resources.  A tile past
+// the partition is read through a resource of zero records, which the
+// buffer unit answers with zeros and no memory request: every path of the
+// tile loop then issues the same loads, and the compiler's waits name
+// exactly the tile being attended (a load issued only on some paths leaves
+// it counting conservatively, i.e. waiting for the next tile's loads too).
+// The tile offset is a scalar (soffset) and the lane's offset a loop
+// invariant (voffset), so the loop writes no address registers.
+struct KVRes {
+  const _Float16* k;
+  const _Float16* v;
+  int bytes;   // one kv head's K (or V) slice
+};
+constexpr int kBufWord3 = 0x00020000;   // gfx9 buffer descriptor word 3: 32-bit data format
+
+template <int HD>
+__device__ __forceinline__ void load_tile(KVTile<HD>& t, const KVRes& r, int ti, bool valid, int lane) {
+  constexpr int kNT = 2;   // cache policy: non-temporal (streamed once)
+  const int n = valid ? r.bytes : 0;
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(r.k), (short)0, n, kBufWord3);
+  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(r.v), (short)0, n, kBufWord3);
+  const int soff = valid ? ti * (kTileKeys * HD * 2) : 0;
+#pragma unroll
+  for (int st = 0; st < 2; ++st)
+#pragma unroll
+    for (int kk = 0; kk < HD / 32; ++kk)
+      t.ka[st][kk] = __builtin_bit_cast(
+          h8_t, __builtin_amdgcn_raw_buffer_load_b128(rk, (st * 16 * HD + (kk * 64 + lane) * 8) * 2, soff, kNT));
+#pragma unroll
+  for (int dt = 0; dt < HD / 16; ++dt)
+    t.va[dt] = __builtin_bit_cast(h8_t, __builtin_amdgcn_raw_buffer_load_b128(rv, (dt * 64 + lane) * 8 * 2, soff, kNT));
+}
+
 // One 32-key tile of the online softmax for this wave.
 template <int HD>
 __device__ __forceinline__ void attend_tile(KVTile<HD>& t, const h8_t* qb, int ti, int T, float scale, int j,
@@ -118,16 +151,19 @@ __device__ __forceinline__ int attn_nparts(int T, int P, int* tpp_out) {
 // the wave's online-softmax state (l summed over the lane's 4 key slots).
 template <int HD>
 __device__ __forceinline__ void attend_partition(KVTile<HD>& A, KVTile<HD>& B, const h8_t* qb, int ti, int tile1,
-                                                 int T, const _Float16* kbase, const _Float16* vbase, int lane,
-                                                 float& m, float& l, f4_t* o) {
+                                                 int T, const KVRes& kv, int lane, float& m, float& l, f4_t* o) {
   const int j = lane >> 4;
   const float scale = 1.0f / sqrtf((float)HD);
   for (; ti < tile1; ti += 2 * kAttnWaves) {
     const int t1 = ti + kAttnWaves;
-    if (t1 < tile1) load_tile<HD>(B, kbase, vbase, t1, lane);
+    // the next tile's loads go out before the wait for this one (the
+    // scheduler would otherwise hoist this tile's MFMAs, and their wait, above them)
+    load_tile<HD>(B, kv, t1, t1 < tile1, lane);
+    __builtin_amdgcn_sched_barrier(0);
     attend_tile<HD>(A, qb, ti, T, scale, j, m, l, o);
     if (t1 >= tile1) break;
-    if (t1 + kAttnWaves < tile1) load_tile<HD>(A, kbase, vbase, t1 + kAttnWaves, lane);
+    load_tile<HD>(A, kv, t1 + kAttnWaves, t1 + kAttnWaves < tile1, lane);
+    __builtin_amdgcn_sched_barrier(0);
     attend_tile<HD>(B, qb, t1, T, scale, j, m, l, o);
   }
   l += __shfl_xor(l, 16, kWave);

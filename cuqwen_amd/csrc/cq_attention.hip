@@ -47,7 +47,8 @@ __global__ __launch_bounds__(kAttnThreads) void attention_stage1(const AttnArgs 
   const int kvh = blockIdx.y;
   const int part = blockIdx.x;
   const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
+  // wave-uniform, so the tile loop is a scalar loop with exact load counts
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int g = a.n_heads / a.n_kv;
   const int T = (int)load_ctl_u32(a.d_pos) + 1;
   const int n_tiles = (T + kTileKeys - 1) / kTileKeys;
@@ -63,9 +64,10 @@ __global__ __launch_bounds__(kAttnThreads) void attention_stage1(const AttnArgs 
   const _Float16* kbase = reinterpret_cast<const _Float16*>(a.kcache) + (int64_t)kvh * a.max_seq * HD;
   const _Float16* vbase = reinterpret_cast<const _Float16*>(a.vcache) + (int64_t)kvh * a.max_seq * HD;
 
+  const KVRes kv{kbase, vbase, a.max_seq * HD * 2};
   KVTile<HD> A, B;
   int ti = tile0 + wave;
-  if (ti < tile1) load_tile<HD>(A, kbase, vbase, ti, lane);
+  load_tile<HD>(A, kv, ti, ti < tile1, lane);
 
   // Q^T as the B operand: lane holds q[h][kk*32 + j*8 .. +8]
   h8_t qb[KK];
@@ -82,7 +84,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_stage1(const AttnArgs 
   f4_t o[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) o[dt] = f4_t{0.f, 0.f, 0.f, 0.f};
-  attend_partition<HD>(A, B, qb, ti, tile1, T, kbase, vbase, lane, m, l, o);
+  attend_partition<HD>(A, B, qb, ti, tile1, T, kv, lane, m, l, o);
   block_merge_write<HD>(a, kvh, part, nparts, g, m, l, o);
 }
 
@@ -246,6 +248,8 @@ static int attention_check(const AttnArgs& a) {
   if (a.n_kv <= 0 || a.n_heads % a.n_kv || a.n_heads / a.n_kv > 16 || a.n_kv > 64)
     return fail(CQ_EINVAL, "attention: need n_heads/n_kv_heads <= 16 and n_kv_heads <= 64");
   if (a.max_seq <= 0 || a.max_seq % kTileKeys) return fail(CQ_EINVAL, "attention: max_seq_len must be a multiple of 32");
+  // one kv head's K (or V) slice is read as a buffer resource (32-bit size)
+  if ((int64_t)a.max_seq * a.head_dim * 2 >= ((int64_t)1 << 31)) return fail(CQ_EINVAL, "attention: max_seq_len too large");
   const bool kv8 = a.kcache8 != nullptr;
   if (!a.q || !a.out || !a.d_pos || !a.workspace) return fail(CQ_EINVAL, "attention: null pointer");
   if (kv8 && a.kv_fmt != CQ_KV_INT8 && a.kv_fmt != CQ_KV_FP8) return fail(CQ_EINVAL, "attention: unknown KV code format");
