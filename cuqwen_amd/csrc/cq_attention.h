@@ -48,7 +48,6 @@ struct KVRes {
   const _Float16* v;
   int bytes;   // one kv head's K (or V) slice
 };
-constexpr int kBufWord3 = 0x00020000;   // gfx9 buffer descriptor word 3: 32-bit data format
 
 template <int HD>
 __device__ __forceinline__ void load_tile(KVTile<HD>& t, const KVRes& r, int ti, bool valid, int lane) {

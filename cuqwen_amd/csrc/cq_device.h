@@ -179,6 +179,17 @@ __device__ __forceinline__ u4_t load_u4(const void* p) { return *reinterpret_cas
 // used and a prologue waits for several dependent kernel-argument round
 // trips (≈0.35 us each) before its first streaming load.
 #define CQ_PIN(v) asm volatile("" ::"s"(v))
+// Buffer resource over `base` (word 3: the gfx9 32-bit data format), of
+// 2^31 - 1 bytes when `valid`, else of none: a load through the empty one
+// returns zeros at once without a memory request.  Lets a loop issue the
+// same loads on every path (exact wait counts) while steps past its range
+// cost nothing.
+constexpr int kBufWord3 = 0x00020000;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_or_null(const void* base, bool valid) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, valid ? 0x7fffffff : 0, kBufWord3);
+}
+constexpr int kCacheNT = 2;   // buffer load cache policy: non-temporal (streamed once)
+
 __device__ __forceinline__ u4_t load_u4_stream(const void* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(p));
 }

@@ -78,6 +78,12 @@ __global__ __launch_bounds__(BLK) void gemv_kernel(const GemvArgs a) {
   const int NC = a.K / T::EPC;
   u4_t* xs = smem;
   float* sx = reinterpret_cast<float*>(smem + T::PLANES * NC);
+  // SWIGLU: the block's output rows are collected in LDS and written after
+  // the loop.  A global store inside the loop, issued only
+  // when a unit finishes, is counted by vmcnt like the loads, and the
+  // compiler's waits after such a branch then also wait for the next step's
+  // weight loads, leaving the wave with nothing in flight while it computes.
+  _Float16* stash = reinterpret_cast<_Float16*>(sx + (Q != CQ_QUANT_FP16 ? NC : 0));
   const int lane = threadIdx.x & (kWave - 1);
   const int n_units = units_total<MODE, R>(a);
   constexpr int WPB = BLK / kWave;
@@ -90,6 +96,8 @@ __global__ __launch_bounds__(BLK) void gemv_kernel(const GemvArgs a) {
   const int u_end = (int)(((blockIdx.x + 1) * (uint32_t)n_units) / gridDim.x);
   const int u_last = max(u_end - 1, min(u_begin, n_units - 1));   // always a valid unit
   const int NB = (NC + kWave * U - 1) / (kWave * U);
+  constexpr int RPU = rows_per_unit<MODE, R>();
+  const int row_base = u_begin * RPU;
   if (threadIdx.x == 0) next_unit = u_begin + 2 * WPB;   // published by the staging barrier
 
   auto make = [&](int unit, int kb) {
@@ -158,11 +166,11 @@ __global__ __launch_bounds__(BLK) void gemv_kernel(const GemvArgs a) {
   Cursor ca = make(u_begin + wave, 0);
   Cursor cb = advance(ca);   // never claims: the first unit's next step or the second static unit
   // the first two steps are requested unconditionally (a cursor past the
-  // range reads a valid unit that is never used)
-  load_step<Q, MODE, R, U, G128>(a, A, ca.unit, ca.kb, NC, lane);
-  EpiPre pa = epi_prefetch<MODE, R>(a, ca.unit, lane);
-  load_step<Q, MODE, R, U, G128>(a, B, cb.unit, cb.kb, NC, lane);
-  EpiPre pb = epi_prefetch<MODE, R>(a, cb.unit, lane);
+  // range names a valid unit and loads zeros without a memory access)
+  load_step<Q, MODE, R, U, G128>(a, A, ca.unit, ca.kb, NC, lane, ca.real);
+  EpiPre pa = epi_prefetch<MODE, R>(a, ca.unit, lane, ca.real);
+  load_step<Q, MODE, R, U, G128>(a, B, cb.unit, cb.kb, NC, lane, cb.real);
+  EpiPre pb = epi_prefetch<MODE, R>(a, cb.unit, lane, cb.real);
   if constexpr (MODE == GM_QKV) inv_freq[min((int)threadIdx.x, a.head_dim / 2 - 1)] = rope_f;   // duplicates write equal values
   if constexpr (ADD) {
     // h = half(x + sum): the O-projection sum (fp32) plus the fp16
@@ -211,43 +219,67 @@ __global__ __launch_bounds__(BLK) void gemv_kernel(const GemvArgs a) {
   unsigned long long best = 0ull;   // STORE: argmax key of the rows this lane stored
   auto run_a = [&]() {
     compute_step<Q, R, U>(A, acc, xs, sx, ca.kb, NC, lane, uk);
-    if (ca.kb == NB - 1) finish_unit<MODE, R>(a, acc, ca.unit, lane, scale, pa, inv_freq, step_word, best);
+    if (ca.kb == NB - 1) finish_unit<MODE, R>(a, acc, ca.unit, lane, scale, pa, inv_freq, step_word, best, stash, row_base);
   };
   auto run_b = [&]() {
     compute_step<Q, R, U>(B, acc, xs, sx, cb.kb, NC, lane, uk);
-    if (cb.kb == NB - 1) finish_unit<MODE, R>(a, acc, cb.unit, lane, scale, pb, inv_freq, step_word, best);
+    if (cb.kb == NB - 1) finish_unit<MODE, R>(a, acc, cb.unit, lane, scale, pb, inv_freq, step_word, best, stash, row_base);
   };
-  // Steady state: A and B both hold real steps and each round refills both,
-  // so every load in the loop is unconditional and the compiler's load
-  // counters stay exact.  When the next step is past the wave's range the
-  // wave leaves the loop before issuing its loads (a load whose data is
-  // never used would still hold the wave until it returned) and finishes the
-  // buffer it still holds.
-  if (ca.real) {
-    if (!cb.real) {
+  if constexpr (gemv_buffer_loop<MODE>()) {
+    // A and B alternate; every half-round computes one buffer and refills it
+    // with the step after the other one, unconditionally (a step past the
+    // wave's range loads zeros without a memory access), so each compute
+    // waits for its own buffer only while the other one's loads stay in flight.
+    while (ca.real) {
       run_a();
-    } else {
-      while (true) {
+      ca = advance(cb);
+      load_step<Q, MODE, R, U, G128>(a, A, ca.unit, ca.kb, NC, lane, ca.real);
+      pa = epi_prefetch<MODE, R>(a, ca.unit, lane, ca.real);
+      if (!cb.real) break;
+      run_b();
+      cb = advance(ca);
+      load_step<Q, MODE, R, U, G128>(a, B, cb.unit, cb.kb, NC, lane, cb.real);
+      pb = epi_prefetch<MODE, R>(a, cb.unit, lane, cb.real);
+    }
+  } else {
+    // Steady state: A and B both hold real steps and each round refills both,
+    // so every load in the loop is unconditional and the compiler's load
+    // counters stay exact.  When the next step is past the wave's range the
+    // wave leaves the loop before issuing its loads (a load whose data is
+    // never used would still hold the wave until it returned) and finishes the
+    // buffer it still holds.
+    if (ca.real) {
+      if (!cb.real) {
         run_a();
-        const Cursor na = advance(cb);
-        if (!na.real) {
-          run_b();
-          break;
-        }
-        ca = na;
-        load_step<Q, MODE, R, U, G128>(a, A, ca.unit, ca.kb, NC, lane);
-        pa = epi_prefetch<MODE, R>(a, ca.unit, lane);
-        run_b();
-        const Cursor nb = advance(ca);
-        if (!nb.real) {
+      } else {
+        while (true) {
           run_a();
-          break;
+          const Cursor na = advance(cb);
+          if (!na.real) {
+            run_b();
+            break;
+          }
+          ca = na;
+          load_step<Q, MODE, R, U, G128>(a, A, ca.unit, ca.kb, NC, lane, true);
+          pa = epi_prefetch<MODE, R>(a, ca.unit, lane, true);
+          run_b();
+          const Cursor nb = advance(ca);
+          if (!nb.real) {
+            run_a();
+            break;
+          }
+          cb = nb;
+          load_step<Q, MODE, R, U, G128>(a, B, cb.unit, cb.kb, NC, lane, true);
+          pb = epi_prefetch<MODE, R>(a, cb.unit, lane, true);
         }
-        cb = nb;
-        load_step<Q, MODE, R, U, G128>(a, B, cb.unit, cb.kb, NC, lane);
-        pb = epi_prefetch<MODE, R>(a, cb.unit, lane);
       }
     }
+  }
+  if constexpr (MODE == GM_SWIGLU) {
+    __syncthreads();
+    _Float16* out = reinterpret_cast<_Float16*>(a.out[0]);
+    const int row_end = min(u_end * RPU, a.N);
+    for (int i = row_base + (int)threadIdx.x; i < row_end; i += BLK) out[i] = stash[i - row_base];
   }
   if constexpr (MODE == GM_RESID) {
     if (a.zero)
@@ -318,11 +350,14 @@ int launch_variant(const GemvArgs& a, hipStream_t stream, int max_blocks) {
   constexpr int kWavesPerBlock = BLK / kWave;
   using T = QTraits<Q>;
   const int NC = a.K / T::EPC;
-  const size_t lds = (size_t)T::PLANES * NC * 16 + (Q != CQ_QUANT_FP16 ? (size_t)NC * 4 : 0);
   const int units = units_total<MODE, R>(a);
   // persistent grid: up to max_blocks blocks, each owning a contiguous range
   // of at least one unit per wave
   const int blocks = std::max(1, std::min(max_blocks, (units + kWavesPerBlock - 1) / kWavesPerBlock));
+  // staged x (+ scales) and the output stash of the block's rows
+  const size_t stash = MODE != GM_SWIGLU ? 0 : (size_t)((units + blocks - 1) / blocks) * rows_per_unit<MODE, R>() * 2;
+  const size_t lds = (size_t)T::PLANES * NC * 16 + (Q != CQ_QUANT_FP16 ? (size_t)NC * 4 : 0) + stash;
+  if (lds > 64 * 1024) return fail(CQ_EINVAL, "gemv: input vector and output slice too long for LDS");
   if (a.argmax_out && blocks * kWavesPerBlock > kArgmaxPartials) return fail(CQ_EINVAL, "gemv: too many waves for the argmax slots");
   hipLaunchKernelGGL((gemv_kernel<Q, MODE, R, U, NORM, G128, BLK, ADD>), dim3(blocks), dim3(BLK), lds, stream, a);
   CQ_HIP(hipGetLastError());
