@@ -98,7 +98,8 @@ __global__ __launch_bounds__(kAttnThreads) void attention_stage1_kv8(const AttnA
   pin_attn_args<true>(a);
   constexpr int KK = HD / 32, DT = HD / 16, E = HD / kWave;
   const int kvh = blockIdx.y, part = blockIdx.x;
-  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);   // scalar tile loop
   const int g = a.n_heads / a.n_kv;
   const int pos = (int)load_ctl_u32(a.d_pos), T = pos + 1;
   const int n_tiles = (T + kTileKeys - 1) / kTileKeys;
