@@ -155,14 +155,10 @@ __device__ __forceinline__ void attend_partition(KVTile<HD>& A, KVTile<HD>& B, c
   const float scale = 1.0f / sqrtf((float)HD);
   for (; ti < tile1; ti += 2 * kAttnWaves) {
     const int t1 = ti + kAttnWaves;
-    // the next tile's loads go out before the wait for this one (the
-    // scheduler would otherwise hoist this tile's MFMAs, and their wait, above them)
     load_tile<HD>(B, kv, t1, t1 < tile1, lane);
-    __builtin_amdgcn_sched_barrier(0);
     attend_tile<HD>(A, qb, ti, T, scale, j, m, l, o);
     if (t1 >= tile1) break;
     load_tile<HD>(A, kv, t1 + kAttnWaves, t1 + kAttnWaves < tile1, lane);
-    __builtin_amdgcn_sched_barrier(0);
     attend_tile<HD>(B, qb, t1, T, scale, j, m, l, o);
   }
   l += __shfl_xor(l, 16, kWave);
