@@ -86,6 +86,7 @@ def _load():
         "cq_synth_weights": (I32, [CP, U64, ctypes.POINTER(P)]),
         "cq_free_weights": (I32, [P]),
         "cq_weights_tensor": (I32, [P, ctypes.c_char_p, I32, ctypes.POINTER(P), ctypes.POINTER(SZ)]),
+        "cq_weights_wo_rows": (I32, [P, I32, ctypes.POINTER(P), ctypes.POINTER(P)]),
         "cq_state_create": (I32, [CP, P, ctypes.POINTER(P)]),
         "cq_state_create_kv": (I32, [CP, P, I32, ctypes.POINTER(P)]),
         "cq_state_destroy": (I32, [P]),
@@ -161,7 +162,7 @@ def _load():
 lib = _load()
 EXPORTED = [
     "cq_last_error", "cq_config_preset", "cq_read_header", "cq_write_synthetic_file", "cq_load_weights",
-    "cq_synth_weights", "cq_free_weights", "cq_weights_tensor", "cq_state_create", "cq_state_destroy",
+    "cq_synth_weights", "cq_free_weights", "cq_weights_tensor", "cq_weights_wo_rows", "cq_state_create", "cq_state_destroy",
     "cq_forward", "cq_forward_ex", "cq_decode", "cq_state_logits", "cq_state_fill_kv", "cq_state_kv_read", "cq_state_kv_write",
     "cq_prefill", "cq_state_last_prefill_us", "cq_state_create_kv", "cq_gqa_attention_decode_kv8",
     "cq_gqa_attention_decode_fp8",

@@ -65,6 +65,24 @@ def build_compat_caller():
     if r.returncode != 0:
         raise RuntimeError(f"compat caller build failed:\n{r.stdout}\n{r.stderr}")
     os.replace(COMPAT_BIN + ".tmp", COMPAT_BIN)
+    # the op-level caller (benchmark/kernel_profile.cu's calls), one binary per
+    # preset and precision it is tested at
+    src = os.path.join(ROOT, "tests", "compat", "kernel_caller.cpp")
+    jobs = []
+    for model, quant in KERNEL_CALLER_BUILDS:
+        out = os.path.join(ROOT, "tests", "compat", f"kernel_caller_{model}_{quant}")
+        defs = [f"-DQWEN_MODEL_{model.upper()}"] + ([f"-DQUANT_{quant.upper()}"] if quant != "fp16" else [])
+        jobs.append(([HIPCC, "-O2", "-std=c++17", *defs, "-I", os.path.join(ROOT, "include"), src, "-L", HERE,
+                      "-lcuqwen", "-Wl,-rpath,$ORIGIN/../../cuqwen_amd", "-o", out + ".tmp"], out))
+    with concurrent.futures.ThreadPoolExecutor(max_workers=len(jobs)) as ex:
+        results = list(ex.map(lambda j: subprocess.run(j[0], capture_output=True, text=True), jobs))
+    for (cmd, out), r in zip(jobs, results):
+        if r.returncode != 0:
+            raise RuntimeError(f"kernel caller build failed ({out}):\n{r.stdout}\n{r.stderr}")
+        os.replace(out + ".tmp", out)
+
+
+KERNEL_CALLER_BUILDS = [("0_5b", "int8"), ("0_5b", "int4"), ("0_5b", "fp16"), ("1_5b", "int4")]
 
 
 if __name__ == "__main__":

@@ -36,6 +36,10 @@ struct cq_weights {
   // per tensor placement in the arena, in file order
   struct Slot { TensorSpec spec; size_t w_off, s_off; };
   std::vector<Slot> slots;
+  // exporter-layout (row-major) copy of every layer's Wo and its scales, made
+  // on the first cq_weights_wo_rows call; per layer wo_rows_stride bytes
+  char* wo_rows = nullptr;
+  size_t wo_rows_stride = 0, wo_rows_wbytes = 0;
 };
 
 namespace {
@@ -571,6 +575,7 @@ extern "C" int cq_synth_weights(const cq_config* cfg, uint64_t seed, cq_weights*
 
 extern "C" int cq_free_weights(cq_weights* w) {
   if (!w) return CQ_OK;
+  if (w->wo_rows) CQ_HIP(hipFree(w->wo_rows));
   if (w->arena) CQ_HIP(hipFree(w->arena));
   delete w;
   return CQ_OK;
@@ -604,6 +609,37 @@ extern "C" int cq_weights_tensor(const cq_weights* w, const char* name, int32_t 
     return fail(CQ_EINVAL, "weights_tensor: no such tensor for this layer / config");
   }
   return fail(CQ_EINVAL, std::string("weights_tensor: unknown name ") + name);
+}
+
+extern "C" int cq_weights_wo_rows(cq_weights* w, int32_t layer, void** W, void** S) {
+  if (!w || !W) return fail(CQ_EINVAL, "weights_wo_rows: null argument");
+  const cq_config& c = w->cfg;
+  if (layer < 0 || layer >= c.n_layers) return fail(CQ_EINVAL, "weights_wo_rows: layer out of range");
+  if (!w->wo_rows) {
+    const size_t qd = (size_t)c.n_heads * c.head_dim;
+    const size_t wb = c.quant_type == CQ_QUANT_INT4 ? c.dim * qd / 2 : c.quant_type == CQ_QUANT_INT8 ? c.dim * qd : c.dim * qd * 2;
+    const size_t sb = c.quant_type == CQ_QUANT_FP16 ? 0 : c.dim * (qd / kGroup) * 2;
+    const size_t stride = align_up(align_up(wb) + sb);
+    char* p = nullptr;
+    if (hipMalloc((void**)&p, stride * c.n_layers) != hipSuccess)
+      return fail(CQ_ENOMEM, "weights_wo_rows: allocation failed");
+    int rc = CQ_OK;
+    for (int l = 0; l < c.n_layers && rc == CQ_OK; ++l)
+      rc = wo_from_panels(c.quant_type, w->layers[l].wo, w->layers[l].so, c.dim, (int)qd, p + stride * l,
+                          sb ? reinterpret_cast<__half*>(p + stride * l + align_up(wb)) : nullptr, nullptr);
+    const hipError_t e = hipStreamSynchronize(nullptr);
+    if (rc == CQ_OK && e != hipSuccess) rc = fail(CQ_EHIP, std::string("weights_wo_rows: ") + hipGetErrorString(e));
+    if (rc != CQ_OK) {
+      hipFree(p);
+      return rc;
+    }
+    w->wo_rows = p;
+    w->wo_rows_stride = stride;
+    w->wo_rows_wbytes = align_up(wb);
+  }
+  *W = w->wo_rows + w->wo_rows_stride * layer;
+  if (S) *S = c.quant_type == CQ_QUANT_FP16 ? nullptr : w->wo_rows + w->wo_rows_stride * layer + w->wo_rows_wbytes;
+  return CQ_OK;
 }
 
 extern "C" int cq_state_create(const cq_config* cfg, const cq_weights* w, cq_state** out) {
@@ -1110,6 +1146,11 @@ extern "C" int cq_state_profile(cq_state* s, int32_t pos, int32_t iters, int32_t
     us_per_launch[n] = (double)ms * 1000.0 / ((double)iters * reps);
     bytes_per_launch[n] = k.bytes;
   }
+  // The merged O-projection adds into the accumulator and only the down
+  // projection clears it: a profile that stopped before the down projection
+  // ran last would leave sums behind for the next step's first layer.
+  CQ_HIP(hipMemsetAsync(s->oacc, 0, (size_t)c.dim * sizeof(long long), s->stream));
+  CQ_HIP(hipStreamSynchronize(s->stream));
   *n_kernels = n;
   return CQ_OK;
 }

@@ -111,6 +111,8 @@ int launch_omerge(const OMergeArgs& a, hipStream_t stream);
 // place into K/128 column panels [N][128] (scales [K/128][N]), the layout
 // launch_omerge and the prefill O-projection read; tmp holds N*K weight bytes.
 int wo_to_panels(int quant, void* W, __half* S, int N, int K, void* tmp, hipStream_t stream);
+int wo_from_panels(int quant, const void* W, const __half* S, int N, int K, void* W_rows, __half* S_rows,
+                   hipStream_t stream);
 int omerge_plan(int quant, int head_dim, int n_heads, int N, int* hpb, int* bands, int* rounds, int* wm);
 // Head-major cache path (cq_attention_hm.hip): the reference's layout and
 // partial buffers (partial index (kv_head * 16 + head) * 64 + partition).

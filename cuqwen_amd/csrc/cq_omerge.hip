@@ -280,6 +280,38 @@ __global__ void panelize_scales_kernel(const uint16_t* src, uint16_t* dst, int N
   }
 }
 
+// The inverse of the two above: panels -> row-major [N][K], scales
+// [K/128][N] -> [N][K/128] (the exporter's layouts), out of place.
+__global__ void unpanelize_kernel(const u4_t* src, u4_t* dst, int N, int NC, int CP) {
+  const int64_t total = (int64_t)N * NC;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int n = (int)(i / NC), c = (int)(i % NC);
+    dst[i] = src[((int64_t)(c / CP) * N + n) * CP + c % CP];
+  }
+}
+__global__ void unpanelize_scales_kernel(const uint16_t* src, uint16_t* dst, int N, int G) {
+  const int64_t total = (int64_t)N * G;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int n = (int)(i / G), g = (int)(i % G);
+    dst[i] = src[(int64_t)g * N + n];
+  }
+}
+
+int wo_from_panels(int quant, const void* W, const __half* S, int N, int K, void* W_rows, __half* S_rows,
+                   hipStream_t stream) {
+  if (K % kGroup) return fail(CQ_EINVAL, "wo rows: K must be a multiple of 128");
+  const int epc = quant == CQ_QUANT_INT4 ? 32 : quant == CQ_QUANT_INT8 ? 16 : 8;
+  const int NC = K / epc, CP = kGroup / epc;
+  hipLaunchKernelGGL(unpanelize_kernel, dim3(1024), dim3(256), 0, stream, (const u4_t*)W, (u4_t*)W_rows, N, NC, CP);
+  CQ_HIP(hipGetLastError());
+  if (quant != CQ_QUANT_FP16) {
+    hipLaunchKernelGGL(unpanelize_scales_kernel, dim3(256), dim3(256), 0, stream, (const uint16_t*)S,
+                       (uint16_t*)S_rows, N, K / kGroup);
+    CQ_HIP(hipGetLastError());
+  }
+  return CQ_OK;
+}
+
 int wo_to_panels(int quant, void* W, __half* S, int N, int K, void* tmp, hipStream_t stream) {
   if (K % kGroup) return fail(CQ_EINVAL, "wo panels: K must be a multiple of 128");
   const int epc = quant == CQ_QUANT_INT4 ? 32 : quant == CQ_QUANT_INT8 ? 16 : 8;
@@ -331,12 +363,13 @@ int launch_omerge(const OMergeArgs& a0, hipStream_t stream) {
   if (!a.workspace || !a.attn || !a.W || !a.acc || !a.d_pos || (a.quant != CQ_QUANT_FP16 && !a.S))
     return fail(CQ_EINVAL, "omerge: null pointer");
   if (a.Pmax <= 0) return fail(CQ_EINVAL, "omerge: bad partition count");
-  // the kernel indexes in unsigned 32 bits: Wo bytes, the partial slots and the band rows
+  int hpb = 1, nr = 1, wm = 1;
+  omerge_plan(a.quant, a.head_dim, a.n_heads, a.N, &hpb, &a.bands, &nr, &wm);
+  // the kernel indexes in unsigned 32 bits: Wo bytes, the partial slots and
+  // the band rows (with the band count the launch uses)
   if ((int64_t)a.N * a.K * 2 >= ((int64_t)1 << 31) || (int64_t)a.n_kv * 16 * a.Pmax * a.head_dim >= ((int64_t)1 << 31) ||
       (int64_t)a.N * (a.bands + 1) >= ((int64_t)1 << 31))
     return fail(CQ_EINVAL, "omerge: shape too large for 32-bit indexing");
-  int hpb = 1, nr = 1, wm = 1;
-  omerge_plan(a.quant, a.head_dim, a.n_heads, a.N, &hpb, &a.bands, &nr, &wm);
   const int blocks = a.n_heads / hpb * a.bands;
   if (a.quant == CQ_QUANT_INT4) {
     if (a.head_dim == 128) omerge_launch_q<CQ_QUANT_INT4, 128>(a, stream, nr, wm, blocks);

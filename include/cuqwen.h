@@ -106,6 +106,16 @@ int cq_free_weights(cq_weights* w);
  * (converted once when the weights are loaded or synthesized). */
 int cq_weights_tensor(const cq_weights* w, const char* name, int32_t layer, void** dptr, size_t* bytes);
 
+/* Layer `layer`'s O-projection in the exporter's row-major layout: *W =
+ * [dim][n_heads*head_dim] weights, *S = [dim][n_heads*head_dim/128] fp16
+ * scales (NULL for fp16 weights) -- the pointers the reference's
+ * LayerWeights.o_proj_weight / o_proj_scale hold (include/load_weights.h:25,
+ * :35; consumed by launch_gemv_add_fp16 at src/model.cu:129).  The engine
+ * keeps Wo in panels (cq_weights_tensor "wo"); the first call makes a
+ * row-major copy of every layer, owned by the weights and freed with them
+ * (7B INT4: 185 MB). */
+int cq_weights_wo_rows(cq_weights* w, int32_t layer, void** W, void** S);
+
 /* ---------------------------------------------------------------- state */
 typedef struct cq_state cq_state;       /* opaque: QwenState (include/model.cuh:9-46) */
 

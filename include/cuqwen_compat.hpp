@@ -7,8 +7,16 @@
 //   struct QwenState                        include/model.cuh:9-46
 //   malloc_qwen_state / free_qwen_state     include/model.cuh:48-49
 //   qwen_forward                            include/model.cuh:51-60
+//   launch_embedding_lookup                 include/kernels.cuh:19
 //   launch_gqa_attention_decode             include/kernels.cuh:21-35
 //   launch_kv_cache_store                   include/kernels.cuh:37-47
+//   launch_apply_repetition_penalty         include/kernels.cuh:49-56
+//   launch_argmax                           include/kernels.cuh:58-63
+//   launch_fused_attn_block                 include/kernels.cuh:69-94
+//   launch_fused_mlp_stage1 / _stage2       include/kernels.cuh:96-120
+//   launch_gemv_add_fp16                    include/kernels.cuh:122-130
+//   launch_rmsnorm                          include/kernels.cuh:132-139
+//   launch_compute_logits / _int8           include/kernels.cuh:141-160
 //
 // Model and precision are chosen at compile time with the reference's own
 // macros (-DQWEN_MODEL_0_5B | _1_5B | _3B | _7B | _14B, and -DQUANT_INT8 or
@@ -34,16 +42,27 @@
 #include "cuqwen.h"
 
 constexpr int QUANT_GROUP_SIZE = CQ_QUANT_GROUP;
+// Split-K partial buffers of launch_gqa_attention_decode, sized as the
+// reference sizes them (include/kernels.cuh:17, include/config.h:146).
+constexpr int PARTIAL_HEAD_SLOTS = 16;
+constexpr int ATTN_PARTITIONS = 64;
 
+// include/config.h:18-40: weight element type, row stride in qweight_t
+// elements, QUANT_ENABLED for the builds with scales
 #if defined(QUANT_INT8)
 using qweight_t = int8_t;
 #define CQ_COMPAT_QUANT_TAG "int8"
 #define CQ_COMPAT_QUANT CQ_QUANT_INT8
+#define QUANT_ENABLED
+#define WEIGHT_ROW_STRIDE(cols) (cols)
 #elif defined(QUANT_INT4)
 using qweight_t = int8_t;   // two 4-bit weights per byte
 #define CQ_COMPAT_QUANT_TAG "int4"
 #define CQ_COMPAT_QUANT CQ_QUANT_INT4
+#define QUANT_ENABLED
+#define WEIGHT_ROW_STRIDE(cols) ((cols) / 2)
 #else
+#define WEIGHT_ROW_STRIDE(cols) (cols)
 using qweight_t = __half;
 #define CQ_COMPAT_QUANT_TAG "fp16"
 #define CQ_COMPAT_QUANT CQ_QUANT_FP16
@@ -115,10 +134,13 @@ struct QwenConfig {
   }
 };
 
-// Device pointers into the engine's weight arena, filled by load_weights so
-// op-level callers find every tensor where the reference's loader puts it.
-// Exporter layout, except o_proj_weight / o_proj_scale: 128-column panels
-// (see cq_weights_tensor in cuqwen.h).
+// Device pointers into the engine's weights, filled by load_weights so
+// op-level callers find every tensor where the reference's loader puts it,
+// all in the exporter's layout.  o_proj_weight / o_proj_scale point at a
+// row-major copy (cq_weights_wo_rows): the engine's own Wo is held in
+// 128-column panels for its merged O-projection, and a caller that runs
+// launch_gemv_add_fp16 on these pointers (src/model.cu:129) gets the
+// reference's result.
 struct LayerWeights {
   __half* input_layernorm_weight = nullptr;
   qweight_t* q_proj_weight = nullptr;
@@ -192,7 +214,11 @@ inline QwenConfig load_weights(const std::string& bin_path, QwenWeights& w) {
     L.k_proj_bias = tensor<__half>(w.handle, "bk", l);
     L.v_proj_weight = tensor<qweight_t>(w.handle, "wv", l);
     L.v_proj_bias = tensor<__half>(w.handle, "bv", l);
-    L.o_proj_weight = tensor<qweight_t>(w.handle, "wo", l);
+    void* wo = nullptr;
+    void* so = nullptr;
+    check(cq_weights_wo_rows(w.handle, l, &wo, &so), "load_weights (o_proj rows)");
+    L.o_proj_weight = static_cast<qweight_t*>(wo);
+    L.o_proj_scale = static_cast<__half*>(so);
     L.post_attention_layernorm_weight = tensor<__half>(w.handle, "post_norm", l);
     L.gate_proj_weight = tensor<qweight_t>(w.handle, "wg", l);
     L.up_proj_weight = tensor<qweight_t>(w.handle, "wu", l);
@@ -200,7 +226,6 @@ inline QwenConfig load_weights(const std::string& bin_path, QwenWeights& w) {
     L.q_proj_scale = tensor<__half>(w.handle, "sq", l);
     L.k_proj_scale = tensor<__half>(w.handle, "sk", l);
     L.v_proj_scale = tensor<__half>(w.handle, "sv", l);
-    L.o_proj_scale = tensor<__half>(w.handle, "so", l);
     L.gate_proj_scale = tensor<__half>(w.handle, "sg", l);
     L.up_proj_scale = tensor<__half>(w.handle, "su", l);
     L.down_proj_scale = tensor<__half>(w.handle, "sd", l);
@@ -237,6 +262,129 @@ inline int qwen_forward(int token, int pos, const QwenConfig&, QwenState& s, con
                                  static_cast<void*>(stream), &next),
                    "qwen_forward");
   return next;
+}
+
+// ------------------------------------------------------------------ op level
+// The reference's launch_* family (include/kernels.cuh:19-160) with its
+// signatures: qweight_t weights of this build's precision (-DQUANT_*),
+// row-major as the exporter writes them, scales NULL for fp16; `half eps` /
+// `half penalty` as the reference passes them.  Asynchronous on `stream`;
+// a rejected argument throws std::runtime_error.
+
+namespace cq_compat {
+inline void* as_stream(hipStream_t s) { return static_cast<void*>(s); }
+
+// Device workspace behind launch_argmax / launch_apply_repetition_penalty,
+// which take none in the reference's signatures (it holds a function-local
+// static too, src/kernels.cu:953): allocated on first use, zeroed, grown when
+// a larger vocabulary needs more, kept until the process ends.  Like the
+// reference's, not safe for concurrent callers.
+struct Workspace {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+  void* get(size_t need) {
+    if (need > bytes) {
+      if (ptr && hipFree(ptr) != hipSuccess) throw std::runtime_error("cuqwen_compat: hipFree failed");
+      ptr = nullptr;
+      bytes = 0;
+      if (hipMalloc(&ptr, need) != hipSuccess || hipMemset(ptr, 0, need) != hipSuccess)
+        throw std::runtime_error("cuqwen_compat: workspace allocation failed");
+      bytes = need;
+    }
+    return ptr;
+  }
+};
+inline Workspace& argmax_ws() {
+  static Workspace w;
+  return w;
+}
+inline Workspace& penalty_ws() {
+  static Workspace w;
+  return w;
+}
+}  // namespace cq_compat
+
+inline void launch_embedding_lookup(const __half* embed_table, const int* d_token_id, __half* output, int dim,
+                                    hipStream_t stream = 0) {
+  cq_compat::check(cq_embedding_lookup(embed_table, d_token_id, output, dim, cq_compat::as_stream(stream)),
+                   "launch_embedding_lookup");
+}
+
+inline void launch_apply_repetition_penalty(__half* logits, const int* d_history, const int* d_history_len,
+                                            int vocab_size, __half penalty, hipStream_t stream = 0) {
+  void* ws = cq_compat::penalty_ws().get(cq_penalty_workspace_bytes(vocab_size));
+  cq_compat::check(cq_apply_repetition_penalty(logits, d_history, d_history_len, vocab_size, __half2float(penalty), ws,
+                                               cq_compat::as_stream(stream)),
+                   "launch_apply_repetition_penalty");
+}
+
+inline void launch_argmax(const __half* logits, int* d_sampled_token, int vocab_size, hipStream_t stream = 0) {
+  void* ws = cq_compat::argmax_ws().get(cq_argmax_workspace_bytes(vocab_size));
+  cq_compat::check(cq_argmax(logits, d_sampled_token, vocab_size, ws, cq_compat::as_stream(stream)), "launch_argmax");
+}
+
+// x is already RMS-normalized: the reference leaves norm_weight and eps
+// unused (src/kernels.cu:502), and so does this wrapper.
+inline void launch_fused_attn_block(const __half* x, const __half* norm_weight, const qweight_t* W_q,
+                                    const qweight_t* W_k, const qweight_t* W_v, const __half* W_q_scale,
+                                    const __half* W_k_scale, const __half* W_v_scale, const __half* b_q,
+                                    const __half* b_k, const __half* b_v, __half* q_out, __half* k_out,
+                                    __half* v_out, int dim, int q_dim, int kv_dim, int n_heads, int n_kv_heads,
+                                    int head_dim, const int* d_pos, float rope_theta, __half eps,
+                                    hipStream_t stream = 0) {
+  (void)norm_weight;
+  (void)eps;
+  if (q_dim != n_heads * head_dim || kv_dim != n_kv_heads * head_dim)
+    throw std::runtime_error("launch_fused_attn_block: q_dim / kv_dim do not match the head counts");
+  cq_compat::check(cq_fused_attn_block(CQ_COMPAT_QUANT, x, nullptr, W_q, W_k, W_v, W_q_scale, W_k_scale, W_v_scale,
+                                       b_q, b_k, b_v, q_out, k_out, v_out, dim, n_heads, n_kv_heads, head_dim, d_pos,
+                                       rope_theta, 0.f, cq_compat::as_stream(stream)),
+                   "launch_fused_attn_block");
+}
+
+// x is already RMS-normalized (src/kernels.cu:576).
+inline void launch_fused_mlp_stage1(const __half* x, const __half* norm_weight, const qweight_t* gate_weight,
+                                    const qweight_t* up_weight, const __half* gate_scale, const __half* up_scale,
+                                    __half* intermediate_out, int dim, int inter_dim, __half eps,
+                                    hipStream_t stream = 0) {
+  (void)norm_weight;
+  (void)eps;
+  cq_compat::check(cq_fused_mlp_stage1(CQ_COMPAT_QUANT, x, nullptr, gate_weight, up_weight, gate_scale, up_scale,
+                                       intermediate_out, dim, inter_dim, 0.f, cq_compat::as_stream(stream)),
+                   "launch_fused_mlp_stage1");
+}
+
+inline void launch_fused_mlp_stage2(__half* x, const qweight_t* down_weight, const __half* down_scale,
+                                    const __half* intermediate_in, int dim, int inter_dim, hipStream_t stream = 0) {
+  cq_compat::check(cq_fused_mlp_stage2(CQ_COMPAT_QUANT, x, down_weight, down_scale, intermediate_in, dim, inter_dim,
+                                       cq_compat::as_stream(stream)),
+                   "launch_fused_mlp_stage2");
+}
+
+inline void launch_gemv_add_fp16(const qweight_t* W, const __half* W_scale, const __half* input, __half* x_inout,
+                                 int rows, int cols, hipStream_t stream = 0) {
+  cq_compat::check(cq_gemv_add(CQ_COMPAT_QUANT, W, W_scale, input, x_inout, rows, cols, cq_compat::as_stream(stream)),
+                   "launch_gemv_add_fp16");
+}
+
+inline void launch_rmsnorm(const __half* x, const __half* norm_weight, __half* out, int dim, __half eps,
+                           hipStream_t stream = 0) {
+  cq_compat::check(cq_rmsnorm(x, norm_weight, out, dim, __half2float(eps), cq_compat::as_stream(stream)),
+                   "launch_rmsnorm");
+}
+
+inline void launch_compute_logits(const __half* x_normed, const __half* lm_head_weight, __half* logits,
+                                  int vocab_size, int dim, hipStream_t stream = 0) {
+  cq_compat::check(cq_compute_logits(CQ_LMHEAD_FP16, x_normed, lm_head_weight, nullptr, logits, vocab_size, dim,
+                                     cq_compat::as_stream(stream)),
+                   "launch_compute_logits");
+}
+
+inline void launch_compute_logits_int8(const __half* x_normed, const int8_t* lm_head_w, const __half* lm_head_scale,
+                                       __half* logits, int vocab_size, int dim, hipStream_t stream = 0) {
+  cq_compat::check(cq_compute_logits(CQ_LMHEAD_INT8, x_normed, lm_head_w, lm_head_scale, logits, vocab_size, dim,
+                                     cq_compat::as_stream(stream)),
+                   "launch_compute_logits_int8");
 }
 
 // Op level over the reference's head-major cache (include/kernels.cuh:21-47).

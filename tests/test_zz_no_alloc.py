@@ -1,7 +1,10 @@
 """cq_gqa_attention_decode_noalloc (partials in a static device array)
 against cq_gqa_attention_decode with a caller workspace: bit-identical
 outputs on two calls in a row, the second with a smaller input, and within
-1e-2 of the oracle; shapes past the scratch are rejected."""
+1e-2 of the oracle.  The scratch covers the partials of every shape the
+attention accepts (checked below); the size guard, reachable only with head
+counts the attention itself refuses, returns CQ_ERANGE before any launch,
+and an unsupported head_dim returns CQ_EINVAL."""
 import numpy as np
 import pytest
 
@@ -49,5 +52,9 @@ def test_noalloc_scratch_limit():
         with pytest.raises(cq.CuQwenError, match="EINVAL"):   # shape rejected before any launch
             cq.check(cq.lib.cq_gqa_attention_decode_noalloc(b.ptr, b.ptr, b.ptr, b.ptr, g.i32(0), 28, 4, 96, 64,
                                                             None))
+        assert cq.lib.cq_attention_workspace_bytes(16 * 200, 200, 128) > cq.lib.cq_noalloc_scratch_bytes()
+        with pytest.raises(cq.CuQwenError, match="ERANGE"):   # size guard, before any launch
+            cq.check(cq.lib.cq_gqa_attention_decode_noalloc(b.ptr, b.ptr, b.ptr, b.ptr, g.i32(0), 16 * 200, 200, 128,
+                                                            64, None))
     finally:
         g.close()
