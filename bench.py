@@ -39,6 +39,8 @@ def parse():
     ap.add_argument("--no-windows", action="store_true",
                     help="skip the reference's windowed measurement (nine 500-token windows across 32K)")
     ap.add_argument("--no-kv8", action="store_true", help="skip the int8 and fp8 KV cache legs")
+    ap.add_argument("--kv", choices=["fp16", "int8", "fp8"], default="fp16",
+                    help="KV cache of the main measurement (the headline is the reference's fp16 cache)")
     ap.add_argument("--prompt", type=int, default=1024, help="prompt tokens of the batched-prefill measurement")
     ap.add_argument("--configs", action="store_true",
                     help="also measure decode (and prefill) at every BASELINE config (adds about a minute)")
@@ -424,9 +426,10 @@ def main():
         raise SystemExit("ctx too small for warmup + steps")
     t0 = time.perf_counter()
     w = cq.synth_weights(cfg, 0x5157454E)
-    st = cq.State(cfg, w)
+    kv_dtype = {"fp16": cq.KV_FP16, "int8": cq.KV_INT8, "fp8": cq.KV_FP8}[args.kv]
+    st = cq.State(cfg, w, kv_dtype=kv_dtype)
     st.fill_kv(pos0, 77)
-    log(f"[bench] {args.model} {args.quant}: weights + KV({pos0}) ready in {time.perf_counter() - t0:.1f}s")
+    log(f"[bench] {args.model} {args.quant} ({args.kv} KV): weights + KV({pos0}) ready in {time.perf_counter() - t0:.1f}s")
     tok = int(cq.lib.cq_synth_uniform(42, 0, 0, cfg.vocab_size))
     # Untimed: one chained decode of 8 steps records, instantiates and uploads
     # both step graphs (1-step and 8-step) and replays each once, whatever
@@ -464,7 +467,8 @@ def main():
         per_tok = {k["kernel"]: k["bytes"] * (cfg.n_layers if k["kernel"] not in ("lm_head", "argmax") else 1)
                    for k in kernels}
         dom = max(kernels, key=lambda k: per_tok[k["kernel"]])
-        traffic = measured_traffic(dom["kernel"], args.model, args.quant) if args.ctx == 32768 else None
+        traffic = (measured_traffic(dom["kernel"], args.model, args.quant)
+                   if args.ctx == 32768 and args.kv == "fp16" else None)
         roof = {"bound": "hbm", "kernel": dom["kernel"], "achieved": dom["GBps"], "peak": PEAK_GBPS,
                 "unit": "GB/s", "frac": dom["frac"], "traffic": traffic,
                 "bytes_per_launch": dom["bytes"], "us_per_launch": dom["us"]}

@@ -126,6 +126,8 @@ def _load():
         "cq_argmax": (I32, [P, P, I32, P, P]),
         "cq_argmax_workspace_bytes": (SZ, [I32]),
         "cq_kv_k_offset": (ctypes.c_int64, [I32, I32, I32, I32, I32]),
+        "cq_kv8_k_offset": (ctypes.c_int64, [I32, I32, I32, I32, I32]),
+        "cq_kv8_v_offset": (ctypes.c_int64, [I32, I32, I32, I32, I32]),
         "cq_kv_v_offset": (ctypes.c_int64, [I32, I32, I32, I32, I32]),
         "cq_kv_cache_store": (I32, [P, P, P, P, P, I32, I32, I32, P]),
         "cq_rope": (I32, [P, P, I32, I32, I32, P, ctypes.c_float, P]),
@@ -171,6 +173,7 @@ EXPORTED = [
     "cq_synchronize", "cq_embedding_lookup", "cq_rmsnorm", "cq_gemv", "cq_gemv_add", "cq_fused_attn_block",
     "cq_fused_mlp_stage1", "cq_fused_mlp_stage2", "cq_compute_logits", "cq_apply_repetition_penalty",
     "cq_penalty_workspace_bytes", "cq_argmax", "cq_argmax_workspace_bytes", "cq_kv_k_offset", "cq_kv_v_offset",
+    "cq_kv8_k_offset", "cq_kv8_v_offset",
     "cq_kv_cache_store", "cq_rope", "cq_gqa_attention_decode", "cq_attention_workspace_bytes", "cq_dequantize",
     "cq_kv_cache_store_hm", "cq_gqa_attention_decode_hm", "cq_gqa_attention_decode_noalloc",
     "cq_noalloc_scratch_bytes",

@@ -240,12 +240,22 @@ __device__ __forceinline__ void load_tile8(KVTile8<HD>& t, const int8_t* kbase, 
                                            const float* vsc, int ti, int lane) {
   const int8_t* kt = kbase + (int64_t)ti * kTileKeys * HD;
   const int8_t* vt = vbase + (int64_t)ti * kTileKeys * HD;
+  // one 16-byte load per lane fetches the operand pieces of two instructions
+  // (kv8_k_offset / kv8_v_offset)
 #pragma unroll
   for (int st = 0; st < 2; ++st)
 #pragma unroll
-    for (int kk = 0; kk < HD / 32; ++kk) t.ka[st][kk] = load_u2_stream(kt + st * 16 * HD + (kk * 64 + lane) * 8);
+    for (int kk = 0; kk < HD / 32; kk += 2) {
+      const u4_t w = load_u4_stream(kt + st * 16 * HD + ((kk / 2) * 64 + lane) * 16);
+      t.ka[st][kk] = u2_t{w.x, w.y};
+      t.ka[st][kk + 1] = u2_t{w.z, w.w};
+    }
 #pragma unroll
-  for (int dt = 0; dt < HD / 16; ++dt) t.va[dt] = load_u2_stream(vt + (dt * 64 + lane) * 8);
+  for (int dt = 0; dt < HD / 16; dt += 2) {
+    const u4_t w = load_u4_stream(vt + ((dt / 2) * 64 + lane) * 16);
+    t.va[dt] = u2_t{w.x, w.y};
+    t.va[dt + 1] = u2_t{w.z, w.w};
+  }
   const int j = lane >> 4;
 #pragma unroll
   for (int st = 0; st < 2; ++st) {

@@ -115,6 +115,23 @@ __global__ __launch_bounds__(kAttnThreads) void attention_stage1_kv8(const AttnA
   const float* ksc = a.kscale + (int64_t)kvh * a.max_seq;
   const float* vsc = a.vscale + (int64_t)kvh * a.max_seq;
 
+  // The new row (position pos) belongs to tile n_tiles - 1 of the last
+  // partition.  Its owner wave requests the fp16 k / v rows before anything
+  // else: loads complete in issue order for the wave, so issued after the
+  // tiles they would wait for the whole tile prefetch, and the quantization
+  // below would then sit on the kernel's critical path instead of running
+  // while the tiles are in flight.
+  const int last = n_tiles - 1;
+  const bool owns_new = part == nparts - 1 && ((last - tile0) % kAttnWaves) == wave;
+  float xnew[2][E];
+  if (owns_new) {
+#pragma unroll
+    for (int kind = 0; kind < 2; ++kind) {
+      const _Float16* src = reinterpret_cast<const _Float16*>(kind ? a.v_new : a.k_new) + (int64_t)kvh * HD + lane * E;
+#pragma unroll
+      for (int i = 0; i < E; ++i) xnew[kind][i] = (float)src[i];
+    }
+  }
   KVTile8<HD> A, B;
   int ti = tile0 + wave;
   if (ti < tile1) load_tile8<HD>(A, kbase, vbase, ksc, vsc, ti, lane);
@@ -127,32 +144,25 @@ __global__ __launch_bounds__(kAttnThreads) void attention_stage1_kv8(const AttnA
       else qb[kk] = h8_t{0, 0, 0, 0, 0, 0, 0, 0};
     }
   }
-  // q goes out before the second tile: loads return in issue order, so the
-  // first tile's scores wait only for the first tile and q
+  // q goes out before the second tile: the first tile's scores wait only
+  // for the first tile and q
   if (ti + kAttnWaves < tile1) load_tile8<HD>(B, kbase, vbase, ksc, vsc, ti + kAttnWaves, lane);
-  // the new row (position pos) belongs to tile n_tiles - 1 of the last partition;
-  // its owner quantizes it while its first tiles are in flight (the loaded
-  // tile's copy of that position is replaced by the patch, so whether the
-  // load sees the old or the new bytes does not matter)
+  // the owner quantizes the new rows while its tiles are in flight (the
+  // loaded tile's copy of that position is replaced by the patch, so whether
+  // the load sees the old or the new bytes does not matter)
   __shared__ __align__(16) int8_t newq[2][HD];
   __shared__ float news[2];
-  const int last = n_tiles - 1;
-  const bool owns_new = part == nparts - 1 && ((last - tile0) % kAttnWaves) == wave;
   if (owns_new) {
 #pragma unroll
     for (int kind = 0; kind < 2; ++kind) {
-      const _Float16* src = reinterpret_cast<const _Float16*>(kind ? a.v_new : a.k_new) + (int64_t)kvh * HD + lane * E;
-      float x[E];
       int8_t qv[E];
-#pragma unroll
-      for (int i = 0; i < E; ++i) x[i] = (float)src[i];
-      const float sc = quant_row8_wave<HD, F>(x, qv);
+      const float sc = quant_row8_wave<HD, F>(xnew[kind], qv);
       int8_t* cache = kind ? a.vcache8 : a.kcache8;
 #pragma unroll
       for (int i = 0; i < E; ++i) {
         const int d = lane * E + i;
         newq[kind][d] = qv[i];
-        cache[kind ? kv_v_offset(kvh, pos, d, a.max_seq, HD) : kv_k_offset(kvh, pos, d, a.max_seq, HD)] = qv[i];
+        cache[kind ? kv8_v_offset(kvh, pos, d, a.max_seq, HD) : kv8_k_offset(kvh, pos, d, a.max_seq, HD)] = qv[i];
       }
       if (lane == 0) {
         news[kind] = sc;

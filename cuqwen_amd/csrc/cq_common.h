@@ -197,6 +197,25 @@ CQ_HD int64_t kv_v_offset(int kv_head, int t, int d, int max_seq, int hd) {
   return (int64_t)kv_head * max_seq * hd + tile + ((dt * 64 + j * 16 + dl) * 8 + e);
 }
 
+// The int8 / E4M3 caches (one byte per element) keep the same tiles and
+// operand order, with the 8-byte operand pieces of instruction pairs
+// (kk, kk+1) for K and (dt, dt+1) for V placed side by side, so one 16-byte
+// load per lane fetches two operands: piece (i, lane) of the fp16 layout
+// (i = kk or dt) sits at ((i/2)*64 + lane)*16 + (i%2)*8.
+CQ_HD int64_t kv8_k_offset(int kv_head, int t, int d, int max_seq, int hd) {
+  const int kk = d >> 5, j = (d >> 3) & 3, e = d & 7;
+  const int64_t tile = (int64_t)(t >> 4) * 16 * hd;
+  return (int64_t)kv_head * max_seq * hd + tile + (((kk >> 1) * 64 + j * 16 + (t & 15)) * 16 + (kk & 1) * 8 + e);
+}
+CQ_HD int64_t kv8_v_offset(int kv_head, int t, int d, int max_seq, int hd) {
+  const int dt = d >> 4, dl = d & 15;
+  const int t32 = t & 31;
+  const int j = (t32 & 15) >> 2;
+  const int e = (t32 & 3) + ((t32 >> 4) << 2);
+  const int64_t tile = (int64_t)(t >> 5) * 32 * hd;
+  return (int64_t)kv_head * max_seq * hd + tile + (((dt >> 1) * 64 + j * 16 + dl) * 16 + (dt & 1) * 8 + e);
+}
+
 // Weight row bytes for `cols` logical weights (include/config.h:36-40).
 inline int64_t row_bytes(int quant, int64_t cols) {
   return quant == CQ_QUANT_INT4 ? cols / 2 : quant == CQ_QUANT_INT8 ? cols : cols * 2;

@@ -355,8 +355,6 @@ int ensure_run_graph(cq_state* s) {
   CQ_HIP(e);
   s->graph_run = g;
   CQ_HIP(hipGraphInstantiate(&s->exec_run, g, nullptr, nullptr, 0));
-  // pay the first-launch upload now, not inside the caller's first replay
-  CQ_HIP(hipGraphUpload(s->exec_run, s->stream));
   return CQ_OK;
 }
 
@@ -374,7 +372,6 @@ int ensure_graph(cq_state* s) {
   CQ_HIP(e);
   s->graph = g;
   CQ_HIP(hipGraphInstantiate(&s->exec, g, nullptr, nullptr, 0));
-  CQ_HIP(hipGraphUpload(s->exec, s->stream));
   return CQ_OK;
 }
 
@@ -473,7 +470,7 @@ __global__ void fill_kv8_kernel(int fmt, int8_t* kc, int8_t* vc, float* ks, floa
     for (int d = 0; d < hd; ++d) {
       const float x = h2f_bits(synth_half(seed, st, (uint64_t)t * hd + d, mul, 0.f));
       const int8_t q = sc == 0.f ? (int8_t)0 : quant_code(fmt, x / sc);
-      c[lo + (kind ? kv_v_offset(h, t, d, max_seq, hd) : kv_k_offset(h, t, d, max_seq, hd))] = q;
+      c[lo + (kind ? kv8_v_offset(h, t, d, max_seq, hd) : kv8_k_offset(h, t, d, max_seq, hd))] = q;
     }
     (kind ? vs : ks)[((size_t)l * n_kv + h) * max_seq + t] = sc;
   }
@@ -766,9 +763,9 @@ extern "C" int cq_decode(cq_state* s, int32_t token, int32_t pos0, int32_t n_ste
   CQ_TRY(check_step_args(s, token, pos0, history, history_len));
   if (n_steps <= 0 || (int64_t)pos0 + n_steps > s->cfg.max_seq_len)
     return fail(CQ_ERANGE, "decode: pos0 + n_steps exceeds max_seq_len");
-  // Both graphs are recorded, instantiated and uploaded on the first chained
-  // decode whatever its length, so a later call never records inside the
-  // span its caller times.
+  // Both graphs are recorded and instantiated on the first chained decode
+  // whatever its length, so a later call never records inside the span its
+  // caller times.
   CQ_TRY(ensure_graph(s));
   CQ_TRY(ensure_run_graph(s));
   CQ_TRY(set_ctl(s, token, pos0, history, history_len, 1));
@@ -840,6 +837,9 @@ static int kv_slab(cq_state* s, int layer, int kv_head, int kind, int n_pos, cha
 static size_t kv_index(int kind, int t, int d, int ms, int hd) {
   return (size_t)(kind == 0 ? kv_k_offset(0, t, d, ms, hd) : kv_v_offset(0, t, d, ms, hd));
 }
+static size_t kv8_index(int kind, int t, int d, int ms, int hd) {
+  return (size_t)(kind == 0 ? kv8_k_offset(0, t, d, ms, hd) : kv8_v_offset(0, t, d, ms, hd));
+}
 
 extern "C" int cq_state_kv_read(cq_state* s, int32_t layer, int32_t kv_head, int32_t kind, int32_t n_pos,
                                 uint16_t* host_out) {
@@ -864,7 +864,7 @@ extern "C" int cq_state_kv_read(cq_state* s, int32_t layer, int32_t kv_head, int
   if (n_pos) CQ_HIP(hipMemcpy(sc.data(), scales, (size_t)n_pos * 4, hipMemcpyDeviceToHost));
   for (int t = 0; t < n_pos; ++t)
     for (int d = 0; d < hd; ++d)
-      host_out[(size_t)t * hd + d] = f2h_bits(code_value(s->kv_dtype, tmp[kv_index(kind, t, d, ms, hd)]) * sc[t]);
+      host_out[(size_t)t * hd + d] = f2h_bits(code_value(s->kv_dtype, tmp[kv8_index(kind, t, d, ms, hd)]) * sc[t]);
   return CQ_OK;
 }
 
@@ -891,7 +891,7 @@ extern "C" int cq_state_kv_write(cq_state* s, int32_t layer, int32_t kv_head, in
   CQ_HIP(hipMemcpy(tmp.data(), base, elems, hipMemcpyDeviceToHost));
   for (int t = 0; t < n_pos; ++t) {
     quant_row8_host(s->kv_dtype, host_in + (size_t)t * hd, hd, q.data(), &sc[t]);
-    for (int d = 0; d < hd; ++d) tmp[kv_index(kind, t, d, ms, hd)] = q[d];
+    for (int d = 0; d < hd; ++d) tmp[kv8_index(kind, t, d, ms, hd)] = q[d];
   }
   CQ_HIP(hipMemcpy(base, tmp.data(), elems, hipMemcpyHostToDevice));
   if (n_pos) CQ_HIP(hipMemcpy(scales, sc.data(), (size_t)n_pos * 4, hipMemcpyHostToDevice));
@@ -1100,7 +1100,9 @@ extern "C" int cq_state_profile(cq_state* s, int32_t pos, int32_t iters, int32_t
   // bytes: weights + scales + activations in/out (+ bias, residual)
   const K ks[] = {
       {"qkv_rope_kvstore", wbytes(qt, qd + 2 * kvd, d) + 2 * d * 2 + 2 * (qd + 2 * kvd) * 2, 0},
-      {"attention_stage1", 2.0 * c.n_kv_heads * T * c.head_dim * 2 + 2 * qd * 2, 1},
+      // K and V: fp16, or one code byte per element plus an fp32 scale per row
+      {"attention_stage1", (s->kv_dtype == CQ_KV_FP16 ? 2.0 * c.n_kv_heads * T * c.head_dim * 2
+                                                      : 2.0 * c.n_kv_heads * T * (c.head_dim + 4.0)) + 2 * qd * 2, 1},
       {"merge_o_proj", wbytes(qt, d, qd) + 8 * d * (double)c.n_heads, 2},
       {"gate_up_swiglu", wbytes(qt, 2 * I, d) + 2 * d * 2 + 8 * d + 2 * I, 3},
       {"down_residual", wbytes(qt, d, I) + 2 * I + 2 * d * 2, 4},

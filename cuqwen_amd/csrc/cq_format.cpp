@@ -281,3 +281,9 @@ extern "C" int64_t cq_kv_k_offset(int32_t kv_head, int32_t t, int32_t d, int32_t
 extern "C" int64_t cq_kv_v_offset(int32_t kv_head, int32_t t, int32_t d, int32_t max_seq_len, int32_t head_dim) {
   return kv_v_offset(kv_head, t, d, max_seq_len, head_dim);
 }
+extern "C" int64_t cq_kv8_k_offset(int32_t kv_head, int32_t t, int32_t d, int32_t max_seq_len, int32_t head_dim) {
+  return cq::kv8_k_offset(kv_head, t, d, max_seq_len, head_dim);
+}
+extern "C" int64_t cq_kv8_v_offset(int32_t kv_head, int32_t t, int32_t d, int32_t max_seq_len, int32_t head_dim) {
+  return cq::kv8_v_offset(kv_head, t, d, max_seq_len, head_dim);
+}

@@ -174,7 +174,7 @@ __device__ __forceinline__ void pf_kv8_store(const PfGemmArgs& a, int mat, int k
   for (int d = 0; d < hd; ++d) {
     const float v = value(d) / sc;
     const int8_t q = sc == 0.f ? (int8_t)0 : (f8 ? kv_encode<CQ_KV_FP8>(v) : kv_encode<CQ_KV_INT8>(v));
-    c[mat == 1 ? kv_k_offset(kvh, pos, d, a.max_seq, hd) : kv_v_offset(kvh, pos, d, a.max_seq, hd)] = q;
+    c[mat == 1 ? kv8_k_offset(kvh, pos, d, a.max_seq, hd) : kv8_v_offset(kvh, pos, d, a.max_seq, hd)] = q;
   }
   (mat == 1 ? a.kscale : a.vscale)[(int64_t)kvh * a.max_seq + pos] = sc;
 }
@@ -729,7 +729,7 @@ __global__ __launch_bounds__(kPfQkvThreads) void pf_split_qkv(const PfGemmArgs a
 #pragma unroll
       for (int e = 0; e < E; ++e) {
         const int d = lane * E + e;
-        c[mat == 1 ? kv_k_offset(kvh, pos, d, a.max_seq, HD) : kv_v_offset(kvh, pos, d, a.max_seq, HD)] = q[e];
+        c[mat == 1 ? kv8_k_offset(kvh, pos, d, a.max_seq, HD) : kv8_v_offset(kvh, pos, d, a.max_seq, HD)] = q[e];
       }
       if (lane == 0) (mat == 1 ? a.kscale : a.vscale)[(int64_t)kvh * a.max_seq + pos] = sc;
     }

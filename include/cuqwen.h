@@ -319,6 +319,12 @@ size_t cq_argmax_workspace_bytes(int32_t vocab);
  * at half-index cq_kv_k_offset(...), of V at cq_kv_v_offset(...). */
 int64_t cq_kv_k_offset(int32_t kv_head, int32_t t, int32_t d, int32_t max_seq_len, int32_t head_dim);
 int64_t cq_kv_v_offset(int32_t kv_head, int32_t t, int32_t d, int32_t max_seq_len, int32_t head_dim);
+/* Byte offsets of element (kv_head, t, d) in an int8 / E4M3 layer cache
+ * (CQ_KV_INT8 / CQ_KV_FP8): the same tiles and operand order as the fp16
+ * cache, with the 8-byte operand pieces of two consecutive matrix-core
+ * instructions side by side, so a lane fetches both with one 16-byte load. */
+int64_t cq_kv8_k_offset(int32_t kv_head, int32_t t, int32_t d, int32_t max_seq_len, int32_t head_dim);
+int64_t cq_kv8_v_offset(int32_t kv_head, int32_t t, int32_t d, int32_t max_seq_len, int32_t head_dim);
 
 /* apply_rope_kernel (src/kernels.cu:370-398, launched inside
  * launch_fused_attn_block, kernels.cu:513-517): NeoX rotation of the pairs
@@ -383,9 +389,8 @@ int cq_gqa_attention_decode_hm(const void* q, const void* layer_k_cache, const v
 
 /* The same decode attention over an int8 layer cache (see CQ_KV_INT8; no
  * counterpart in the reference): k_new / v_new ([n_kv_heads * head_dim]
- * fp16) are quantized into position *d_pos of k_cache8 / v_cache8 (same
- * tiled element layout as the fp16 cache, one byte per element, see
- * cq_kv_*_offset) with their scales into k_scale / v_scale
+ * fp16) are quantized into position *d_pos of k_cache8 / v_cache8 (tiled,
+ * one byte per element, see cq_kv8_*_offset) with their scales into k_scale / v_scale
  * ([n_kv_heads][max_seq_len] fp32), then attn_out is computed over keys
  * [0, *d_pos].  `workspace` as for cq_gqa_attention_decode. */
 int cq_gqa_attention_decode_kv8(const void* q, const void* k_new, const void* v_new, void* k_cache8, void* v_cache8,

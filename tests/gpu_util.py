@@ -60,6 +60,23 @@ def v_offsets(n_kv, T, hd, max_seq):
     return h * max_seq * hd + (t >> 5) * 32 * hd + ((dt * 64 + j * 16 + dl) * 8 + e)
 
 
+def k8_offsets(n_kv, T, hd, max_seq):
+    """Vectorised kv8_k_offset (cq_common.h): byte offsets in an int8 / E4M3
+    cache, operand pieces of instruction pairs side by side."""
+    h, t, d = np.meshgrid(np.arange(n_kv), np.arange(T), np.arange(hd), indexing="ij")
+    kk, j, e = d >> 5, (d >> 3) & 3, d & 7
+    return h * max_seq * hd + (t >> 4) * 16 * hd + (((kk >> 1) * 64 + j * 16 + (t & 15)) * 16 + (kk & 1) * 8 + e)
+
+
+def v8_offsets(n_kv, T, hd, max_seq):
+    h, t, d = np.meshgrid(np.arange(n_kv), np.arange(T), np.arange(hd), indexing="ij")
+    dt, dl = d >> 4, d & 15
+    t32 = t & 31
+    j = (t32 & 15) >> 2
+    e = (t32 & 3) + ((t32 >> 4) << 2)
+    return h * max_seq * hd + (t >> 5) * 32 * hd + (((dt >> 1) * 64 + j * 16 + dl) * 16 + (dt & 1) * 8 + e)
+
+
 def tile_kv(K, V, max_seq):
     """Head-major K, V [n_kv][T][hd] -> the device cache layout."""
     n_kv, T, hd = K.shape

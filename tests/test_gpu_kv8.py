@@ -8,7 +8,7 @@ import pytest
 import cuqwen_amd as cq
 from oracle import oracle as orc
 from tests.conftest import tiny_config
-from tests.gpu_util import Pool, rel_err, k_offsets, v_offsets
+from tests.gpu_util import Pool, rel_err, k8_offsets, v8_offsets
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-2
@@ -43,8 +43,8 @@ def _tile8(Kq, Vq, max_seq):
     n_kv, T, hd = Kq.shape
     kc = np.zeros(n_kv * max_seq * hd, dtype=Kq.dtype)
     vc = np.zeros(n_kv * max_seq * hd, dtype=Vq.dtype)
-    kc[k_offsets(n_kv, T, hd, max_seq).ravel()] = Kq.ravel()
-    vc[v_offsets(n_kv, T, hd, max_seq).ravel()] = Vq.ravel()
+    kc[k8_offsets(n_kv, T, hd, max_seq).ravel()] = Kq.ravel()
+    vc[v8_offsets(n_kv, T, hd, max_seq).ravel()] = Vq.ravel()
     return kc, vc
 
 
@@ -105,7 +105,7 @@ def test_attention_kv8_matches_oracle(g, fmt, H, KV, hd, T):
     cq.check(cq.lib.cq_memcpy_d2h(vc2.ctypes.data, pv, vc2.nbytes))
     cq.check(cq.lib.cq_memcpy_d2h(ks2.ctypes.data, pks, ks2.nbytes))
     cq.check(cq.lib.cq_memcpy_d2h(vs2.ctypes.data, pvs, vs2.nbytes))
-    ko, vo = k_offsets(KV, T, hd, ms), v_offsets(KV, T, hd, ms)
+    ko, vo = k8_offsets(KV, T, hd, ms), v8_offsets(KV, T, hd, ms)
     np.testing.assert_array_equal(kc2[ko[:, T - 1]], Kq[:, T - 1])
     np.testing.assert_array_equal(vc2[vo[:, T - 1]], Vq[:, T - 1])
     np.testing.assert_array_equal(ks2[:, T - 1], Ks[:, T - 1])

@@ -133,3 +133,29 @@ def test_kv_tile_layout_is_a_bijection():
     k = {cq.lib.cq_kv_k_offset(h, t, d, ms, hd) for h in range(2) for t in range(ms) for d in range(hd)}
     v = {cq.lib.cq_kv_v_offset(h, t, d, ms, hd) for h in range(2) for t in range(ms) for d in range(hd)}
     assert k == set(range(2 * ms * hd)) and v == set(range(2 * ms * hd))
+
+
+@pytest.mark.parametrize("hd", [64, 128])
+def test_kv8_tile_layout(hd):
+    """The int8 / E4M3 cache layout: a bijection per kv head, equal to the
+    test helpers' vectorised form, and each lane's operand pieces of the
+    instruction pairs (kk, kk+1) for K and (dt, dt+1) for V form one
+    contiguous 16-byte run."""
+    from tests.gpu_util import k8_offsets, v8_offsets
+    ms = 64
+    k = np.array([[[cq.lib.cq_kv8_k_offset(h, t, d, ms, hd) for d in range(hd)] for t in range(ms)] for h in range(2)])
+    v = np.array([[[cq.lib.cq_kv8_v_offset(h, t, d, ms, hd) for d in range(hd)] for t in range(ms)] for h in range(2)])
+    assert set(k.ravel()) == set(range(2 * ms * hd)) and set(v.ravel()) == set(range(2 * ms * hd))
+    assert np.array_equal(k, k8_offsets(2, ms, hd, ms)) and np.array_equal(v, v8_offsets(2, ms, hd, ms))
+    for t in (0, 5, 17, 63):
+        for kk in range(0, hd // 32, 2):
+            for j in range(4):
+                run = [k[1, t, kk * 32 + j * 8 + e] for e in range(8)] + [k[1, t, (kk + 1) * 32 + j * 8 + e] for e in range(8)]
+                assert run == list(range(run[0], run[0] + 16)) and run[0] % 16 == 0
+        for dt in range(0, hd // 16, 2):
+            for dl in (0, 9, 15):
+                # the 8 keys of one V piece: key slots j*8 + e of the 32-key tile
+                t0 = (t // 32) * 32
+                keys = [t0 + 4 * (t % 16 // 4) + (e if e < 4 else 16 + e - 4) for e in range(8)]
+                run = [v[0, kt, dt * 16 + dl] for kt in keys] + [v[0, kt, (dt + 1) * 16 + dl] for kt in keys]
+                assert run == list(range(run[0], run[0] + 16)) and run[0] % 16 == 0
