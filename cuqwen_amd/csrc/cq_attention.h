@@ -264,6 +264,57 @@ __device__ __forceinline__ void load_tile8(KVTile8<HD>& t, const int8_t* kbase, 
   }
 }
 
+// The codes and scales of one kv head read through buffer resources, as
+// KVRes does for the fp16 cache: a tile past the partition reads through
+// resources of zero records (zeros, no memory request), so every path of
+// the tile loop issues the same loads and each wait names only the tile
+// being attended.
+struct KVRes8 {
+  const int8_t* k;
+  const int8_t* v;
+  const float* ks;
+  const float* vs;
+  int bytes;    // one kv head's K (or V) codes
+  int sbytes;   // one kv head's K (or V) scales
+};
+
+template <int HD>
+__device__ __forceinline__ void load_tile8(KVTile8<HD>& t, const KVRes8& r, int ti, bool valid, int lane) {
+  constexpr int kNT = 2;   // cache policy: non-temporal (streamed once)
+  const __amdgpu_buffer_rsrc_t rk =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(r.k), (short)0, valid ? r.bytes : 0, kBufWord3);
+  const __amdgpu_buffer_rsrc_t rv =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(r.v), (short)0, valid ? r.bytes : 0, kBufWord3);
+  const __amdgpu_buffer_rsrc_t rks =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(r.ks), (short)0, valid ? r.sbytes : 0, kBufWord3);
+  const __amdgpu_buffer_rsrc_t rvs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(r.vs), (short)0, valid ? r.sbytes : 0, kBufWord3);
+  const int soff = valid ? ti * (kTileKeys * HD) : 0;
+  const int ssoff = valid ? ti * (kTileKeys * 4) : 0;
+#pragma unroll
+  for (int st = 0; st < 2; ++st)
+#pragma unroll
+    for (int kk = 0; kk < HD / 32; kk += 2) {
+      const u4_t w = __builtin_bit_cast(
+          u4_t, __builtin_amdgcn_raw_buffer_load_b128(rk, st * 16 * HD + ((kk / 2) * 64 + lane) * 16, soff, kNT));
+      t.ka[st][kk] = u2_t{w.x, w.y};
+      t.ka[st][kk + 1] = u2_t{w.z, w.w};
+    }
+#pragma unroll
+  for (int dt = 0; dt < HD / 16; dt += 2) {
+    const u4_t w =
+        __builtin_bit_cast(u4_t, __builtin_amdgcn_raw_buffer_load_b128(rv, ((dt / 2) * 64 + lane) * 16, soff, kNT));
+    t.va[dt] = u2_t{w.x, w.y};
+    t.va[dt + 1] = u2_t{w.z, w.w};
+  }
+  const int j = lane >> 4;
+#pragma unroll
+  for (int st = 0; st < 2; ++st) {
+    t.ks[st] = __builtin_bit_cast(f4_t, __builtin_amdgcn_raw_buffer_load_b128(rks, (st * 16 + 4 * j) * 4, ssoff, 0));
+    t.vs[st] = __builtin_bit_cast(f4_t, __builtin_amdgcn_raw_buffer_load_b128(rvs, (st * 16 + 4 * j) * 4, ssoff, 0));
+  }
+}
+
 // 8 int8 (natural order) -> 8 exact fp16: (byte ^ 0x80) under the exponent
 // pattern 0x64 is 1024 + q + 128; minus 1152 leaves q.
 __device__ __forceinline__ h8_t i8x8_to_h8(u2_t w, uint32_t magic_v) {

@@ -132,9 +132,12 @@ __global__ __launch_bounds__(kAttnThreads) void attention_stage1_kv8(const AttnA
       for (int i = 0; i < E; ++i) xnew[kind][i] = (float)src[i];
     }
   }
+  // codes and scales through buffer resources (KVRes8): the loop issues the
+  // same loads on every path, so each wait names only the tile attended
+  const KVRes8 kv{kbase, vbase, ksc, vsc, a.max_seq * HD, a.max_seq * 4};
   KVTile8<HD> A, B;
   int ti = tile0 + wave;
-  if (ti < tile1) load_tile8<HD>(A, kbase, vbase, ksc, vsc, ti, lane);
+  load_tile8<HD>(A, kv, ti, ti < tile1, lane);
   h8_t qb[KK];
   {
     const _Float16* q = reinterpret_cast<const _Float16*>(a.q) + (int64_t)(kvh * g + h) * HD;
@@ -144,12 +147,10 @@ __global__ __launch_bounds__(kAttnThreads) void attention_stage1_kv8(const AttnA
       else qb[kk] = h8_t{0, 0, 0, 0, 0, 0, 0, 0};
     }
   }
-  // q goes out before the second tile: the first tile's scores wait only
-  // for the first tile and q
-  if (ti + kAttnWaves < tile1) load_tile8<HD>(B, kbase, vbase, ksc, vsc, ti + kAttnWaves, lane);
-  // the owner quantizes the new rows while its tiles are in flight (the
-  // loaded tile's copy of that position is replaced by the patch, so whether
-  // the load sees the old or the new bytes does not matter)
+  // The owner quantizes the new rows while its first tile is in flight and
+  // patches them into its loaded tile (the tile's copy of that position is
+  // replaced, so whether the load saw the old or the new bytes does not
+  // matter); the codes and scales also go to the cache for later steps.
   __shared__ __align__(16) int8_t newq[2][HD];
   __shared__ float news[2];
   if (owns_new) {
@@ -171,23 +172,20 @@ __global__ __launch_bounds__(kAttnThreads) void attention_stage1_kv8(const AttnA
     }
     __builtin_amdgcn_wave_barrier();
   }
-
   float m = -INFINITY, l = 0.f;
   f4_t o[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) o[dt] = f4_t{0.f, 0.f, 0.f, 0.f};
   const int kp = pos & (kTileKeys - 1);
-  // A and B each hold (or have in flight) one tile; a buffer is refilled as
-  // soon as its tile has been computed
   for (; ti < tile1; ti += 2 * kAttnWaves) {
     const int t1 = ti + kAttnWaves;
+    load_tile8<HD>(B, kv, t1, t1 < tile1, lane);
     if (owns_new && ti == last) patch_key8<HD>(A, kp, newq[0], newq[1], news[0], news[1], lane);
     attend_tile8<HD, F>(A, qb, ti, T, scale, j, m, l, o, magic);
-    if (t1 + kAttnWaves < tile1) load_tile8<HD>(A, kbase, vbase, ksc, vsc, t1 + kAttnWaves, lane);
     if (t1 >= tile1) break;
+    load_tile8<HD>(A, kv, t1 + kAttnWaves, t1 + kAttnWaves < tile1, lane);
     if (owns_new && t1 == last) patch_key8<HD>(B, kp, newq[0], newq[1], news[0], news[1], lane);
     attend_tile8<HD, F>(B, qb, t1, T, scale, j, m, l, o, magic);
-    if (t1 + 2 * kAttnWaves < tile1) load_tile8<HD>(B, kbase, vbase, ksc, vsc, t1 + 2 * kAttnWaves, lane);
   }
   l += __shfl_xor(l, 16, kWave);
   l += __shfl_xor(l, 32, kWave);
