@@ -422,7 +422,7 @@ def main():
     cfg = cq.preset(args.model, args.quant)
     total = args.warmup + args.steps
     pos0 = args.ctx - total
-    if pos0 < 1 or pos0 + 9 > args.ctx:
+    if pos0 < 1 or args.ctx < 10:
         raise SystemExit("ctx too small for warmup + steps")
     t0 = time.perf_counter()
     w = cq.synth_weights(cfg, 0x5157454E)
@@ -433,9 +433,9 @@ def main():
     tok = int(cq.lib.cq_synth_uniform(42, 0, 0, cfg.vocab_size))
     # Untimed: one chained decode of 8 steps records, instantiates and uploads
     # both step graphs (1-step and 8-step) and replays each once, whatever
-    # --warmup is; the warm-up below starts at the same position and
-    # overwrites those cache rows with the same values.
-    st.decode(tok, pos0, 9)
+    # --warmup is (it writes cache rows the timed steps rewrite or that only
+    # stand in for the prefilled context).
+    st.decode(tok, min(pos0, args.ctx - 9), 9)
     cq.synchronize()
     # warmup, chained on the device
     warm = st.decode(tok, pos0, args.warmup) if args.warmup > 0 else [tok]
