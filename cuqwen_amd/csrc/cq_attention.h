@@ -193,18 +193,26 @@ __device__ __forceinline__ void block_merge_write(const AttnArgs& a, int kvh, in
   float* ws_o = ws_l + (size_t)a.n_kv * Pmax * 16;
   _Float16* out = reinterpret_cast<_Float16*>(a.out);
 
+  // One head per wave and round (HD is a multiple of 64, so the 64 items of
+  // a wave share their head): lane w & 7 reads wave w's (m, l), the eight
+  // rescale factors exp(m_w - M) are formed once per wave with 8-lane
+  // reductions and broadcast through scalar registers, and each item is then
+  // eight LDS reads and fused multiply-adds.
+  const int w8 = lane & (kAttnWaves - 1);
   for (int idx = threadIdx.x; idx < g * HD; idx += kAttnThreads) {
-    const int hh = idx / HD, d = idx % HD;
-    float M = -INFINITY;
+    const int hh = __builtin_amdgcn_readfirstlane(idx / HD), d = idx % HD;
+    const float mw = wm[w8][hh], lw = wl[w8][hh];
+    float M = mw;
 #pragma unroll
-    for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, wm[w][hh]);
-    float L = 0.f, O = 0.f;
+    for (int sh = 1; sh < kAttnWaves; sh <<= 1) M = fmaxf(M, __shfl_xor(M, sh, kWave));
+    const float f = mw == -INFINITY ? 0.f : __expf(mw - M);
+    float L = lw * f;
 #pragma unroll
-    for (int w = 0; w < kAttnWaves; ++w) {
-      const float f = wm[w][hh] == -INFINITY ? 0.f : __expf(wm[w][hh] - M);
-      L += wl[w][hh] * f;
-      O += wo[w][hh][d] * f;
-    }
+    for (int sh = 1; sh < kAttnWaves; sh <<= 1) L += __shfl_xor(L, sh, kWave);
+    float O = 0.f;
+#pragma unroll
+    for (int w = 0; w < kAttnWaves; ++w)
+      O = fmaf(wo[w][hh][d], __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, f), w)), O);
     if (nparts == 1) {
       out[(int64_t)(kvh * g + hh) * HD + d] = (_Float16)(O * (1.0f / (L + 1e-9f)));
     } else {
