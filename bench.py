@@ -46,7 +46,7 @@ def parse():
                     help="also measure decode (and prefill) at every BASELINE config (adds about a minute)")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--attention-compare", action="store_true",
-                    help="also time the MFMA tiled decode attention against the VALU head-major one at 7B, T=32768")
+                    help="also time the tiled decode attention against the head-major (reference layout) one at 7B, T=32768")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a 256 MiB device-to-device copy (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     return ap.parse_args()
@@ -127,12 +127,14 @@ def floors_leg(cq, kernels):
 
 
 def attention_compare_leg(cq, np):
-    """The engine's decode attention (MFMA-tiled cache, cq_gqa_attention_decode)
-    against the reference-layout compatibility path (head-major cache, VALU,
-    cq_gqa_attention_decode_hm) at Qwen2.5-7B shapes, position 32767, over 8
-    layer caches (537 MB > the 256 MB last-level cache), 3 rounds each.
-    Wall-clock per call includes the launches (no graph); rocprofv3's kernel
-    trace of this leg gives the kernel durations."""
+    """The engine's decode attention (MFMA-ordered tiled cache,
+    cq_gqa_attention_decode) against the reference-layout compatibility path
+    (head-major cache and the reference's partial buffers,
+    cq_gqa_attention_decode_hm, also on the matrix cores) at Qwen2.5-7B
+    shapes, position 32767, over 8 layer caches (537 MB > the 256 MB
+    last-level cache), 3 rounds each.  Wall-clock per call includes the
+    launches (no graph); rocprofv3's kernel trace of this leg gives the
+    kernel durations."""
     H, KV, hd, ms, lay = 28, 4, 128, 32768, 8
     nbytes = KV * ms * hd * 2
     rng = np.random.default_rng(0)
@@ -150,7 +152,7 @@ def attention_compare_leg(cq, np):
     headmajor = lambda l: cq.lib.cq_gqa_attention_decode_hm(q.ptr, ks[l].ptr, vs[l].ptr, out.ptr, dpos.ptr, H, KV, hd,
                                                              ms, po.ptr, pm.ptr, psum.ptr, None)
     res = {"shape": "H=28 KV=4 hd=128 T=32768", "bytes": 2 * nbytes}
-    for name, f in (("mfma_tiled", tiled), ("valu_head_major", headmajor)):
+    for name, f in (("tiled", tiled), ("head_major", headmajor)):
         for l in range(lay):
             cq.check(f(l))   # warm-up
         cq.synchronize()

@@ -165,12 +165,14 @@ __device__ __forceinline__ void attend_partition(KVTile<HD>& A, KVTile<HD>& B, c
   l += __shfl_xor(l, 32, kWave);
 }
 
-// Merge of the block's 8 waves in LDS (per wave m[16], l[16], O[16][HD]);
-// the block writes one (m, l, O) partial into the workspace, or the
-// normalised output itself when a single partition covers the context.
+// Merge of the block's 8 waves in LDS (per wave m[16], l[16], O[16][HD]).
+// The merged (m, l, O) of head hh goes to slot (kvh * 16 + hh) * Pmax + part
+// of ws_m / ws_l / ws_o (O: HD floats per slot), or, when out is non-NULL
+// (a single partition covers the context), the normalised output to
+// out[(kvh * g + hh) * HD + d].
 template <int HD>
-__device__ __forceinline__ void block_merge_write(const AttnArgs& a, int kvh, int part, int nparts, int g, float m,
-                                                  float l, const f4_t* o) {
+__device__ __forceinline__ void block_merge_store(int kvh, int part, int g, float m, float l, const f4_t* o,
+                                                  float* ws_m, float* ws_l, float* ws_o, int Pmax, _Float16* out) {
   constexpr int DT = HD / 16;
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
   const int h = lane & 15, j = lane >> 4;
@@ -184,14 +186,6 @@ __device__ __forceinline__ void block_merge_write(const AttnArgs& a, int kvh, in
       for (int i = 0; i < 4; ++i) wo[wave][h][dt * 16 + 4 * j + i] = o[dt][i];
   }
   __syncthreads();
-
-  // partial slots head-major: slot (kvh * 16 + head) * Pmax + part, so the
-  // merge reads each head's partitions as one contiguous run
-  float* ws_m = reinterpret_cast<float*>(a.workspace);
-  const int Pmax = gridDim.x;
-  float* ws_l = ws_m + (size_t)a.n_kv * Pmax * 16;
-  float* ws_o = ws_l + (size_t)a.n_kv * Pmax * 16;
-  _Float16* out = reinterpret_cast<_Float16*>(a.out);
 
   // One head per wave and round (HD is a multiple of 64, so the 64 items of
   // a wave share their head): lane w & 7 reads wave w's (m, l), the eight
@@ -213,7 +207,7 @@ __device__ __forceinline__ void block_merge_write(const AttnArgs& a, int kvh, in
 #pragma unroll
     for (int w = 0; w < kAttnWaves; ++w)
       O = fmaf(wo[w][hh][d], __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, f), w)), O);
-    if (nparts == 1) {
+    if (out) {
       out[(int64_t)(kvh * g + hh) * HD + d] = (_Float16)(O * (1.0f / (L + 1e-9f)));
     } else {
       const size_t slot = ((size_t)kvh * 16 + hh) * Pmax + part;
@@ -221,6 +215,20 @@ __device__ __forceinline__ void block_merge_write(const AttnArgs& a, int kvh, in
       if (d == 0) { ws_m[slot] = M; ws_l[slot] = L; }
     }
   }
+}
+
+// The engine's partials: workspace [m: n_kv*16*P][l: n_kv*16*P][o: n_kv*16*P*HD]
+// floats, slots head-major so the merge reads each head's partitions as one
+// contiguous run; a single partition writes the output itself.
+template <int HD>
+__device__ __forceinline__ void block_merge_write(const AttnArgs& a, int kvh, int part, int nparts, int g, float m,
+                                                  float l, const f4_t* o) {
+  float* ws_m = reinterpret_cast<float*>(a.workspace);
+  const int Pmax = gridDim.x;
+  float* ws_l = ws_m + (size_t)a.n_kv * Pmax * 16;
+  float* ws_o = ws_l + (size_t)a.n_kv * Pmax * 16;
+  block_merge_store<HD>(kvh, part, g, m, l, o, ws_m, ws_l, ws_o, Pmax,
+                        nparts == 1 ? reinterpret_cast<_Float16*>(a.out) : nullptr);
 }
 
 // ------------------------------------------------------- quantized KV cache
