@@ -98,6 +98,7 @@ def _load():
         "cq_state_kv_read": (I32, [P, I32, I32, I32, I32, P]),
         "cq_state_kv_write": (I32, [P, I32, I32, I32, I32, P]),
         "cq_state_last_decode_us": (I32, [P, ctypes.POINTER(ctypes.c_double)]),
+        "cq_state_set_attention_mode": (I32, [P, I32]),
         "cq_prefill": (I32, [P, IP, I32, I32, IP]),
         "cq_state_last_prefill_us": (I32, [P, ctypes.POINTER(ctypes.c_double)]),
         "cq_synth_normal": (ctypes.c_uint16, [U64, U64, U64, F]),
@@ -168,7 +169,7 @@ EXPORTED = [
     "cq_forward", "cq_forward_ex", "cq_decode", "cq_state_logits", "cq_state_fill_kv", "cq_state_kv_read", "cq_state_kv_write",
     "cq_prefill", "cq_state_last_prefill_us", "cq_state_create_kv", "cq_gqa_attention_decode_kv8",
     "cq_gqa_attention_decode_fp8",
-    "cq_state_last_decode_us", "cq_synth_normal", "cq_synth_uniform", "cq_tensor_stream_id", "cq_kv_stream_id",
+    "cq_state_last_decode_us", "cq_state_set_attention_mode", "cq_synth_normal", "cq_synth_uniform", "cq_tensor_stream_id", "cq_kv_stream_id",
     "cq_quantize", "cq_device_count", "cq_malloc", "cq_free", "cq_memcpy_h2d", "cq_memcpy_d2h", "cq_memset", "cq_memcpy_d2d",
     "cq_synchronize", "cq_embedding_lookup", "cq_rmsnorm", "cq_gemv", "cq_gemv_add", "cq_fused_attn_block",
     "cq_fused_mlp_stage1", "cq_fused_mlp_stage2", "cq_compute_logits", "cq_apply_repetition_penalty",
@@ -189,6 +190,7 @@ def check(rc):
 
 
 KV_FP16, KV_INT8, KV_FP8 = 0, 1, 2
+ATTN_SPLIT, ATTN_WHOLE_CONTEXT = 0, 1
 
 
 def preset(model, quant="int8"):
@@ -382,6 +384,10 @@ class State:
         us = ctypes.c_double()
         check(lib.cq_state_last_decode_us(self.handle, ctypes.byref(us)))
         return us.value
+
+    def set_attention_mode(self, mode):
+        """ATTN_SPLIT (default) or ATTN_WHOLE_CONTEXT (cq_state_set_attention_mode)."""
+        check(lib.cq_state_set_attention_mode(self.handle, mode))
 
     def logits(self):
         out = np.zeros(self.cfg.vocab_size, dtype=np.uint16)

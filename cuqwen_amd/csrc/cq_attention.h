@@ -168,8 +168,8 @@ __device__ __forceinline__ void attend_partition(KVTile<HD>& A, KVTile<HD>& B, c
 // Merge of the block's 8 waves in LDS (per wave m[16], l[16], O[16][HD]).
 // The merged (m, l, O) of head hh goes to slot (kvh * 16 + hh) * Pmax + part
 // of ws_m / ws_l / ws_o (O: HD floats per slot), or, when out is non-NULL
-// (a single partition covers the context), the normalised output to
-// out[(kvh * g + hh) * HD + d].
+// (a single partition covers the context), the normalised output of the
+// group's head hh to out[hh * HD + d] (global memory or LDS).
 template <int HD>
 __device__ __forceinline__ void block_merge_store(int kvh, int part, int g, float m, float l, const f4_t* o,
                                                   float* ws_m, float* ws_l, float* ws_o, int Pmax, _Float16* out) {
@@ -208,7 +208,7 @@ __device__ __forceinline__ void block_merge_store(int kvh, int part, int g, floa
     for (int w = 0; w < kAttnWaves; ++w)
       O = fmaf(wo[w][hh][d], __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, f), w)), O);
     if (out) {
-      out[(int64_t)(kvh * g + hh) * HD + d] = (_Float16)(O * (1.0f / (L + 1e-9f)));
+      out[hh * HD + d] = (_Float16)(O * (1.0f / (L + 1e-9f)));
     } else {
       const size_t slot = ((size_t)kvh * 16 + hh) * Pmax + part;
       ws_o[slot * HD + d] = O;
@@ -228,7 +228,7 @@ __device__ __forceinline__ void block_merge_write(const AttnArgs& a, int kvh, in
   float* ws_l = ws_m + (size_t)a.n_kv * Pmax * 16;
   float* ws_o = ws_l + (size_t)a.n_kv * Pmax * 16;
   block_merge_store<HD>(kvh, part, g, m, l, o, ws_m, ws_l, ws_o, Pmax,
-                        nparts == 1 ? reinterpret_cast<_Float16*>(a.out) : nullptr);
+                        nparts == 1 ? reinterpret_cast<_Float16*>(a.out) + (int64_t)kvh * g * HD : nullptr);
 }
 
 // ------------------------------------------------------- quantized KV cache

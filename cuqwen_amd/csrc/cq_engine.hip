@@ -196,6 +196,7 @@ struct cq_state {
   hipGraphExec_t exec = nullptr;
   hipGraph_t graph_run = nullptr;       // kStepsPerRun chained steps (cq_decode)
   hipGraphExec_t exec_run = nullptr;
+  int attn_mode = CQ_ATTN_SPLIT;        // cq_state_set_attention_mode
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
   double last_us = 0.0;
   double last_prefill_us = 0.0;
@@ -310,8 +311,12 @@ int layer_step(cq_state* s, int l, hipStream_t st) {
   layer_gemvs(s, l, &qkv, &m1, &m2);
   fused_mlp(s, &m1, &m2);
   CQ_TRY(launch_gemv(qkv, st));
-  CQ_TRY(launch_attention_stage1(layer_attn(s, l), st));
-  CQ_TRY(launch_omerge(layer_omerge(s, l), st));
+  if (s->attn_mode == CQ_ATTN_WHOLE_CONTEXT) {
+    CQ_TRY(launch_attn_oproj(layer_attn(s, l), layer_omerge(s, l), st));
+  } else {
+    CQ_TRY(launch_attention_stage1(layer_attn(s, l), st));
+    CQ_TRY(launch_omerge(layer_omerge(s, l), st));
+  }
   CQ_TRY(launch_gemv(m1, st));
   CQ_TRY(launch_gemv(m2, st));
   return CQ_OK;
@@ -395,10 +400,7 @@ int set_ctl(cq_state* s, int token, int pos, const int32_t* history, int history
 // or a switch to another weight set of the same shape).  The recorded step
 // graph holds the old weight pointers, so it is dropped and recorded again
 // on the next step.
-int bind_weights(cq_state* s, const cq_weights* w) {
-  if (!w || w == s->w) return CQ_OK;
-  if (std::memcmp(&s->cfg, &w->cfg, offsetof(cq_config, norm_eps)) != 0)
-    return fail(CQ_EINVAL, "forward: the weights do not match the state's config");
+int drop_graphs(cq_state* s) {
   if (s->exec) {
     CQ_HIP(hipStreamSynchronize(s->stream));
     hipGraphExecDestroy(s->exec);
@@ -416,6 +418,14 @@ int bind_weights(cq_state* s, const cq_weights* w) {
     hipGraphDestroy(s->graph_run);
     s->graph_run = nullptr;
   }
+  return CQ_OK;
+}
+
+int bind_weights(cq_state* s, const cq_weights* w) {
+  if (!w || w == s->w) return CQ_OK;
+  if (std::memcmp(&s->cfg, &w->cfg, offsetof(cq_config, norm_eps)) != 0)
+    return fail(CQ_EINVAL, "forward: the weights do not match the state's config");
+  CQ_TRY(drop_graphs(s));
   s->w = w;
   return CQ_OK;
 }
@@ -783,6 +793,17 @@ extern "C" int cq_decode(cq_state* s, int32_t token, int32_t pos0, int32_t n_ste
   return CQ_OK;
 }
 
+extern "C" int cq_state_set_attention_mode(cq_state* s, int32_t mode) {
+  if (!s) return fail(CQ_EINVAL, "attention mode: null state");
+  if (mode != CQ_ATTN_SPLIT && mode != CQ_ATTN_WHOLE_CONTEXT) return fail(CQ_EINVAL, "attention mode: unknown mode");
+  if (mode == CQ_ATTN_WHOLE_CONTEXT && s->kv_dtype != CQ_KV_FP16)
+    return fail(CQ_EINVAL, "attention mode: the whole-context launch reads the fp16 cache only");
+  if (mode == s->attn_mode) return CQ_OK;
+  CQ_TRY(drop_graphs(s));   // the recorded steps hold the other mode's launches
+  s->attn_mode = mode;
+  return CQ_OK;
+}
+
 extern "C" int cq_state_last_decode_us(cq_state* s, double* us) {
   if (!s || !us) return fail(CQ_EINVAL, "null argument");
   *us = s->last_us;
@@ -1108,12 +1129,16 @@ extern "C" int cq_state_profile(cq_state* s, int32_t pos, int32_t iters, int32_t
       {"down_residual", wbytes(qt, d, I) + 2 * I + 2 * d * 2, 4},
       {"lm_head", wbytes(lmq, V, d) + 2 * d * 2 + 2 * V, 5},
       {"argmax", 8.0 * kArgmaxPartials, 6},   // the lm_head GEMV already reduced the logits to one key per wave
+      // the whole-context mode's attention + O-projection (one launch; not in the default step)
+      {"attn_oproj_whole_context", 2.0 * c.n_kv_heads * T * c.head_dim * 2 + 2 * qd * 2 + wbytes(qt, d, qd) + 8 * d * (double)c.n_kv_heads, 7},
   };
-  const int nk = (int)(sizeof ks / sizeof ks[0]);
+  // (timed only where one kv head's K and V are at most 4 MiB: beyond that it runs for milliseconds)
+  const bool short_ok = s->kv_dtype == CQ_KV_FP16 && T * c.head_dim * 4 <= 4.0 * 1024 * 1024;
+  const int nk = (int)(sizeof ks / sizeof ks[0]) - (short_ok ? 0 : 1);
   int n = 0;
   for (int i = 0; i < nk && n < max_kernels; ++i, ++n) {
     const K& k = ks[i];
-    const bool per_layer = k.kind <= 4;
+    const bool per_layer = k.kind <= 4 || k.kind == 7;
     const int reps = per_layer ? c.n_layers : 1;
     auto run = [&]() -> int {
       for (int l = 0; l < reps; ++l) {
@@ -1133,6 +1158,7 @@ extern "C" int cq_state_profile(cq_state* s, int32_t pos, int32_t iters, int32_t
             break;
           }
           case 6: CQ_TRY(launch_argmax_reduce(s->argmax_ws, kArgmaxPartials, nullptr, nullptr, nullptr, nullptr, s->stream)); break;
+          case 7: CQ_TRY(launch_attn_oproj(layer_attn(s, l), layer_omerge(s, l), s->stream)); break;
         }
       }
       return CQ_OK;

@@ -114,6 +114,11 @@ int wo_to_panels(int quant, void* W, __half* S, int N, int K, void* tmp, hipStre
 int wo_from_panels(int quant, const void* W, const __half* S, int N, int K, void* W_rows, __half* S_rows,
                    hipStream_t stream);
 int omerge_plan(int quant, int head_dim, int n_heads, int N, int* hpb, int* bands, int* rounds, int* wm);
+// Short contexts (cq_omerge.hip): attention over the whole fp16 cache and
+// the O-projection in one launch, block (kv head, row band) recomputing its
+// group's attention; same accumulator as launch_omerge.
+int launch_attn_oproj(const AttnArgs& at, const OMergeArgs& a, hipStream_t stream);
+int attn_oproj_plan(int quant, int head_dim, int n_heads, int n_kv, int N, int* bands, int* rounds, int* cpl);
 // Head-major cache path (cq_attention_hm.hip): the reference's layout and
 // partial buffers (partial index (kv_head * 16 + head) * 64 + partition).
 int launch_attention_hm(const __half* q, const __half* kc, const __half* vc, __half* out, const int* d_pos,

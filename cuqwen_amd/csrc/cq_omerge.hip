@@ -261,6 +261,204 @@ static void omerge_launch_q(const OMergeArgs& a, hipStream_t stream, int nr, int
   omerge_launch_h<Q, HD, HD == 64 ? 2 : 1>(a, stream, nr, wm, blocks);
 }
 
+// ------------------------------------------- short contexts: attention + O-projection
+// When a kv head's whole context is short, its attention is cheap enough to
+// compute in every block that needs it, and the split over partitions (and
+// the launch boundary between stage 1 and the merge) can go.  Block (kv head
+// k, row band c) runs stage 1's tile loop over all T keys with its 8 waves
+// (wave w takes tiles w, w + 8, ...), merges the waves in LDS into the
+// group's normalised attention output -- exactly what a single-partition
+// stage 1 writes -- and multiplies it by Wo[band rows][group columns]: the
+// g heads of the group are g * hd contiguous columns of Wo, read here as
+// 16-byte chunks through the 128-column panel layout.  One fixed-point
+// atomic per row and kv head into the same accumulator as omerge_kernel,
+// so the MLP launch that follows is unchanged.
+//
+// Lanes of a row: the group's chunks per row padded to a power of two P2,
+// CPL chunks per lane (P2 / CPL <= 64 lanes), rows per wave 64 / (P2 / CPL);
+// NR rounds of rows per wave, all requested before the attention starts.
+template <int Q, int HD, int NR, int CPL>
+__global__ __launch_bounds__(kAttnThreads) void attn_oproj_kernel(const AttnArgs at, const OMergeArgs a) {
+  using T = QTraits<Q>;
+  pin_attn_args<false>(at);
+  CQ_PIN(a.W); CQ_PIN(a.acc); CQ_PIN(a.N); CQ_PIN(a.bands);
+  if constexpr (Q != CQ_QUANT_FP16) CQ_PIN(a.S);
+  constexpr int KK = HD / 32, DT = HD / 16;
+  constexpr int CP = kGroup / T::EPC;   // chunks of a panel row
+  __shared__ __align__(16) _Float16 attn_s[16 * HD];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const uint32_t gi = om_order(blockIdx.x, gridDim.x);   // a kv head's bands share an XCD's L2 copy of its K/V
+  const uint32_t bands = (uint32_t)a.bands, N = (uint32_t)a.N;
+  const int kvh = (int)(gi / bands), band = (int)(gi % bands);
+  const int row0 = (int)(((uint32_t)band * N) / bands);
+  const int row1 = (int)(((uint32_t)(band + 1) * N) / bands);
+  const int g = at.n_heads / at.n_kv;
+  const int Tn = (int)load_ctl_u32(at.d_pos) + 1;
+  const int n_tiles = (Tn + kTileKeys - 1) / kTileKeys;
+
+  // 1. the wave's first K/V tile, then q of the group (stage 1's order)
+  const _Float16* kbase = reinterpret_cast<const _Float16*>(at.kcache) + (int64_t)kvh * at.max_seq * HD;
+  const _Float16* vbase = reinterpret_cast<const _Float16*>(at.vcache) + (int64_t)kvh * at.max_seq * HD;
+  const KVRes kv{kbase, vbase, at.max_seq * HD * 2};
+  KVTile<HD> A, B;
+  int ti = wave;
+  load_tile<HD>(A, kv, ti, ti < n_tiles, lane);
+  const int h = lane & 15, j = lane >> 4;
+  h8_t qb[KK];
+  {
+    const _Float16* q = reinterpret_cast<const _Float16*>(at.q) + (int64_t)(kvh * g + h) * HD;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      if (h < g) qb[kk] = __builtin_bit_cast(h8_t, load_u4(q + kk * 32 + j * 8));
+      else qb[kk] = h8_t{0, 0, 0, 0, 0, 0, 0, 0};
+    }
+  }
+
+  // 2. the band's weight slice (consumed after the attention)
+  const int nchg = g * HD / T::EPC;   // chunks of the group's columns in one row
+  int p2 = 1;
+  while (p2 < nchg) p2 <<= 1;
+  const int lpr = p2 / CPL;           // lanes per row (host-checked <= 64)
+  const int rpw = kWave / lpr, rpr = kAttnWaves * rpw;
+  const int lrow = lane / lpr, cl = lane % lpr;
+  u4_t wv[NR][CPL];
+  _Float16 sc[NR][CPL];
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    const uint32_t row = (uint32_t)min(row0 + r * rpr + wave * rpw + lrow, row1 - 1);
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      const int ch = cl + c * lpr;
+      wv[r][c] = u4_t{0u, 0u, 0u, 0u};
+      sc[r][c] = (_Float16)0.f;
+      if (ch < nchg) {
+        const uint32_t kc = (uint32_t)(kvh * nchg + ch), pan = kc / CP;
+        wv[r][c] = load_u4_stream(reinterpret_cast<const char*>(a.W) + ((pan * N + row) * CP + kc % CP) * 16u);
+        if constexpr (Q != CQ_QUANT_FP16) sc[r][c] = reinterpret_cast<const _Float16*>(a.S)[pan * N + row];
+      }
+    }
+  }
+
+  // 3. the whole context, then the 8-wave merge into the normalised output
+  float m = -INFINITY, l = 0.f;
+  f4_t o[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) o[dt] = f4_t{0.f, 0.f, 0.f, 0.f};
+  attend_partition<HD>(A, B, qb, ti, n_tiles, Tn, kv, lane, m, l, o);
+  block_merge_store<HD>(kvh, 0, g, m, l, o, nullptr, nullptr, nullptr, 0, attn_s);
+  __syncthreads();
+
+  // 4. the lane's chunks of the group's output in the GEMV's plane order
+  u4_t xv[CPL][T::PLANES];
+  float corr[CPL];
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const int ch = cl + c * lpr;
+    corr[c] = 0.f;
+    if (ch < nchg) {
+      const u4_t* src = reinterpret_cast<const u4_t*>(attn_s) + ch * T::PLANES;
+#pragma unroll
+      for (int p = 0; p < T::PLANES; ++p) corr[c] += plane_order_packed<Q>(src[p], xv[c][p]);
+    } else {
+#pragma unroll
+      for (int p = 0; p < T::PLANES; ++p) xv[c][p] = u4_t{0u, 0u, 0u, 0u};
+    }
+  }
+
+  // 5. row dots, reduced over the row's lanes, one atomic per row
+  const UnpackRegs uk = unpack_regs();
+  unsigned long long* acc = reinterpret_cast<unsigned long long*>(a.acc);
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    float v = 0.f;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      const float d = chunk_dot<Q>(wv[r][c], xv[c], uk);
+      if constexpr (Q != CQ_QUANT_FP16) v = fmaf(d - corr[c], (float)sc[r][c], v);
+      else v += d;
+    }
+    for (int off = lpr / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+    const int row = row0 + r * rpr + wave * rpw + lrow;
+    if (cl == 0 && row < row1) {
+      v = fminf(kFixClamp, fmaxf(-kFixClamp, v));
+      const long long fx = __float2ll_rn(v * kFixScale);
+      atomicAdd(acc + row, (unsigned long long)fx);
+    }
+  }
+}
+
+int attn_oproj_plan(int quant, int head_dim, int n_heads, int n_kv, int N, int* bands, int* rounds, int* cpl) {
+  const int epc = quant == CQ_QUANT_INT4 ? 32 : quant == CQ_QUANT_INT8 ? 16 : 8;
+  const int nchg = n_heads / n_kv * head_dim / epc;
+  int p2 = 1;
+  while (p2 < nchg) p2 <<= 1;
+  const int c = p2 > kWave ? p2 / kWave : 1;
+  if (c > 2) return fail(CQ_EINVAL, "attention + O-projection: group too wide");
+  const int rpr = kAttnWaves * (kWave / (p2 / c));
+  // rounds of rows per wave that fit the registers beside the attention's
+  // (head_dim 128: NR * CPL <= 4, head_dim 64: NR <= 8)
+  const int max_nr = head_dim == 128 ? 4 / c : 8;
+  int b = std::max(1, kNumCUs / n_kv);
+  b = std::max(b, (N + max_nr * rpr - 1) / (max_nr * rpr));
+  b = std::min(b, N);
+  const int rows = (N + b - 1) / b;
+  const int nr = (rows + rpr - 1) / rpr;
+  int r2 = 1;
+  while (r2 < nr) r2 <<= 1;
+  *bands = b;
+  *rounds = r2;
+  *cpl = c;
+  return CQ_OK;
+}
+
+template <int Q, int HD, int CPL>
+static void attn_oproj_launch_c(const AttnArgs& at, const OMergeArgs& a, int nr, hipStream_t stream) {
+  const dim3 grid(a.n_kv * a.bands), block(kAttnThreads);
+  switch (nr) {
+    case 1: hipLaunchKernelGGL((attn_oproj_kernel<Q, HD, 1, CPL>), grid, block, 0, stream, at, a); break;
+    case 2: hipLaunchKernelGGL((attn_oproj_kernel<Q, HD, 2, CPL>), grid, block, 0, stream, at, a); break;
+    case 4: hipLaunchKernelGGL((attn_oproj_kernel<Q, HD, 4, CPL>), grid, block, 0, stream, at, a); break;
+    default: hipLaunchKernelGGL((attn_oproj_kernel<Q, HD, 8, CPL>), grid, block, 0, stream, at, a); break;
+  }
+}
+
+template <int Q, int HD>
+static void attn_oproj_launch_q(const AttnArgs& at, const OMergeArgs& a, int nr, int cpl, hipStream_t stream) {
+  if (cpl == 2) attn_oproj_launch_c<Q, HD, 2>(at, a, nr, stream);
+  else attn_oproj_launch_c<Q, HD, 1>(at, a, nr, stream);
+}
+
+int launch_attn_oproj(const AttnArgs& at, const OMergeArgs& a0, hipStream_t stream) {
+  OMergeArgs a = a0;
+  if (!at.kcache || !at.vcache || at.kcache8) return fail(CQ_EINVAL, "attention + O-projection: fp16 cache only");
+  if (a.head_dim != 64 && a.head_dim != 128) return fail(CQ_EINVAL, "attention + O-projection: head_dim must be 64 or 128");
+  if (a.quant < 0 || a.quant > 2) return fail(CQ_EINVAL, "attention + O-projection: bad quant type");
+  if (a.n_kv <= 0 || a.n_heads % a.n_kv || a.n_heads / a.n_kv > 16) return fail(CQ_EINVAL, "attention + O-projection: bad head layout");
+  if (a.K != a.n_heads * a.head_dim || a.N <= 0 || a.K % kGroup) return fail(CQ_EINVAL, "attention + O-projection: bad shape");
+  if (at.n_heads != a.n_heads || at.n_kv != a.n_kv || at.head_dim != a.head_dim || at.d_pos != a.d_pos)
+    return fail(CQ_EINVAL, "attention + O-projection: attention and projection shapes differ");
+  if (!at.q || !a.W || !a.acc || !a.d_pos || (a.quant != CQ_QUANT_FP16 && !a.S))
+    return fail(CQ_EINVAL, "attention + O-projection: null pointer");
+  int nr = 1, cpl = 1;
+  CQ_TRY(attn_oproj_plan(a.quant, a.head_dim, a.n_heads, a.n_kv, a.N, &a.bands, &nr, &cpl));
+  if ((int64_t)a.N * a.K * 2 >= ((int64_t)1 << 31) || (int64_t)a.N * (a.bands + 1) >= ((int64_t)1 << 31) ||
+      (int64_t)at.max_seq * a.head_dim * 2 >= ((int64_t)1 << 31))
+    return fail(CQ_EINVAL, "attention + O-projection: shape too large for 32-bit indexing");
+  if (a.quant == CQ_QUANT_INT4) {
+    if (a.head_dim == 128) attn_oproj_launch_q<CQ_QUANT_INT4, 128>(at, a, nr, cpl, stream);
+    else attn_oproj_launch_q<CQ_QUANT_INT4, 64>(at, a, nr, cpl, stream);
+  } else if (a.quant == CQ_QUANT_INT8) {
+    if (a.head_dim == 128) attn_oproj_launch_q<CQ_QUANT_INT8, 128>(at, a, nr, cpl, stream);
+    else attn_oproj_launch_q<CQ_QUANT_INT8, 64>(at, a, nr, cpl, stream);
+  } else {
+    if (a.head_dim == 128) attn_oproj_launch_q<CQ_QUANT_FP16, 128>(at, a, nr, cpl, stream);
+    else attn_oproj_launch_q<CQ_QUANT_FP16, 64>(at, a, nr, cpl, stream);
+  }
+  CQ_HIP(hipGetLastError());
+  return CQ_OK;
+}
+
 // ------------------------------------------------------------ Wo panels
 // Row-major [N][K] (the file's layout) -> K/128 panels of [N][128]: 16-byte
 // chunk c of row n (chunk c % CP of panel c / CP) moves to

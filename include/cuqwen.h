@@ -216,6 +216,20 @@ int cq_state_kv_write(cq_state* s, int32_t layer, int32_t kv_head, int32_t kind,
  * measured with HIP events on the state's stream. */
 int cq_state_last_decode_us(cq_state* s, double* us_per_step);
 
+/* How a decode step does its attention (no counterpart in the reference,
+ * whose attention is always the split-K pair, src/kernels.cu:105-324).
+ * CQ_ATTN_SPLIT (the default): stage 1 over partitions of the context, then
+ * the merge fused into the O-projection -- two launches per layer.
+ * CQ_ATTN_WHOLE_CONTEXT: one launch per layer in which block (kv head, row
+ * band) attends over the whole context itself and projects its group's
+ * output; fp16 KV cache only.  Measured slower than the default at every
+ * shape tried (each block streams its kv head's whole K/V), so it exists to
+ * make that comparison reproducible.  Changing the mode drops the recorded
+ * step graphs; they are recorded again on the next step. */
+#define CQ_ATTN_SPLIT 0
+#define CQ_ATTN_WHOLE_CONTEXT 1
+int cq_state_set_attention_mode(cq_state* s, int32_t mode);
+
 /* ------------------------------------------- synthetic data (host side) */
 /* Deterministic approximately-normal value: Irwin-Hall sum of four 16-bit
  * uniforms from splitmix64(seed, stream, index), scaled to N(0, sigma) and
