@@ -50,6 +50,9 @@ def parse():
     ap.add_argument("--attention", choices=["split", "whole"], default="split",
                     help="attention mode of the main measurement: the split-K pair (default) or one "
                          "whole-context launch per layer (cq_state_set_attention_mode; measured slower)")
+    ap.add_argument("--library-gemm", action="store_true",
+                    help="also time PyTorch's fp16 GEMM (hipBLASLt / rocBLAS) at the shapes of the prefill GEMMs")
+    ap.add_argument("--library-gemm-child", default=None, help=argparse.SUPPRESS)
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a 256 MiB device-to-device copy (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     return ap.parse_args()
@@ -246,6 +249,54 @@ def prefill_leg(cq, cfg, st, n):
                          "frac": round(tflops / 2500.0, 4)}}
 
 
+def library_gemm_shapes(cfg):
+    d, I = cfg.dim, cfg.intermediate_size
+    qkv = (cfg.n_heads + 2 * cfg.n_kv_heads) * cfg.head_dim
+    return [("qkv", qkv, d), ("o_proj", d, cfg.n_heads * cfg.head_dim), ("gate_up", 2 * I, d), ("down", d, I)]
+
+
+def library_gemm_child(n, shapes):
+    """PyTorch's fp16 GEMM (x @ W^T, fp32 accumulation; hipBLASLt or rocBLAS
+    as torch picks) at the shapes of the batched prefill's GEMMs for an
+    n-token chunk: a vendor-library point of comparison for the int4 / int8
+    matrix-core GEMMs, which also dequantize the weights and run their
+    epilogues.  Three weight copies rotate so the weights are not reused
+    from the cache; CUDA events on torch's current stream.  Runs in a child
+    process: torch brings its own HIP runtime, which cannot share a process
+    with the library's."""
+    import torch
+    torch.backends.cuda.matmul.allow_fp16_reduced_precision_reduction = False
+    out = []
+    for name, N, K in shapes:
+        ws = [torch.randn(N, K, device="cuda", dtype=torch.float16) * 0.02 for _ in range(3)]
+        x = torch.randn(n, K, device="cuda", dtype=torch.float16)
+        for i in range(6):
+            y = x @ ws[i % 3].t()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = 30
+        e0.record()
+        for i in range(reps):
+            y = x @ ws[i % 3].t()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / reps
+        out.append({"gemm": name, "M": n, "N": N, "K": K, "us": round(us, 2),
+                    "TFLOPs": round(2.0 * n * N * K / us / 1e6, 1)})
+        del ws, x, y
+    print(json.dumps(out), flush=True)
+
+
+def library_gemm_leg(cfg, n):
+    import subprocess
+    shapes = library_gemm_shapes(cfg)
+    r = subprocess.run([sys.executable, os.path.abspath(__file__), "--library-gemm-child", json.dumps([n, shapes])],
+                       capture_output=True, text=True, timeout=600)
+    if r.returncode != 0:
+        raise SystemExit(f"library GEMM child failed: {r.stderr[-2000:]}")
+    return json.loads(r.stdout.strip().splitlines()[-1])
+
+
 def kv8_leg(cq, cfg, w, pos0, args, fmt):
     """The same decode workload with a quantized KV cache (CQ_KV_INT8 or
     CQ_KV_FP8): tok/s and whole-step bytes (the K/V stream halves)."""
@@ -424,10 +475,18 @@ def main():
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
               "the multi-GPU path is a design note, not built", file=sys.stderr)
         sys.exit(2)
+    if args.library_gemm_child:
+        n, shapes = json.loads(args.library_gemm_child)
+        library_gemm_child(n, shapes)
+        return
     import numpy as np
     import cuqwen_amd as cq
 
     cfg = cq.preset(args.model, args.quant)
+    # before this process touches the GPU (the child brings its own HIP runtime)
+    lib_gemm = library_gemm_leg(cfg, args.prompt) if args.library_gemm else None
+    if lib_gemm is not None:
+        log(f"[bench] library fp16 GEMM at the prefill shapes: {lib_gemm}")
     total = args.warmup + args.steps
     pos0 = args.ctx - total
     if pos0 < 1 or args.ctx < 10:
@@ -539,6 +598,8 @@ def main():
     }
     if attn_cmp is not None:
         res["attention_compare"] = attn_cmp
+    if lib_gemm is not None:
+        res["library_gemm"] = lib_gemm
     print(json.dumps(res), flush=True)
 
 
