@@ -1073,15 +1073,20 @@ static int launch_pf_gemm_m(const PfGemmArgs& a, hipStream_t stream) {
   // Split K when it shortens the GEMM plus its split epilogue.  Model: one
   // block fits a CU (its LDS), so B blocks take ceil(B / CUs) rounds and S
   // splits ceil(S B / CUs) rounds of 1/S the work; a full-K block runs at
-  // ~3.2 TFLOP/s per CU (measured, int4 gate/up); the split epilogue streams
-  // the S fp32 partials at ~5 TB/s after a launch of ~2 us.  Within the
-  // workspace.
+  // ~4.2 TFLOP/s per CU (measured: int4 gate/up, 56 us per round of 256
+  // blocks at K = 3584); the split epilogue reads the S fp32 partials at
+  // ~2.8 TB/s after a launch of ~2 us (measured: QKV's 3 x 18.9 MB in 20.4
+  // us, the residual's 2 x 14.7 MB in 10.7 us).  Within the workspace.
   int S = 1;
   if (a.part) {
     auto rounds = [&](int s) { return (double)(((int64_t)gx * s + kNumCUs - 1) / kNumCUs); };
-    const double t1 = (double)bn * nmat * kPfTok * a.K * 2 / 3.2e6;     // us, one round of full-K blocks
-    const double part_us = (double)nmat * a.M * a.N * sizeof(float) / 5e6;   // us per split of partials
-    double best = rounds(1) * t1;
+    const double t1 = (double)bn * nmat * kPfTok * a.K * 2 / 4.2e6;     // us, one round of full-K blocks
+    const double part_us = (double)nmat * a.M * a.N * sizeof(float) / 2.8e6;   // us per split of partials
+    // QKV's unsplit epilogue (RoPE through an LDS tile, scattered cache
+    // stores) costs about what the split epilogue's pass does (measured: at
+    // 1024 tokens the unsplit QKV launch took ~25 us longer than the 3-way
+    // split plus its epilogue)
+    double best = rounds(1) * t1 + (MODE == GM_QKV ? part_us + 2.0 : 0.0);
     for (int s = 2; s <= std::min(kPfMaxSplit, nks); ++s) {
       if ((size_t)s * nmat * a.M * a.N * sizeof(float) > a.part_bytes) break;
       const double t = rounds(s) / s * t1 + s * part_us + 2.0;
