@@ -50,6 +50,8 @@ def parse():
     ap.add_argument("--attention", choices=["split", "whole"], default="split",
                     help="attention mode of the main measurement: the split-K pair (default) or one "
                          "whole-context launch per layer (cq_state_set_attention_mode; measured slower)")
+    ap.add_argument("--sync-costs", action="store_true",
+                    help="also time a graph node boundary against grid-wide barriers inside one kernel")
     ap.add_argument("--library-gemm", action="store_true",
                     help="also time PyTorch's fp16 GEMM (hipBLASLt / rocBLAS) at the shapes of the prefill GEMMs")
     ap.add_argument("--library-gemm-child", default=None, help=argparse.SUPPRESS)
@@ -132,6 +134,27 @@ def floors_leg(cq, kernels):
             leg["TBps"] = round(n / us.value / 1e6, 3)
         out.append(leg)
         log(f"[bench] floor {leg}")
+    return out
+
+
+def sync_costs_leg(cq):
+    """What a dependency between two stages costs: a graph node boundary
+    (the empty kernel in a graph chain, cq_time_stream with no bytes)
+    against a grid-wide barrier inside one kernel (cq_time_grid_barrier:
+    per-block flags polled by every block, one atomic counter, or flags
+    gathered by one block that releases the rest through one word, and that
+    signalling without memory ordering as the lower bound), at 256 and 128
+    blocks."""
+    import ctypes
+    us = ctypes.c_double()
+    cq.check(cq.lib.cq_time_stream(0, 1, None, 256, ctypes.byref(us)))
+    out = {"graph_node_us": round(us.value, 3), "grid_barrier": []}
+    for kind, name in ((0, "flags"), (1, "counter"), (2, "gather_release"), (3, "gather_release_unordered")):
+        for blocks in (256, 128):
+            t, to = ctypes.c_double(), ctypes.c_int32()
+            cq.check(cq.lib.cq_time_grid_barrier(kind, blocks, 200, ctypes.byref(t), ctypes.byref(to)))
+            out["grid_barrier"].append({"kind": name, "blocks": blocks, "us": round(t.value, 3),
+                                        "timed_out": bool(to.value)})
     return out
 
 
@@ -572,6 +595,10 @@ def main():
         dst.free()
 
     legs = config_legs(cq) if args.configs else None
+    sync = None
+    if args.sync_costs:
+        sync = sync_costs_leg(cq)
+        log(f"[bench] sync costs: {sync}")
     attn_cmp = None
     if args.attention_compare:
         attn_cmp = attention_compare_leg(cq, np)
@@ -600,6 +627,8 @@ def main():
         res["attention_compare"] = attn_cmp
     if lib_gemm is not None:
         res["library_gemm"] = lib_gemm
+    if sync is not None:
+        res["sync_costs"] = sync
     print(json.dumps(res), flush=True)
 
 

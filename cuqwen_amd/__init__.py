@@ -144,6 +144,7 @@ def _load():
         "cq_time_gemv": (I32, [I32, I32, I32, ctypes.POINTER(P), ctypes.POINTER(P), P, P, I32, I32, I32,
                                ctypes.POINTER(ctypes.c_double)]),
         "cq_time_stream": (I32, [SZ, I32, ctypes.POINTER(P), I32, ctypes.POINTER(ctypes.c_double)]),
+        "cq_time_grid_barrier": (I32, [I32, I32, I32, ctypes.POINTER(ctypes.c_double), IP]),
         "cq_state_profile": (I32, [P, I32, I32, I32, ctypes.c_char_p, ctypes.POINTER(ctypes.c_double),
                                    ctypes.POINTER(ctypes.c_double), IP]),
         "cq_tokenizer_load": (I32, [ctypes.c_char_p, ctypes.POINTER(P)]),
@@ -178,7 +179,7 @@ EXPORTED = [
     "cq_kv_cache_store", "cq_rope", "cq_gqa_attention_decode", "cq_attention_workspace_bytes", "cq_dequantize",
     "cq_kv_cache_store_hm", "cq_gqa_attention_decode_hm", "cq_gqa_attention_decode_noalloc",
     "cq_noalloc_scratch_bytes",
-    "cq_time_gemv", "cq_time_stream", "cq_state_profile", "cq_tokenizer_load", "cq_tokenizer_free", "cq_tokenizer_encode",
+    "cq_time_gemv", "cq_time_stream", "cq_time_grid_barrier", "cq_state_profile", "cq_tokenizer_load", "cq_tokenizer_free", "cq_tokenizer_encode",
     "cq_tokenizer_decode", "cq_tokenizer_token_id", "cq_tokenizer_vocab_size", "cq_chat_template",
 ]
 

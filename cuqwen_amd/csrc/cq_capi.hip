@@ -295,6 +295,119 @@ __global__ __launch_bounds__(256) void stream_read_kernel(const u4_t* p, size_t 
 }
 }  // namespace
 
+// Grid-wide barriers inside one kernel, the alternative to a graph-node
+// boundary between dependent stages.  Block b arrives at barrier r by
+// publishing r (kind 0: its own flag, one 128-byte line per block, which
+// every block then polls, one flag per thread; kind 1: one device-scope
+// atomic add to a shared counter, which every block polls until it reaches
+// r * blocks; kind 2: its own flag, which only block 0 polls before it
+// publishes r in one word that every other block polls; kind 3: kind 2
+// with relaxed stores and no acquire fence, i.e. the signalling alone --
+// a barrier that orders no other memory, the lower bound).  Every poll loop is bounded: past kBarrierSpins polls the
+// block records a time-out and all blocks leave, so the kernel always ends.
+namespace {
+constexpr int kBarrierSpins = 1 << 22;
+constexpr int kFlagStride = 32;   // uint32 per 128-byte line
+
+// polls are relaxed device-scope loads; one acquire fence follows the wait
+__device__ __forceinline__ uint32_t ld_poll(const uint32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__global__ __launch_bounds__(256) void grid_barrier_kernel(uint32_t* flags, uint32_t* counter, uint32_t* timed_out,
+                                                           int kind, int rounds) {
+  __shared__ int stop;
+  const uint32_t nb = gridDim.x;
+  for (int r = 1; r <= rounds; ++r) {
+    if (threadIdx.x == 0) {
+      if (kind == 3) __hip_atomic_store(flags + blockIdx.x * kFlagStride, (uint32_t)r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      else if (kind != 1) __hip_atomic_store(flags + blockIdx.x * kFlagStride, (uint32_t)r, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+      else __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+      stop = 0;
+    }
+    __syncthreads();
+    int spins = 0;
+    if (kind == 0) {
+      if (threadIdx.x < nb)
+        while (ld_poll(flags + threadIdx.x * kFlagStride) < (uint32_t)r && ++spins < kBarrierSpins) {}
+    } else if (kind == 1) {
+      if (threadIdx.x == 0)
+        while (ld_poll(counter) < (uint32_t)r * nb && ++spins < kBarrierSpins) {}
+    } else {
+      // block 0 gathers the flags and publishes round r in one word the others poll
+      if (blockIdx.x == 0) {
+        if (threadIdx.x < nb)
+          while (ld_poll(flags + threadIdx.x * kFlagStride) < (uint32_t)r && ++spins < kBarrierSpins) {}
+        __syncthreads();
+        if (threadIdx.x == 0) {
+          if (kind == 3) __hip_atomic_store(counter, (uint32_t)r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          else __hip_atomic_store(counter, (uint32_t)r, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      } else if (threadIdx.x == 0) {
+        while (ld_poll(counter) < (uint32_t)r && ++spins < kBarrierSpins) {}
+      }
+    }
+    if (kind != 3) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    if (spins >= kBarrierSpins) {
+      stop = 1;
+      __hip_atomic_store(timed_out, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (stop || __hip_atomic_load(timed_out, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return;
+  }
+}
+}  // namespace
+
+extern "C" int cq_time_grid_barrier(int32_t kind, int32_t blocks, int32_t rounds, double* us_per_barrier,
+                                    int32_t* timed_out) {
+  if (kind < 0 || kind > 3 || rounds <= 0 || !us_per_barrier || !timed_out)
+    return fail(CQ_EINVAL, "time_grid_barrier: bad arguments");
+  int dev = 0, cus = 0;
+  CQ_HIP(hipGetDevice(&dev));
+  CQ_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  // one block per CU at most: all blocks resident at once (every block waits for every other)
+  if (blocks <= 0 || blocks > cus || blocks > 256) return fail(CQ_EINVAL, "time_grid_barrier: blocks outside [1, CUs]");
+  hipStream_t st;
+  CQ_HIP(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
+  uint32_t* mem = nullptr;
+  hipEvent_t e[4] = {nullptr, nullptr, nullptr, nullptr};
+  float ms_full = 0.f, ms_empty = 0.f;
+  uint32_t to = 0;
+  const size_t flag_words = (size_t)blocks * kFlagStride;
+  auto body = [&]() -> int {
+    CQ_HIP(hipMalloc(&mem, (flag_words + 64) * sizeof(uint32_t)));
+    uint32_t* counter = mem + flag_words;
+    uint32_t* tflag = counter + 32;
+    for (auto& ev : e) CQ_HIP(hipEventCreate(&ev));
+    for (int rep = 0; rep < 2; ++rep) {   // the first pass warms up
+      CQ_HIP(hipMemsetAsync(mem, 0, (flag_words + 64) * sizeof(uint32_t), st));
+      CQ_HIP(hipEventRecord(e[0], st));
+      hipLaunchKernelGGL(grid_barrier_kernel, dim3(blocks), dim3(256), 0, st, mem, counter, tflag, (int)kind, 0);
+      CQ_HIP(hipEventRecord(e[1], st));
+      CQ_HIP(hipEventRecord(e[2], st));
+      hipLaunchKernelGGL(grid_barrier_kernel, dim3(blocks), dim3(256), 0, st, mem, counter, tflag, (int)kind, (int)rounds);
+      CQ_HIP(hipEventRecord(e[3], st));
+      CQ_HIP(hipGetLastError());
+      CQ_HIP(hipEventSynchronize(e[3]));
+    }
+    CQ_HIP(hipEventElapsedTime(&ms_empty, e[0], e[1]));
+    CQ_HIP(hipEventElapsedTime(&ms_full, e[2], e[3]));
+    CQ_HIP(hipMemcpy(&to, tflag, sizeof to, hipMemcpyDeviceToHost));
+    return CQ_OK;
+  };
+  const int rc = body();
+  for (auto& ev : e)
+    if (ev) hipEventDestroy(ev);
+  hipStreamSynchronize(st);
+  if (mem) hipFree(mem);
+  hipStreamDestroy(st);
+  if (rc == CQ_OK) {
+    *us_per_barrier = (double)(ms_full - ms_empty) * 1000.0 / rounds;
+    *timed_out = to ? 1 : 0;
+  }
+  return rc;
+}
+
 extern "C" int cq_time_stream(size_t n_bytes, int32_t n_bufs, void* const* bufs, int32_t iters, double* us_per_launch) {
   if (n_bufs <= 0 || (!bufs && n_bytes) || iters <= 0 || !us_per_launch || n_bytes % 16)
     return fail(CQ_EINVAL, "time_stream: bad arguments");

@@ -436,13 +436,26 @@ int cq_time_gemv(int32_t quant_type, int32_t group_size, int32_t n_bufs, void* c
                  void* const* S_list, const void* x, void* y, int32_t rows, int32_t cols,
                  int32_t iters, double* us_per_launch);
 
-/* Streaming floor: a plain read of n_bytes (16-byte loads, one block per
- * CU) recorded `iters` times into one HIP graph rotating over the n_bufs
- * buffers, replayed between HIP events; *us_per_launch = elapsed / iters.
- * The time any kernel that reads n_bytes meets in the decode step's graph
- * chain.  n_bytes 0 times the empty launch (per-node cost).  Measurement
- * hook; no counterpart in the reference. */
+/* Streaming floor: a plain read of n_bytes (16-byte non-temporal loads,
+ * four 256-thread blocks per CU striding over the buffer) recorded `iters`
+ * times into one HIP graph rotating over the n_bufs buffers, replayed
+ * between HIP events; *us_per_launch = elapsed / iters.  The time any
+ * kernel that reads n_bytes meets in the decode step's graph chain.
+ * n_bytes 0 times the empty launch (per-node cost).  Measurement hook; no
+ * counterpart in the reference. */
 int cq_time_stream(size_t n_bytes, int32_t n_bufs, void* const* bufs, int32_t iters, double* us_per_launch);
+
+/* Cost of a grid-wide barrier inside one kernel, the alternative to a graph
+ * node boundary between dependent stages: `blocks` 256-thread blocks (at
+ * most one per CU) pass `rounds` barriers; kind 0: each block publishes its
+ * own flag (one 128-byte line per block) and polls all of them, kind 1:
+ * one device-scope atomic counter, kind 2: the flags gathered by block 0,
+ * which then releases the others through one word, kind 3: kind 2 without
+ * release / acquire ordering (the signalling alone, a lower bound).  *us_per_barrier = (time with `rounds`
+ * barriers - time with none) / rounds, HIP events.  Every poll is bounded:
+ * *timed_out = 1 if some block gave up waiting (the figure is then not
+ * valid).  Measurement hook; no counterpart in the reference. */
+int cq_time_grid_barrier(int32_t kind, int32_t blocks, int32_t rounds, double* us_per_barrier, int32_t* timed_out);
 
 /* Per-kernel profile of the decode step at position `pos` (the reference's
  * benchmark/kernel_profile.cu): each kernel of the step is launched for every
