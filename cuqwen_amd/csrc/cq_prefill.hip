@@ -241,7 +241,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
   constexpr int NMAT = SH::NMAT, RT = SH::RT, WROWS = SH::WROWS, BN = SH::BN, TT = kPfTT;
   constexpr int L = PfW<Q>::LOADS;
   constexpr int XS = kPfTok * kPfK;                         // halves of one activation stage
-  constexpr int OT = MODE == GM_QKV ? BN * kPfTok : 0;      // QKV epilogue tile (rows x tokens)
+  constexpr int OT = MODE == GM_QKV ? kPfTok / 2 * (BN + 2) : 0;   // QKV epilogue tile (half the tokens x rows)
   constexpr int NS = 2;                                     // LDS stages
   // the epilogues reuse the stages: QKV tile, residual fp32 half tile
   constexpr int SM = std::max({NS * XS, OT, kPfTok / 2 * (BN + 4) * 2});
@@ -531,57 +531,65 @@ __global__ __launch_bounds__(kPfThreads, 2) void pf_gemm_kernel(const PfGemmArgs
     }
   } else {
     // QKV: norm scale, bias, fp16 into LDS (over the activation buffers, all
-    // reads of which finished at the loop's last barrier); then pairs
-    // (i, i + hd/2) of each head rotate (q, k) and go to Q or the KV cache
+    // reads of which finished at the loop's last barrier), 64 tokens per
+    // pass, token-major rows; then pairs (i, i + hd/2) of each head rotate
+    // (q, k) and go to Q or the KV cache, consecutive threads taking
+    // consecutive pairs of one token (so Q's stores are contiguous)
+    constexpr int HT = kPfTok / 2;
+    constexpr int LDQ = BN + 2;   // odd dword stride: the token-per-lane reads below are conflict-free
+    static_assert(HT * LDQ <= SM, "QKV staging fits");
     _Float16* ot = smem;
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-      for (int tt = 0; tt < TT; ++tt)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int nl = wave * WROWS + rt * 16 + 4 * j + v, ml = tt * 16 + r;
-          const int n = nb0 + nl, m = min(m0 + ml, a.M - 1);
-          int local;
-          const int mat = pf_mat(a, min(n, a.N - 1), &local);
-          const _Float16* b = a.bias[mat];
-          const float y = acc[0][rt][tt][v] * a.inv[m] + (b ? (float)b[local] : 0.f);
-          ot[nl * kPfTok + ml] = (_Float16)y;   // q/k/v are fp16 before RoPE (kernels.cu:470)
-        }
-    __syncthreads();
     const int hd = a.head_dim, half = hd / 2;
-    for (int idx = threadIdx.x; idx < (BN / 2) * kPfTok; idx += kPfThreads) {
-      const int ml = idx % kPfTok, pi = idx / kPfTok;   // pair pi of the block's BN/2 pairs
-      const int nl0 = (pi / half) * hd + pi % half, nl1 = nl0 + half;
-      const int n0 = nb0 + nl0, m = m0 + ml;
-      if (n0 >= a.N || m >= a.M) continue;
-      int local;
-      const int mat = pf_mat(a, n0, &local);
-      float y0 = (float)ot[nl0 * kPfTok + ml], y1 = (float)ot[nl1 * kPfTok + ml];
-      const int pos = a.pos0 + m, i = local % hd;
-      if (mat < 2) rope_rotate(y0, y1, pos, a.inv_freq[i]);
-      if (a.kcache8 && mat > 0) {
-        // quantized cache: rotated values back into the tile, quantized per head below
-        ot[nl0 * kPfTok + ml] = (_Float16)y0;
-        ot[nl1 * kPfTok + ml] = (_Float16)y1;
-      } else {
-        pf_qkv_store(a, mat, local, m, (_Float16)y0, (_Float16)y1);
-      }
-    }
-    if (a.kcache8) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      if (h) __syncthreads();
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int tt = h * TT / 2; tt < (h + 1) * TT / 2; ++tt)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int nl = wave * WROWS + rt * 16 + 4 * j + v, ml = tt * 16 + r;
+            const int n = nb0 + nl, m = min(m0 + ml, a.M - 1);
+            int local;
+            const int mat = pf_mat(a, min(n, a.N - 1), &local);
+            const _Float16* b = a.bias[mat];
+            const float y = acc[0][rt][tt][v] * a.inv[m] + (b ? (float)b[local] : 0.f);
+            ot[(ml - h * HT) * LDQ + nl] = (_Float16)y;   // q/k/v are fp16 before RoPE (kernels.cu:470)
+          }
       __syncthreads();
-      const int heads = BN / hd;
-      for (int idx = threadIdx.x; idx < heads * kPfTok; idx += kPfThreads) {
-        const int hb = idx / kPfTok, ml = idx % kPfTok;
-        const int n0 = nb0 + hb * hd, m = m0 + ml;
+      for (int idx = threadIdx.x; idx < (BN / 2) * HT; idx += kPfThreads) {
+        const int pi = idx % (BN / 2), ml = idx / (BN / 2);   // pair pi of the block's BN/2 pairs
+        const int nl0 = (pi / half) * hd + pi % half, nl1 = nl0 + half;
+        const int n0 = nb0 + nl0, m = m0 + h * HT + ml;
         if (n0 >= a.N || m >= a.M) continue;
         int local;
         const int mat = pf_mat(a, n0, &local);
-        if (mat == 0) continue;
-        float amax = 0.f;
-        for (int d = 0; d < hd; ++d) amax = fmaxf(amax, fabsf((float)ot[(hb * hd + d) * kPfTok + ml]));
-        pf_kv8_store(a, mat, local / hd, a.pos0 + m, amax,
-                     [&](int d) { return (float)ot[(hb * hd + d) * kPfTok + ml]; });
+        float y0 = (float)ot[ml * LDQ + nl0], y1 = (float)ot[ml * LDQ + nl1];
+        const int pos = a.pos0 + m, i = local % hd;
+        if (mat < 2) rope_rotate(y0, y1, pos, a.inv_freq[i]);
+        if (a.kcache8 && mat > 0) {
+          // quantized cache: rotated values back into the tile, quantized per head below
+          ot[ml * LDQ + nl0] = (_Float16)y0;
+          ot[ml * LDQ + nl1] = (_Float16)y1;
+        } else {
+          pf_qkv_store(a, mat, local, m, (_Float16)y0, (_Float16)y1);
+        }
+      }
+      if (a.kcache8) {
+        __syncthreads();
+        const int heads = BN / hd;
+        for (int idx = threadIdx.x; idx < heads * HT; idx += kPfThreads) {
+          const int hb = idx / HT, ml = idx % HT;
+          const int n0 = nb0 + hb * hd, m = m0 + h * HT + ml;
+          if (n0 >= a.N || m >= a.M) continue;
+          int local;
+          const int mat = pf_mat(a, n0, &local);
+          if (mat == 0) continue;
+          float amax = 0.f;
+          for (int d = 0; d < hd; ++d) amax = fmaxf(amax, fabsf((float)ot[ml * LDQ + hb * hd + d]));
+          pf_kv8_store(a, mat, local / hd, a.pos0 + m, amax, [&](int d) { return (float)ot[ml * LDQ + hb * hd + d]; });
+        }
       }
     }
   }
